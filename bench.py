@@ -1,0 +1,312 @@
+#!/usr/bin/env python3
+"""Benchmark of the block-scaled FP8 linear path on one MI355X.
+
+Headline (the JSON ``value``): BASELINE config 2, the fused SiLU*Mul + 1x128
+FP8 quant over bf16 [8192, 36864] -> fp8 [8192, 18432] + fp32 scales
+[8192, 144], in GB/s of algorithmic traffic (inputs resident in HBM).  One
+"step" is one launch over the whole tensor.
+
+The same JSON line carries the other BASELINE configs under ``extra``:
+per-token-group quant, the DeepSeek-V3 dense GEMMs at M in {128, 4096}, the
+MoE grouped GEMMs (config 4) and the Llama-3.1-70B decode GEMMs (config 5),
+each with TFLOP/s or GB/s and its roofline fraction.  HBM-bound cases rotate
+through enough buffer copies to exceed the 256 MB Infinity Cache.
+
+All inputs are synthetic (seeded torch generators), weights random-init.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+FP8_PEAK_TFLOPS = 5000.0     # MI355X dense fp8 MFMA, TFLOP/s
+MALL_BYTES = 256 * 2 ** 20
+METRIC = "FP8 block-scaled GEMM TFLOPS (% fp8 MFMA peak); quant kernels GB/s (% HBM)"
+
+
+def _events_time_ms(fn, steps: int, warmup: int) -> float:
+    """Average ms per call of fn() on the current stream, by HIP events."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def _copies_for(bytes_per_set: int, minimum: int = 1) -> int:
+    return max(minimum, math.ceil(2 * MALL_BYTES / max(bytes_per_set, 1)))
+
+
+# ----------------------------------------------------------------- inputs
+
+def _quant_weight(w, torch):
+    from kb_nano_amd.fp8_linear import _block_requant
+    return _block_requant(w, use_ue8m0=True, eps=1e-10)
+
+
+def _rand_weight(N, K, gen, dev, torch):
+    w = torch.randn(N, K, generator=gen, device=dev) * 0.02
+    q, s = _quant_weight(w, torch)
+    del w
+    return q, s
+
+
+def _quant_act(a, torch):
+    from kb_nano_amd import _ops
+    from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
+    M, K = a.shape
+    q = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=a.device)
+    s = _alloc_colmajor_scale(M, K // 128, a.device)
+    _ops.per_token_group_quant_fp8(a, q, s)
+    return q, s
+
+
+# --------------------------------------------------------------- sections
+
+def bench_silu(steps, warmup, dev):
+    import torch
+    from kb_nano_amd import _ops
+    M, Nh = 8192, 18432
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(M, 2 * Nh, generator=g)
+    x = torch.where(torch.rand(M, 2 * Nh, generator=g) < 1e-3, x * 50, x).bfloat16().to(dev)
+    q = torch.empty(M, Nh, dtype=torch.float8_e4m3fn, device=dev)
+    s = torch.empty(Nh // 128, M, dtype=torch.float32, device=dev).t()
+    nbytes = M * 2 * Nh * 2 + M * Nh + 4 * M * (Nh // 128)
+    ms = _events_time_ms(lambda i: _ops.silu_mul_quant_fp8(x, q, s), steps, warmup)
+    return {"ms": ms, "bytes": nbytes, "gbs": nbytes / (ms * 1e-3) / 1e9}
+
+
+def bench_quant(steps, warmup, dev, M=4096, K=18432):
+    import torch
+    from kb_nano_amd import _ops
+    nbytes = M * K * 2 + M * K + 4 * M * (K // 128)
+    n = _copies_for(nbytes, 2)
+    gen = torch.Generator(device=dev).manual_seed(3)
+    xs = [torch.randn(M, K, generator=gen, device=dev).bfloat16() for _ in range(n)]
+    qs = [torch.empty(M, K, dtype=torch.float8_e4m3fn, device=dev) for _ in range(n)]
+    ss = [torch.empty(K // 128, M, device=dev).t() for _ in range(n)]
+    ms = _events_time_ms(lambda i: _ops.per_token_group_quant_fp8(xs[i % n], qs[i % n], ss[i % n]), steps, warmup)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"M": M, "K": K, "us": ms * 1e3, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS, "rotated_copies": n}
+
+
+def _gemm_case(name, M, N, K, steps, warmup, dev, seed):
+    import torch
+    from kb_nano_amd import _ops
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    w_bytes = N * K + 4 * (-(-N // 128)) * (K // 128)
+    a_bytes = M * K + 4 * M * (K // 128)
+    nbytes = w_bytes + a_bytes + 2 * M * N
+    n = _copies_for(nbytes) if M <= 256 else 1
+    Ws = [_rand_weight(N, K, gen, dev, torch) for _ in range(n)]
+    A, sA = _quant_act(torch.randn(M, K, generator=gen, device=dev).bfloat16(), torch)
+    D = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    ms = _events_time_ms(lambda i: _ops.fp8_gemm_nt(A, sA, Ws[i % n][0], Ws[i % n][1], D, use_ue8m0=True),
+                         steps, warmup)
+    flop = 2.0 * M * N * K
+    t = ms * 1e-3
+    tflops = flop / t / 1e12
+    gbs = nbytes / t / 1e9
+    roof = max(flop / (FP8_PEAK_TFLOPS * 1e12), nbytes / (HBM_PEAK_GBS * 1e9))
+    del Ws, A, sA, D
+    torch.cuda.empty_cache()
+    return {"name": name, "M": M, "N": N, "K": K, "us": ms * 1e3, "TFLOPS": tflops,
+            "frac_mfma": tflops / FP8_PEAK_TFLOPS, "GB/s": gbs, "frac_roof": roof / t,
+            "bound": "mfma" if flop / (FP8_PEAK_TFLOPS * 1e12) > nbytes / (HBM_PEAK_GBS * 1e9) else "hbm",
+            "rotated_copies": n}
+
+
+DSV3 = [("q_b_proj", 24576, 1536), ("gate_up", 36864, 7168), ("down_proj", 7168, 18432), ("o_proj", 7168, 16384)]
+LLAMA70B = [("qkv", 10240, 8192), ("o", 8192, 8192), ("gate_up", 57344, 8192), ("down", 8192, 28672)]
+
+
+def bench_dsv3(steps, warmup, dev):
+    out = []
+    for M in (4096, 128):
+        for name, N, K in DSV3:
+            out.append(_gemm_case(name, M, N, K, steps, warmup, dev, seed=2))
+    return out
+
+
+def bench_decode(steps, warmup, dev):
+    out = []
+    for name, N, K in LLAMA70B:
+        for M in (1, 8, 32, 64):
+            out.append(_gemm_case(name, M, N, K, steps, warmup, dev, seed=4))
+    return out
+
+
+def bench_moe(steps, warmup, dev):
+    """Config 4: 4096 tokens, hidden 7168, 256 experts, top-8 from seeded
+    softmax logits, per-expert rows padded to 128; gate_up (N=4096, K=7168)
+    then down (N=7168, K=2048)."""
+    import torch
+    from kb_nano_amd import _ops
+    from kb_nano_amd.moe_layout import _deepgemm_permute
+    T, H, E, topk, I2, I = 4096, 7168, 256, 8, 4096, 2048
+    g = torch.Generator().manual_seed(0)
+    logits = torch.randn(T, E, generator=g)
+    topk_ids = torch.topk(torch.softmax(logits, -1), topk, dim=-1).indices.to(dev)
+    gen = torch.Generator(device=dev).manual_seed(5)
+    hidden = torch.randn(T, H, generator=gen, device=dev).bfloat16()
+    a_tok, s_tok = _quant_act(hidden, torch)
+    a_perm, s_perm, expert_ids, _ = _deepgemm_permute(a_tok.view(torch.uint8), s_tok.contiguous(), topk_ids, E, 128)
+    a_perm = a_perm.view(torch.float8_e4m3fn)
+    M_sum = a_perm.shape[0]
+    ids = expert_ids.cpu()
+    rows_in_segments = int(sum(1 for r in range(0, M_sum, 128) if ids[r] >= 0)) * 128
+    valid_rows = int((ids >= 0).sum())
+
+    def experts(N, K):
+        w = torch.empty(E, N, K, dtype=torch.float8_e4m3fn, device=dev)
+        s = torch.empty(E, -(-N // 128), K // 128, device=dev)
+        for e in range(E):
+            w[e], s[e] = _rand_weight(N, K, gen, dev, torch)
+        return w, s
+
+    res = {"M_sum": M_sum, "rows_in_segments": rows_in_segments, "valid_rows": valid_rows}
+    w13, s13 = experts(I2, H)
+    c1 = torch.empty(M_sum, I2, dtype=torch.bfloat16, device=dev)
+    ms1 = _events_time_ms(lambda i: _ops.m_grouped_gemm_nt_contiguous(a_perm, s_perm, w13, s13, c1, expert_ids, False),
+                          steps, warmup)
+    del w13, s13
+    a2 = torch.randn(M_sum, I, generator=gen, device=dev).bfloat16()
+    a2q, a2s = _quant_act(a2, torch)
+    del a2
+    w2, s2 = experts(H, I)
+    c2 = torch.empty(M_sum, H, dtype=torch.bfloat16, device=dev)
+    ms2 = _events_time_ms(lambda i: _ops.m_grouped_gemm_nt_contiguous(a2q, a2s, w2, s2, c2, expert_ids, False),
+                          steps, warmup)
+    for tag, ms, N, K in (("gate_up", ms1, I2, H), ("down", ms2, H, I)):
+        t = ms * 1e-3
+        flop = 2.0 * valid_rows * N * K
+        nbytes = E * (N * K + 4 * (N // 128) * (K // 128)) + rows_in_segments * (K + 4 * K // 128 + 2 * N)
+        res[tag] = {"N": N, "K": K, "us": ms * 1e3, "TFLOPS": flop / t / 1e12, "GB/s": nbytes / t / 1e9,
+                    "frac_hbm": nbytes / t / 1e9 / HBM_PEAK_GBS,
+                    "frac_roof": max(flop / (FP8_PEAK_TFLOPS * 1e12), nbytes / (HBM_PEAK_GBS * 1e9)) / t}
+    del w2, s2
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline_silu():
+    """The C oracle (a port of the reference algorithm) on the host cores,
+    over the full config-2 workload; median of 3 runs."""
+    import numpy as np
+    import torch
+
+    import oracle
+    M, Nh = 8192, 18432
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(M, 2 * Nh, generator=g)
+    x = torch.where(torch.rand(M, 2 * Nh, generator=g) < 1e-3, x * 50, x).bfloat16()
+    bits = x.view(torch.int16).numpy().view(np.uint16)
+    oracle.silu_mul_quant(bits[:8])  # load + warm
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oracle.silu_mul_quant(bits)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    nbytes = M * 2 * Nh * 2 + M * Nh + 4 * M * (Nh // 128)
+    cores = int(os.environ.get("OMP_NUM_THREADS", 0)) or len(os.sched_getaffinity(0))
+    return {"value": nbytes / t / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"full config-2 workload (8192 x 36864 bf16) through oracle/kbn_oracle.c "
+                      f"(OpenMP, {cores} threads), median of 3 runs = {t:.3f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", default="all",
+                    help="comma list of extra sections: quant,dsv3,moe,decode (default all; 'none' = headline only)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): this build covers the "
+              "single-GPU hot path; see DESIGN.md for how it would shard.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    from kb_nano_amd._lib import require_gfx950
+    require_gfx950(0)
+
+    sections = {"quant", "dsv3", "moe", "decode"} if args.only == "all" else \
+        set() if args.only == "none" else set(args.only.split(","))
+
+    torch.cuda.synchronize()
+    head = bench_silu(args.steps, args.warmup, dev)
+    print(f"[bench] silu_mul_quant cfg2: {head['ms'] * 1e3:.1f} us/launch, {head['gbs']:.0f} GB/s", file=sys.stderr,
+          flush=True)
+    extra = {}
+    small = dict(steps=max(5, args.steps // 2), warmup=max(2, args.warmup // 2), dev=dev)
+    if "quant" in sections:
+        extra["quant_cfg_4096x18432"] = bench_quant(**small)
+        print(f"[bench] quant: {extra['quant_cfg_4096x18432']}", file=sys.stderr, flush=True)
+    if "dsv3" in sections:
+        extra["gemm_dsv3_cfg3"] = bench_dsv3(**small)
+        for r in extra["gemm_dsv3_cfg3"]:
+            print(f"[bench] dsv3 {r['name']} M={r['M']}: {r['us']:.1f} us {r['TFLOPS']:.0f} TFLOPS "
+                  f"{r['frac_roof'] * 100:.1f}% roof", file=sys.stderr, flush=True)
+    if "moe" in sections:
+        extra["moe_grouped_cfg4"] = bench_moe(**small)
+        print(f"[bench] moe: {extra['moe_grouped_cfg4']}", file=sys.stderr, flush=True)
+    if "decode" in sections:
+        extra["decode_llama70b_cfg5"] = bench_decode(**small)
+        for r in extra["decode_llama70b_cfg5"]:
+            print(f"[bench] decode {r['name']} M={r['M']}: {r['us']:.1f} us {r['GB/s']:.0f} GB/s "
+                  f"{r['frac_roof'] * 100:.1f}% roof", file=sys.stderr, flush=True)
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline_silu()
+    value = head["gbs"]
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16->fp8_e4m3 (f32 math)",
+        "data": "synthetic (seeded torch RNG; cfg2: N(0,1) gate/up with 0.1% x50 outliers)",
+        "config": {"workload": "cfg2 fused SiLU*Mul + 1x128 FP8 quant: bf16 [8192, 36864] -> "
+                               "fp8 [8192, 18432] + fp32 column-major scales [8192, 144]",
+                   "M": 8192, "N_half": 18432, "algorithmic_bytes": head["bytes"]},
+        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

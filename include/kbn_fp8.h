@@ -1,0 +1,116 @@
+/*
+ * kbn_fp8.h -- C-ABI of libkbn_fp8.so, the MI355X (gfx950) implementation of
+ * kb_nano's block-scaled FP8 linear path.
+ *
+ * Conventions for every entry point:
+ *   - Plain device pointers and sizes; bf16 and fp8 buffers are passed as
+ *     void* (bf16 = 16-bit bfloat16 bit patterns, fp8 = OCP float8_e4m3fn).
+ *   - `stream` is a hipStream_t (NULL = the default stream).  Calls are
+ *     asynchronous on that stream; they never allocate, free or synchronise,
+ *     so they may be captured into HIP graphs and may run concurrently on
+ *     different streams.  The caller owns every buffer.
+ *   - Return 0 on success.  A non-zero code means the arguments were
+ *     rejected (1) or the launch failed (2); kbn_last_error() then holds a
+ *     message (thread-local).  Nothing is launched when arguments are rejected.
+ *   - Strides are in elements of the buffer's type.
+ *
+ * Paths cited below are relative to the kb_nano tree.
+ */
+#ifndef KBN_FP8_H
+#define KBN_FP8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* kbn_last_error(void);
+
+/* ABI revision of this header (1). */
+int kbn_abi_version(void);
+
+/* gcnArchName of a HIP device into buf (e.g. "gfx950:sramecc+:xnack-"). */
+int kbn_device_arch(int device, char* buf, int len);
+
+/*
+ * Per-token-group (1x128) FP8 quantization.
+ * Replaces _per_token_group_quant_fp8 / op kb_nano_fp8::per_token_group_quant_fp8
+ * (tasks/baseline/L1/fp8_linear.py:157-178, :234-279; kernel :181-215).
+ *   x       bf16 [M, K], row stride ld_x (multiple of 8, 16-byte aligned), K % 128 == 0
+ *   q       fp8  [M, K], row stride ld_q (multiple of 8)
+ *   scale   fp32 [M, K/128]; element (m, g) at scale[m*s_stride_m + g*s_stride_g]
+ *           (row-major: (K/128, 1); column-major: (1, M))
+ *   For each group: amax = max(max|x|, eps); s = amax/448, rounded up to a
+ *   power of two when use_ue8m0; q = e4m3_rne(clamp(x/s, -448, 448)).
+ */
+int kbn_per_token_group_quant_fp8(const void* x_bf16, int64_t M, int64_t K, int64_t ld_x,
+                                  void* q_fp8, int64_t ld_q, float* scale,
+                                  int64_t s_stride_m, int64_t s_stride_g,
+                                  float eps, int use_ue8m0, void* stream);
+
+/*
+ * Fused SiLU*Mul + per-token-group FP8 quantization.
+ * Replaces the Triton kernel _silu_mul_per_token_group_quant_fp8_colmajor and
+ * SiluMulQuantFp8.forward (tasks/baseline/L1/silu_mul_quant_fp8.py:23-76, :87-143).
+ *   in      bf16 [M, 2*N_half] = [gate | up], row stride ld_in (multiple of 8)
+ *   q       fp8  [M, N_half], row stride ld_q;  N_half % 128 == 0
+ *   scale   fp32 [M, N_half/128] at scale[m*s_stride_m + g*s_stride_g]
+ *   y = bf16(bf16(silu(gate)) * up) with silu correctly rounded to bf16,
+ *   then quantized per 1x128 group as above.
+ */
+int kbn_silu_mul_quant_fp8(const void* in_bf16, int64_t M, int64_t N_half, int64_t ld_in,
+                           void* q_fp8, int64_t ld_q, float* scale,
+                           int64_t s_stride_m, int64_t s_stride_g,
+                           float eps, int use_ue8m0, void* stream);
+
+/*
+ * Block-scaled FP8 GEMM, "NT" (both operands K-contiguous).
+ * Replaces op kb_nano_fp8::fp8_gemm_nt -> deep_gemm.fp8_gemm_nt
+ * (tasks/baseline/L1/fp8_linear.py:89-118).
+ *   A    fp8 [M, K] row stride lda;  sA fp32 [M, K/128] at sA[m*sA_stride_m + kb*sA_stride_k]
+ *   W    fp8 [N, K] row stride ldw;  sW fp32 [ceil(N/128), K/128] row stride sW_ld
+ *   D    bf16 [M, N] row stride ldd (written)
+ *   D[m,n] = bf16_rne( sum_kb sA[m,kb] * sW[n/128,kb] * sum_{k in kb} A[m,k] * W[n,k] ), fp32 accumulate.
+ *   scale_ue8m0 != 0: every scale is first rounded up to a power of two (the
+ *   UE8M0 contract, DeepGEMM's disable_ue8m0_cast=False); 0: scales used as given.
+ *   K % 128 == 0; A/W rows 16-byte aligned (lda, ldw multiples of 16).
+ */
+int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m, int64_t sA_stride_k,
+                    const void* W, int64_t ldw, const float* sW, int64_t sW_ld,
+                    void* D_bf16, int64_t ldd, int64_t M, int64_t N, int64_t K,
+                    int scale_ue8m0, void* stream);
+
+/*
+ * Contiguous-layout grouped FP8 GEMM (MoE experts).
+ * Replaces op kb_nano_fp8_moe::m_grouped_gemm_nt_contiguous ->
+ * deep_gemm.m_grouped_fp8_gemm_nt_contiguous
+ * (tasks/baseline/L1/fp8_grouped_gemm_contiguous.py:100-133; free function
+ * tasks/baseline/L1/moe_grouped_gemm.py:71-83).
+ *   A   fp8 [M_sum, K] row stride lda; sA fp32 [M_sum, K/128] (strides as above)
+ *   B   fp8 [E, N, K] contiguous;      sB fp32 [E, ceil(N/128), K/128] contiguous
+ *   C   bf16 [M_sum, N] row stride ldc; expert_ids int32 [M_sum]
+ *   Rows are taken in 128-row blocks (M_sum % 128 == 0).  A block whose first
+ *   row has id e in [0, E) computes C[r] = A[r] x B[e]^T (block-scaled as in
+ *   kbn_fp8_gemm_nt) for its rows with id e; rows with any other id (-1 =
+ *   padding) and blocks whose first id is outside [0, E) are not written.
+ *   scale_ue8m0 = !disable_ue8m0_cast.
+ */
+int kbn_fp8_grouped_gemm_nt_contiguous(const void* A, int64_t lda, const float* sA,
+                                       int64_t sA_stride_m, int64_t sA_stride_k,
+                                       const void* B, const float* sB, void* C_bf16, int64_t ldc,
+                                       const int32_t* expert_ids, int64_t M_sum, int64_t N, int64_t K,
+                                       int64_t E, int scale_ue8m0, void* stream);
+
+/*
+ * Test hook (no counterpart in the reference): the kernels' bf16 SiLU
+ * applied elementwise to n bf16 bit patterns, for exhaustive checking.
+ */
+int kbn_debug_silu_bf16(const uint16_t* g_bf16, uint16_t* out_bf16, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KBN_FP8_H */

@@ -1,0 +1,237 @@
+"""Tensor-level wrappers over the C-ABI and the opaque ``torch.library`` ops.
+
+Every wrapper validates dtype, device, shape and strides on the host, then
+launches on the caller's current HIP stream; nothing here allocates device
+memory, synchronises, or computes on the CPU, so the ops are safe inside
+HIP-graph capture and stay opaque to ``torch.compile``.
+
+Op schemas follow the reference (tasks/baseline/L1/fp8_linear.py:89-178 and
+tasks/baseline/L1/fp8_grouped_gemm_contiguous.py:100-133).  The reference
+creates its namespaces with ``Library(..., "DEF")``; this package owns the
+same names on ROCm (the reference module cannot import there: it needs
+``deep_gemm``), and uses ``FRAGMENT`` so a second registration in one
+process is a no-op rather than an error.
+"""
+from __future__ import annotations
+
+import functools
+import os
+
+import torch
+
+from ._lib import check, lib, require_gfx950
+
+FP8 = torch.float8_e4m3fn
+GROUP = 128
+QUANT_EPS = 1e-10  # tasks/baseline/L1/fp8_linear.py:44
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _dev_check(what: str, *tensors: torch.Tensor) -> int:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(f"{what}: tensors must be on a ROCm GPU, got {dev} (no CPU path)")
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise RuntimeError(f"{what}: all tensors must be on {dev}, got {t.device}")
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    require_gfx950(idx)
+    if idx != torch.cuda.current_device():
+        raise RuntimeError(f"{what}: tensors are on cuda:{idx} but the current device is "
+                           f"cuda:{torch.cuda.current_device()}; wrap the call in torch.cuda.device()")
+    return idx
+
+
+def _dtype_check(what: str, t: torch.Tensor, dtype: torch.dtype, name: str) -> None:
+    if t.dtype != dtype:
+        raise TypeError(f"{what}: {name} must be {dtype}, got {t.dtype}")
+
+
+@functools.cache
+def is_e8m0_used() -> bool:
+    """Whether the GEMM ops treat block scales under the UE8M0 contract.
+
+    Mirrors ``_is_deep_gemm_e8m0_used`` (tasks/baseline/L1/
+    fp8_grouped_gemm_contiguous.py:53-71): on by default, switched off by
+    ``VLLM_USE_DEEP_GEMM=0`` or ``VLLM_USE_DEEP_GEMM_E8M0=0``.  Under the
+    UE8M0 contract each fp32 scale is rounded up to a power of two and applied
+    inside the block-scaled MFMA; otherwise scales are used as given."""
+    if not bool(int(os.environ.get("VLLM_USE_DEEP_GEMM", "1"))):
+        return False
+    return bool(int(os.environ.get("VLLM_USE_DEEP_GEMM_E8M0", "1")))
+
+
+# ---------------------------------------------------------------------------
+# Raw launchers
+# ---------------------------------------------------------------------------
+
+def per_token_group_quant_fp8(x: torch.Tensor, out_fp8: torch.Tensor, out_scale: torch.Tensor,
+                              use_ue8m0: bool = True, eps: float = QUANT_EPS) -> None:
+    """1x128 quant of bf16 ``x [M,K]`` into ``out_fp8 [M,K]`` and ``out_scale
+    [M,K/128]`` (any strides for the scales, e.g. column-major)."""
+    what = "per_token_group_quant_fp8"
+    _dev_check(what, x, out_fp8, out_scale)
+    _dtype_check(what, x, torch.bfloat16, "input")
+    _dtype_check(what, out_fp8, FP8, "output_fp8")
+    _dtype_check(what, out_scale, torch.float32, "output_scale")
+    if x.dim() != 2 or out_fp8.shape != x.shape:
+        raise ValueError(f"{what}: expected 2-D input and matching output, got {tuple(x.shape)} / {tuple(out_fp8.shape)}")
+    M, K = x.shape
+    if K % GROUP:
+        raise ValueError(f"{what}: K={K} must be a multiple of {GROUP}")
+    if tuple(out_scale.shape) != (M, K // GROUP):
+        raise ValueError(f"{what}: output_scale must be {(M, K // GROUP)}, got {tuple(out_scale.shape)}")
+    if x.stride(1) != 1 or out_fp8.stride(1) != 1:
+        raise ValueError(f"{what}: input and output rows must be contiguous")
+    check(lib().kbn_per_token_group_quant_fp8(
+        x.data_ptr(), M, K, x.stride(0), out_fp8.data_ptr(), out_fp8.stride(0),
+        out_scale.data_ptr(), out_scale.stride(0), out_scale.stride(1),
+        float(eps), int(bool(use_ue8m0)), _stream(x)), what)
+
+
+def silu_mul_quant_fp8(inp: torch.Tensor, out_fp8: torch.Tensor, out_scale: torch.Tensor,
+                       use_ue8m0: bool = True, eps: float = QUANT_EPS) -> None:
+    """y = bf16(silu(gate) * up) for ``inp = [gate | up]`` (bf16 [M, 2N']),
+    quantized 1x128 into ``out_fp8 [M,N']`` and ``out_scale [M, N'/128]``."""
+    what = "silu_mul_quant_fp8"
+    _dev_check(what, inp, out_fp8, out_scale)
+    _dtype_check(what, inp, torch.bfloat16, "input")
+    _dtype_check(what, out_fp8, FP8, "output")
+    _dtype_check(what, out_scale, torch.float32, "output_scales")
+    M, N = inp.shape
+    Nh = N // 2
+    if tuple(out_fp8.shape) != (M, Nh) or tuple(out_scale.shape) != (M, Nh // GROUP):
+        raise ValueError(f"{what}: bad output shapes {tuple(out_fp8.shape)} / {tuple(out_scale.shape)}")
+    if inp.stride(1) != 1 or out_fp8.stride(1) != 1:
+        raise ValueError(f"{what}: input and output rows must be contiguous")
+    check(lib().kbn_silu_mul_quant_fp8(
+        inp.data_ptr(), M, Nh, inp.stride(0), out_fp8.data_ptr(), out_fp8.stride(0),
+        out_scale.data_ptr(), out_scale.stride(0), out_scale.stride(1),
+        float(eps), int(bool(use_ue8m0)), _stream(inp)), what)
+
+
+def fp8_gemm_nt(q_input: torch.Tensor, input_scale: torch.Tensor, weight: torch.Tensor,
+                weight_scale: torch.Tensor, output: torch.Tensor, use_ue8m0: bool | None = None) -> None:
+    """output[M,N] (bf16) = block-scaled q_input[M,K] x weight[N,K]^T."""
+    what = "fp8_gemm_nt"
+    _dev_check(what, q_input, input_scale, weight, weight_scale, output)
+    _dtype_check(what, q_input, FP8, "q_input")
+    _dtype_check(what, weight, FP8, "weight")
+    _dtype_check(what, input_scale, torch.float32, "input_scale")
+    _dtype_check(what, weight_scale, torch.float32, "weight_scale")
+    _dtype_check(what, output, torch.bfloat16, "output")
+    M, K = q_input.shape
+    N, K2 = weight.shape
+    if K2 != K:
+        raise ValueError(f"{what}: K mismatch {K} vs {K2}")
+    if tuple(output.shape) != (M, N):
+        raise ValueError(f"{what}: output must be {(M, N)}, got {tuple(output.shape)}")
+    KB, NB = -(-K // GROUP), -(-N // GROUP)
+    if tuple(input_scale.shape) != (M, KB):
+        raise ValueError(f"{what}: input_scale must be {(M, KB)}, got {tuple(input_scale.shape)}")
+    if weight_scale.dim() != 2 or weight_scale.shape[0] < NB or weight_scale.shape[1] < KB:
+        raise ValueError(f"{what}: weight_scale must be at least {(NB, KB)}, got {tuple(weight_scale.shape)}")
+    if q_input.stride(1) != 1 or weight.stride(1) != 1 or output.stride(1) != 1 or weight_scale.stride(1) != 1:
+        raise ValueError(f"{what}: operands must be contiguous along K (and N for the output)")
+    ue8m0 = is_e8m0_used() if use_ue8m0 is None else bool(use_ue8m0)
+    check(lib().kbn_fp8_gemm_nt(
+        q_input.data_ptr(), q_input.stride(0), input_scale.data_ptr(), input_scale.stride(0), input_scale.stride(1),
+        weight.data_ptr(), weight.stride(0), weight_scale.data_ptr(), weight_scale.stride(0),
+        output.data_ptr(), output.stride(0), M, N, K, int(ue8m0), _stream(output)), what)
+
+
+def m_grouped_gemm_nt_contiguous(a_fp8: torch.Tensor, a_scale: torch.Tensor, b_fp8: torch.Tensor,
+                                 b_scale: torch.Tensor, c_bf16: torch.Tensor, expert_ids: torch.Tensor,
+                                 disable_ue8m0_cast: bool) -> None:
+    """Contiguous-layout grouped GEMM: row r of ``a_fp8`` multiplies expert
+    ``expert_ids[r]`` of ``b_fp8``; rows with id -1 are left unwritten."""
+    what = "m_grouped_gemm_nt_contiguous"
+    _dev_check(what, a_fp8, a_scale, b_fp8, b_scale, c_bf16, expert_ids)
+    _dtype_check(what, a_fp8, FP8, "a_fp8")
+    _dtype_check(what, b_fp8, FP8, "b_fp8")
+    _dtype_check(what, a_scale, torch.float32, "a_scale")
+    _dtype_check(what, b_scale, torch.float32, "b_scale")
+    _dtype_check(what, c_bf16, torch.bfloat16, "c_bf16")
+    _dtype_check(what, expert_ids, torch.int32, "expert_ids")
+    M_sum, K = a_fp8.shape
+    E, N, K2 = b_fp8.shape
+    if K2 != K:
+        raise ValueError(f"{what}: K mismatch {K} vs {K2}")
+    KB, NB = -(-K // GROUP), -(-N // GROUP)
+    if tuple(c_bf16.shape) != (M_sum, N) or tuple(expert_ids.shape) != (M_sum,):
+        raise ValueError(f"{what}: c_bf16 must be {(M_sum, N)} and expert_ids {(M_sum,)}")
+    if tuple(a_scale.shape) != (M_sum, KB) or tuple(b_scale.shape) != (E, NB, KB):
+        raise ValueError(f"{what}: scales must be {(M_sum, KB)} and {(E, NB, KB)}, got "
+                         f"{tuple(a_scale.shape)} / {tuple(b_scale.shape)}")
+    if not (b_fp8.is_contiguous() and b_scale.is_contiguous() and expert_ids.is_contiguous()):
+        raise ValueError(f"{what}: b_fp8, b_scale and expert_ids must be contiguous")
+    if a_fp8.stride(1) != 1 or c_bf16.stride(1) != 1:
+        raise ValueError(f"{what}: a_fp8 and c_bf16 rows must be contiguous")
+    check(lib().kbn_fp8_grouped_gemm_nt_contiguous(
+        a_fp8.data_ptr(), a_fp8.stride(0), a_scale.data_ptr(), a_scale.stride(0), a_scale.stride(1),
+        b_fp8.data_ptr(), b_scale.data_ptr(), c_bf16.data_ptr(), c_bf16.stride(0), expert_ids.data_ptr(),
+        M_sum, N, K, E, int(not disable_ue8m0_cast), _stream(c_bf16)), what)
+
+
+def debug_silu_bf16(g_bits: torch.Tensor, out_bits: torch.Tensor) -> None:
+    """Test hook: the kernels' silu (bf16 in, bf16 out) on int16 bit patterns."""
+    _dev_check("debug_silu_bf16", g_bits, out_bits)
+    if g_bits.dtype != torch.int16 or out_bits.dtype != torch.int16 or not g_bits.is_contiguous():
+        raise TypeError("debug_silu_bf16: contiguous int16 bit patterns expected")
+    check(lib().kbn_debug_silu_bf16(g_bits.data_ptr(), out_bits.data_ptr(), g_bits.numel(), _stream(g_bits)),
+          "debug_silu_bf16")
+
+
+# ---------------------------------------------------------------------------
+# torch.library registration (opaque custom ops with Meta impls)
+# ---------------------------------------------------------------------------
+
+_fp8_lib = torch.library.Library("kb_nano_fp8", "FRAGMENT")
+_moe_lib = torch.library.Library("kb_nano_fp8_moe", "FRAGMENT")
+
+
+def _has_op(ns: str, name: str) -> bool:
+    try:
+        getattr(getattr(torch.ops, ns), name)
+        return True
+    except (AttributeError, RuntimeError):
+        return False
+
+
+def _meta_noop(*args, **kwargs):
+    return None
+
+
+def _register():
+    if not _has_op("kb_nano_fp8", "fp8_gemm_nt"):
+        _fp8_lib.define("fp8_gemm_nt(Tensor q_input, Tensor input_scale, "
+                        "Tensor weight, Tensor weight_scale, Tensor! output) -> ()")
+        _fp8_lib.impl("fp8_gemm_nt", lambda q, s, w, ws, o: fp8_gemm_nt(q, s, w, ws, o), "CUDA")
+        _fp8_lib.impl("fp8_gemm_nt", _meta_noop, "Meta")
+    if not _has_op("kb_nano_fp8", "per_token_group_quant_fp8"):
+        _fp8_lib.define("per_token_group_quant_fp8(Tensor input, Tensor! output_fp8, "
+                        "Tensor! output_scale, bool column_major_scales=False) -> ()")
+        # the scale layout is read from the output's strides, so the
+        # column-major flag needs no separate code path
+        _fp8_lib.impl("per_token_group_quant_fp8",
+                      lambda x, q, s, column_major_scales=False: per_token_group_quant_fp8(x, q, s), "CUDA")
+        _fp8_lib.impl("per_token_group_quant_fp8", _meta_noop, "Meta")
+    if not _has_op("kb_nano_fp8", "silu_mul_quant_fp8"):
+        _fp8_lib.define("silu_mul_quant_fp8(Tensor input, Tensor! output, Tensor! output_scales, "
+                        "bool use_ue8m0=True, float eps=1e-10) -> ()")
+        _fp8_lib.impl("silu_mul_quant_fp8",
+                      lambda x, q, s, use_ue8m0=True, eps=QUANT_EPS: silu_mul_quant_fp8(x, q, s, use_ue8m0, eps),
+                      "CUDA")
+        _fp8_lib.impl("silu_mul_quant_fp8", _meta_noop, "Meta")
+    if not _has_op("kb_nano_fp8_moe", "m_grouped_gemm_nt_contiguous"):
+        _moe_lib.define("m_grouped_gemm_nt_contiguous(Tensor a_fp8, Tensor a_scale, "
+                        "Tensor b_fp8, Tensor b_scale, Tensor! c_bf16, Tensor expert_ids, "
+                        "bool disable_ue8m0_cast) -> ()")
+        _moe_lib.impl("m_grouped_gemm_nt_contiguous", m_grouped_gemm_nt_contiguous, "CUDA")
+        _moe_lib.impl("m_grouped_gemm_nt_contiguous", _meta_noop, "Meta")
+
+
+_register()

@@ -1,0 +1,108 @@
+// Shared device helpers and host-side error plumbing for the gfx950 FP8
+// linear-path kernels.  Only gfx950 (CDNA4) is targeted: fp8 means OCP
+// e4m3fn, wavefronts are 64 lanes wide.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdio>
+#include <cstring>
+
+namespace kbn {
+
+// --------------------------------------------------------------- errors ---
+
+// Per-thread last-error message returned by kbn_last_error().
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
+#define KBN_CHECK_ARG(cond, ...)            \
+    do {                                    \
+        if (!(cond)) {                      \
+            ::kbn::set_error(__VA_ARGS__);  \
+            return 1;                       \
+        }                                   \
+    } while (0)
+
+#define KBN_CHECK_LAUNCH(what)                                                    \
+    do {                                                                          \
+        hipError_t e_ = hipGetLastError();                                        \
+        if (e_ != hipSuccess) {                                                   \
+            ::kbn::set_error("%s: launch failed: %s", what, hipGetErrorString(e_)); \
+            return 2;                                                             \
+        }                                                                         \
+    } while (0)
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ------------------------------------------------------------ constants ---
+
+constexpr int kGroup = 128;          // 1x128 activation groups, 128x128 weight blocks
+constexpr float kFp8Max = 448.0f;    // float8_e4m3fn max finite
+
+// ------------------------------------------------------- device helpers ---
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// Round-to-nearest-even float -> bf16 bits (inputs here are never NaN).
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Smallest power of two >= r for a positive normal float r (exponent bits,
+// +1 when any mantissa bit is set): the UE8M0 rounding of the scale.
+__device__ __forceinline__ float ue8m0_ceil(float r) {
+    uint32_t u = __float_as_uint(r);
+    uint32_t e = (u >> 23) & 0xFFu;
+    if (u & 0x7FFFFFu) e += 1;
+    return __uint_as_float(e << 23);
+}
+
+// Biased exponent byte (E8M0) of ue8m0_ceil(r): the per-operand scale
+// consumed by the block-scaled MFMA.
+__device__ __forceinline__ int ue8m0_ceil_byte(float r) {
+    uint32_t u = __float_as_uint(r);
+    uint32_t e = (u >> 23) & 0xFFu;
+    if (u & 0x7FFFFFu) e += 1;
+    return (int)(e > 254u ? 254u : e);
+}
+
+// Exact reciprocal of a power of two in the normal range.
+__device__ __forceinline__ float pow2_recip(float s) {
+    uint32_t e = (__float_as_uint(s) >> 23) & 0xFFu;
+    return __uint_as_float((254u - e) << 23);
+}
+
+// Max over each row of 16 lanes (DPP quad swaps + row rotates); operands
+// are non-negative floats carried as bits, so an unsigned max is a float max.
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
+    uint32_t t;
+    t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    v = v > t ? v : t;
+    t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    v = v > t ? v : t;
+    t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xF, 0xF, false); // row_ror:4
+    v = v > t ? v : t;
+    t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false); // row_ror:8
+    v = v > t ? v : t;
+    return v;
+}
+
+// Pack four already-clamped floats into four e4m3fn codes (RNE, hardware).
+__device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    return (uint32_t)w;
+}
+
+// clamp(v, -448, 448) that keeps NaN (comparisons with NaN are false).
+__device__ __forceinline__ float clamp_fp8(float v) {
+    v = v > kFp8Max ? kFp8Max : v;
+    return v < -kFp8Max ? -kFp8Max : v;
+}
+
+}  // namespace kbn

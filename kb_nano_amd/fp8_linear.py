@@ -1,0 +1,183 @@
+"""Block-scaled FP8 linear and per-token-group activation quant on MI355X.
+
+Drop-in for ``tasks/baseline/L1/fp8_linear.py`` (kb_nano): same classes,
+attributes, helper functions and op names, backed by the gfx950 HIP kernels
+of ``libkbn_fp8.so`` instead of Triton + DeepGEMM + FlashInfer.
+
+Reference interface mirrored here:
+  * ``PerTokenGroupQuantFp8.forward(x, out_fp8, out_scale) -> None``   (:282-297)
+  * ``_alloc_colmajor_scale(M, num_groups, device)``                  (:300-313)
+  * ``_Fp8PrefillBufs(max_tokens, K, N, device)`` with ``.a .s .o``    (:316-332)
+  * ``Fp8Linear`` (``BLOCK_SIZE``, ``_FLASHINFER_M_THRESHOLD``,
+    ``_a_buf/_s_buf/_o_buf/_pf``, ``_ensure_buffers``, ``forward``)   (:335-450)
+  * ``postprocess_fp8_weights[_batched]``                            (:453-554)
+  * ops ``torch.ops.kb_nano_fp8.{fp8_gemm_nt, per_token_group_quant_fp8}`` (:89-178)
+
+The reference sends M < 32 to FlashInfer's Hopper-only swapAB kernel
+(:398-417); on gfx950 that branch does not exist and small M is handled
+inside ``fp8_gemm_nt`` by the GEMM's own small-M tile configuration.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+
+from . import _ops
+from ._ops import FP8, GROUP, QUANT_EPS, is_e8m0_used
+
+_FP8_INFO = torch.finfo(FP8)
+_QUANT_EPS = QUANT_EPS
+
+
+def _is_deep_gemm_e8m0_used() -> bool:
+    """Name kept from the reference (fp8_grouped_gemm_contiguous.py:53-71)."""
+    return is_e8m0_used()
+
+
+def _per_token_group_quant_fp8(x: torch.Tensor, out_fp8: torch.Tensor, out_scale: torch.Tensor,
+                               use_ue8m0: bool = True, column_major_scales: bool = False) -> None:
+    """In-place 1x128 quant (reference :234-279).  The scale layout comes from
+    ``out_scale``'s strides; ``column_major_scales`` only documents the
+    caller's intent, as in the reference's Triton path."""
+    _ops.per_token_group_quant_fp8(x, out_fp8, out_scale, use_ue8m0=use_ue8m0, eps=_QUANT_EPS)
+
+
+class PerTokenGroupQuantFp8(nn.Module):
+    """In-place per-token-group FP8 quantization (one HIP kernel launch).
+
+    ``forward(x, out_fp8, out_scale)``: x bf16 [M,K] (made contiguous if it is
+    not), out_fp8 float8_e4m3fn [M,K], out_scale float32 [M,K/128] with any
+    strides (row-major by default, column-major for the dense GEMM)."""
+
+    def forward(self, x: torch.Tensor, out_fp8: torch.Tensor, out_scale: torch.Tensor) -> None:
+        torch.ops.kb_nano_fp8.per_token_group_quant_fp8(
+            x if x.is_contiguous() else x.contiguous(), out_fp8, out_scale)
+
+
+def _alloc_colmajor_scale(M: int, num_groups: int, device: torch.device) -> torch.Tensor:
+    """fp32 scales exposed as [M, num_groups] over [num_groups, M] storage:
+    strides (1, M), element (m, g) at g*M + m."""
+    return torch.empty((num_groups, M), device=device, dtype=torch.float32).t()
+
+
+class _Fp8PrefillBufs:
+    """One shared set of prefill buffers per (K, N): fp8 activations ``a``,
+    column-major scales ``s`` and bf16 output ``o`` for ``max_tokens`` rows."""
+
+    __slots__ = ("a", "s", "o")
+
+    def __init__(self, max_tokens: int, K: int, N: int, device: torch.device):
+        self.a = torch.empty(max_tokens, K, dtype=FP8, device=device)
+        self.s = _alloc_colmajor_scale(max_tokens, math.ceil(K / GROUP), device)
+        self.o = torch.empty(max_tokens, N, dtype=torch.bfloat16, device=device)
+
+
+def _maybe_get_flashinfer_fp8_gemm():
+    """The reference's Hopper-only small-M kernel (:55-82); never present on
+    gfx950, where ``fp8_gemm_nt`` covers every M."""
+    return None
+
+
+class Fp8Linear(nn.Module):
+    """Block-scaled FP8 linear: bf16 input, fp8 e4m3 weight [N,K] with fp32
+    scales [ceil(N/128), ceil(K/128)], bf16 output [..., N].
+
+    ``forward`` quantizes the input 1x128 with UE8M0 scales into column-major
+    scale storage and runs the block-scaled GEMM; with buffers installed the
+    result is a view into the reused output buffer, exactly as the reference
+    returns ``_o_buf[:M]`` / ``_pf.o[:M]``."""
+
+    BLOCK_SIZE = GROUP
+    _FLASHINFER_M_THRESHOLD = 32
+
+    def __init__(self):
+        super().__init__()
+        self._a_buf: torch.Tensor | None = None
+        self._s_buf: torch.Tensor | None = None
+        self._o_buf: torch.Tensor | None = None
+        self._pf: _Fp8PrefillBufs | None = None
+
+    def _ensure_buffers(self, max_tokens: int, K: int, N: int, device: torch.device):
+        num_groups = math.ceil(K / self.BLOCK_SIZE)
+        self._a_buf = torch.empty(max_tokens, K, dtype=FP8, device=device)
+        self._s_buf = _alloc_colmajor_scale(max_tokens, num_groups, device)
+        self._o_buf = torch.empty(max_tokens, N, dtype=torch.bfloat16, device=device)
+
+    def forward(self, input_bf16: torch.Tensor, weight_fp8: torch.Tensor,
+                weight_scale_inv: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+        N, K = weight_fp8.shape
+        x2 = input_bf16.reshape(-1, K)
+        M = x2.shape[0]
+        G = (K + self.BLOCK_SIZE - 1) // self.BLOCK_SIZE
+        dev = x2.device
+
+        bufs = None
+        if not torch.compiler.is_compiling():
+            if self._a_buf is not None and M <= self._a_buf.shape[0]:
+                bufs = (self._a_buf, self._o_buf)
+            elif self._pf is not None and M <= self._pf.a.shape[0]:
+                bufs = (self._pf.a, self._pf.o)
+        if bufs is not None:
+            q_input, output = bufs[0][:M], bufs[1][:M]
+        else:
+            q_input = torch.empty(M, K, dtype=FP8, device=dev)
+            output = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        input_scale = _alloc_colmajor_scale(M, G, dev)
+
+        torch.ops.kb_nano_fp8.per_token_group_quant_fp8(x2, q_input, input_scale, True)
+        torch.ops.kb_nano_fp8.fp8_gemm_nt(q_input, input_scale, weight_fp8, weight_scale_inv, output)
+
+        if bias is not None:
+            output = output + bias
+        return output.view(*input_bf16.shape[:-1], N)
+
+
+# ---------------------------------------------------------------------------
+# Load-time weight processing
+# ---------------------------------------------------------------------------
+
+def _block_requant(w_f32: torch.Tensor, use_ue8m0: bool, eps: float = 1e-4):
+    """128x128 block quantization of a float32 [N,K] matrix on its device.
+
+    Follows DeepGEMM v2.1.1.post3's ``per_block_cast_to_fp8`` (pyproject.toml:21;
+    called at fp8_linear.py:497-499): pad to whole blocks, amax per block
+    clamped to 1e-4, sf = amax/448 rounded up to a power of two under UE8M0,
+    codes = fp8(x * (1/sf)).  Returns (fp8 [N,K], fp32 [ceil(N/128), ceil(K/128)])."""
+    N, K = w_f32.shape
+    NB, KB = math.ceil(N / GROUP), math.ceil(K / GROUP)
+    pad = torch.zeros(NB * GROUP, KB * GROUP, dtype=torch.float32, device=w_f32.device)
+    pad[:N, :K] = w_f32
+    blocks = pad.view(NB, GROUP, KB, GROUP)
+    sf = blocks.abs().amax(dim=(1, 3), keepdim=True).clamp_min(eps) / _FP8_INFO.max
+    if use_ue8m0:
+        sf = torch.pow(2.0, torch.ceil(torch.log2(sf)))
+    q = (blocks * (1.0 / sf)).to(FP8).view(NB * GROUP, KB * GROUP)[:N, :K].contiguous()
+    return q, sf.view(NB, KB)
+
+
+def postprocess_fp8_weights(weight_fp8: torch.Tensor, scale_inv: torch.Tensor):
+    """Re-quantize a checkpoint's fp8 weight to the scale format the GEMM
+    consumes (reference :453-512).  Under the UE8M0 contract the weight is
+    dequantized per 128x128 block and re-quantized with power-of-two scales;
+    the scale layout stays the canonical fp32 [ceil(N/128), ceil(K/128)]
+    (the gfx950 kernels read it directly, no layout transform is needed)."""
+    N, K = weight_fp8.shape
+    NB, KB = math.ceil(N / GROUP), math.ceil(K / GROUP)
+    scale = scale_inv[:NB, :KB].to(torch.float32)
+    expand = scale.repeat_interleave(GROUP, 0)[:N].repeat_interleave(GROUP, 1)[:, :K]
+    w_f32 = weight_fp8.to(torch.float32) * expand
+    return _block_requant(w_f32, use_ue8m0=is_e8m0_used())
+
+
+def postprocess_fp8_weights_batched(weight_fp8: torch.Tensor, scale_inv: torch.Tensor) -> None:
+    """In-place per-expert version for MoE weights [E,N,K] / scales
+    [E, ceil(N/128), ceil(K/128)] (reference :515-554)."""
+    assert weight_fp8.ndim == 3
+    E, N, K = weight_fp8.shape
+    NB, KB = math.ceil(N / GROUP), math.ceil(K / GROUP)
+    for e in range(E):
+        w_new, s_new = postprocess_fp8_weights(weight_fp8[e], scale_inv[e])
+        weight_fp8[e].copy_(w_new)
+        scale_inv[e, :NB, :KB].copy_(s_new)

@@ -1,0 +1,327 @@
+"""CPU oracle for the block-scaled FP8 linear path (TEST INFRASTRUCTURE ONLY).
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg import this package, and only as the checker or the timed CPU baseline.
+The product package ``kb_nano_amd`` never imports it.
+
+The arithmetic lives in ``kbn_oracle.c`` (plain C, built by ``oracle/Makefile``
+into ``libkbn_oracle.so``); this module wraps it with numpy and restates the
+contiguous MoE layout of ``tasks/baseline/L2/fused_experts.py:32-136`` in numpy.
+Every function cites the reference lines it follows.
+
+Parity pins (see ``tests/test_oracle.py``):
+  * e4m3 encode: exhaustive over all 65,536 bf16 bit patterns against torch's
+    ``.to(torch.float8_e4m3fn)`` (an independent library routine).
+  * UE8M0 scale: exhaustive over every finite non-negative bf16 absmax against
+    torch's ``pow(2, ceil(log2(x/448)))`` form used by the reference.
+  * silu: all 65,536 bf16 gate values against a 40-digit ``decimal`` evaluation.
+  * quant / silu-quant: the reference's own torch formula
+    (``tasks/reference/L1/fp8_linear.py:41-64``) on seeded tensors, plus the
+    committed golden fixtures.
+  * GEMM: float64 brute force on tiny shapes, torch fp32 dequant-matmul on
+    small shapes, and closed-form special cases (single non-zero K block,
+    identity-like weights, all-equal scales).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+import threading
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libkbn_oracle.so")
+_SRC_PATH = os.path.join(_HERE, "kbn_oracle.c")
+_LOCK = threading.Lock()
+_LIB = None
+
+GROUP = 128
+FP8_MAX = 448.0
+EPS = 1e-10
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+
+
+def build(force: bool = False) -> str:
+    """Compile the oracle with gcc (via its Makefile) if missing or stale."""
+    stale = (not os.path.exists(_LIB_PATH)
+             or os.path.getmtime(_LIB_PATH) < os.path.getmtime(_SRC_PATH))
+    if force or stale:
+        cmd = ["make", "-s", "-C", _HERE]
+        if force:
+            cmd.append("-B")
+        subprocess.run(cmd, check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _LIB
+    with _LOCK:
+        if _LIB is None:
+            build()
+            L = ctypes.CDLL(_LIB_PATH)
+            L.orc_e4m3_encode.restype = ctypes.c_uint8
+            L.orc_e4m3_encode.argtypes = [ctypes.c_float]
+            L.orc_e4m3_decode.restype = ctypes.c_float
+            L.orc_e4m3_decode.argtypes = [ctypes.c_uint8]
+            L.orc_ue8m0_from_ratio.restype = ctypes.c_float
+            L.orc_ue8m0_from_ratio.argtypes = [ctypes.c_float]
+            L.orc_silu_bf16.restype = ctypes.c_uint16
+            L.orc_silu_bf16.argtypes = [ctypes.c_uint16]
+            L.orc_double_to_bf16.restype = ctypes.c_uint16
+            L.orc_double_to_bf16.argtypes = [ctypes.c_double]
+            L.orc_float_to_bf16.restype = ctypes.c_uint16
+            L.orc_float_to_bf16.argtypes = [ctypes.c_float]
+            qargs = [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, ctypes.c_float, ctypes.c_int]
+            L.orc_quant_group128.restype = ctypes.c_int
+            L.orc_quant_group128.argtypes = qargs
+            L.orc_silu_mul_quant.restype = ctypes.c_int
+            L.orc_silu_mul_quant.argtypes = qargs
+            L.orc_gemm_nt_sample.restype = ctypes.c_int
+            L.orc_gemm_nt_sample.argtypes = [_P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64,
+                                             _I64, _I64, _I64, _P, _I64, _P, _I64, _P, ctypes.c_int]
+            L.orc_grouped_gemm_nt_sample.restype = ctypes.c_int
+            L.orc_grouped_gemm_nt_sample.argtypes = [_P, _P, _I64, _I64, _P, _P, _P,
+                                                     _I64, _I64, _I64, _I64,
+                                                     _P, _I64, _P, _I64, _P, ctypes.c_int]
+            _LIB = L
+    return _LIB
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+# ---------------------------------------------------------------------------
+# bf16 helpers (numpy has no bf16: bf16 tensors travel as uint16 bit patterns)
+# ---------------------------------------------------------------------------
+
+def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round float32 to bf16 (RNE) and return the bit patterns."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7F800000) == 0x7F800000
+    nan &= (u & 0x007FFFFF) != 0
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+# ---------------------------------------------------------------------------
+# Scalar-table views of the C encoders (vectorised through lookup tables)
+# ---------------------------------------------------------------------------
+
+_E4M3_DECODE = None
+
+
+def e4m3_decode_table() -> np.ndarray:
+    global _E4M3_DECODE
+    if _E4M3_DECODE is None:
+        L = lib()
+        _E4M3_DECODE = np.array([L.orc_e4m3_decode(i) for i in range(256)], dtype=np.float32)
+    return _E4M3_DECODE
+
+
+def e4m3_decode(codes: np.ndarray) -> np.ndarray:
+    return e4m3_decode_table()[np.asarray(codes, dtype=np.uint8)]
+
+
+def e4m3_encode(x: np.ndarray) -> np.ndarray:
+    L = lib()
+    flat = np.asarray(x, dtype=np.float32).ravel()
+    return np.array([L.orc_e4m3_encode(float(v)) for v in flat], dtype=np.uint8).reshape(np.shape(x))
+
+
+def ue8m0_from_ratio(r: np.ndarray) -> np.ndarray:
+    L = lib()
+    flat = np.asarray(r, dtype=np.float32).ravel()
+    return np.array([L.orc_ue8m0_from_ratio(float(v)) for v in flat], dtype=np.float32).reshape(np.shape(r))
+
+
+_SILU_TABLE = None
+
+
+def silu_bf16_table() -> np.ndarray:
+    """bf16 silu(g) for every one of the 65,536 bf16 bit patterns g."""
+    global _SILU_TABLE
+    if _SILU_TABLE is None:
+        L = lib()
+        _SILU_TABLE = np.array([L.orc_silu_bf16(i) for i in range(65536)], dtype=np.uint16)
+    return _SILU_TABLE
+
+
+# ---------------------------------------------------------------------------
+# Quantizers
+# ---------------------------------------------------------------------------
+
+def quant_group128(x_bits: np.ndarray, eps: float = EPS, use_ue8m0: bool = True):
+    """Per-token-group 1x128 quant (tasks/baseline/L1/fp8_linear.py:181-215).
+
+    ``x_bits``: uint16 bf16 bit patterns [M, K].  Returns (q uint8 [M,K],
+    s float32 [M, K/128] row-major)."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    M, K = x.shape
+    q = np.empty((M, K), dtype=np.uint8)
+    s = np.empty((M, K // GROUP), dtype=np.float32)
+    rc = lib().orc_quant_group128(_ptr(x), M, K, K, _ptr(q), K, _ptr(s), K // GROUP, 1,
+                                  float(eps), int(use_ue8m0))
+    if rc:
+        raise ValueError(f"orc_quant_group128 failed ({rc}); K must be a multiple of 128")
+    return q, s
+
+
+def silu_mul_quant(in_bits: np.ndarray, eps: float = EPS, use_ue8m0: bool = True):
+    """Fused SiLU*Mul + 1x128 quant (tasks/baseline/L1/silu_mul_quant_fp8.py:48-76).
+
+    ``in_bits``: uint16 bf16 [M, 2*Nh].  Returns (q uint8 [M, Nh], s float32
+    [M, Nh/128] row-major values; the device op stores them column-major)."""
+    x = np.ascontiguousarray(in_bits, dtype=np.uint16)
+    M, N2 = x.shape
+    Nh = N2 // 2
+    q = np.empty((M, Nh), dtype=np.uint8)
+    s = np.empty((M, Nh // GROUP), dtype=np.float32)
+    rc = lib().orc_silu_mul_quant(_ptr(x), M, Nh, N2, _ptr(q), Nh, _ptr(s), Nh // GROUP, 1,
+                                  float(eps), int(use_ue8m0))
+    if rc:
+        raise ValueError(f"orc_silu_mul_quant failed ({rc}); N/2 must be a multiple of 128")
+    return q, s
+
+
+def quant_block128(w_f32: np.ndarray, eps: float = EPS, use_ue8m0: bool = True):
+    """128x128 block quant of a float32 [R, C] matrix
+    (bench/kernels/scenario_registry.py:185-221): one scale per block, codes
+    via the C encoder.  Returns (q uint8 [R, C], s float32 [ceil(R/128), ceil(C/128)])."""
+    w = np.asarray(w_f32, dtype=np.float32)
+    R, C = w.shape
+    RB, CB = -(-R // GROUP), -(-C // GROUP)
+    pad = np.zeros((RB * GROUP, CB * GROUP), dtype=np.float32)
+    pad[:R, :C] = w
+    amax = np.abs(pad.reshape(RB, GROUP, CB, GROUP)).max(axis=(1, 3))
+    ratio = (np.maximum(amax, np.float32(eps)) / np.float32(FP8_MAX)).astype(np.float32)
+    s = ue8m0_from_ratio(ratio) if use_ue8m0 else ratio
+    sx = np.repeat(np.repeat(s, GROUP, 0), GROUP, 1)[:R, :C]
+    v = np.clip(w / sx, -FP8_MAX, FP8_MAX).astype(np.float32)
+    q = _encode_fast(v)
+    return q, s.astype(np.float32)
+
+
+def _encode_fast(v: np.ndarray) -> np.ndarray:
+    """Vectorised e4m3 encoding of already-clamped float32 values: nearest
+    code by value with ties to the even code, matching ``orc_e4m3_encode``
+    (checked against it in tests)."""
+    table = e4m3_decode_table()
+    pos = np.arange(0, 127, dtype=np.uint8)      # 0x00..0x7E, non-negative finite codes
+    vals = table[pos].astype(np.float64)
+    a = np.abs(v.astype(np.float64)).ravel()
+    idx = np.searchsorted(vals, a, side="left")
+    idx = np.clip(idx, 1, len(vals) - 1)
+    lo, hi = vals[idx - 1], vals[idx]
+    dlo, dhi = a - lo, hi - a
+    pick_hi = (dhi < dlo) | ((dhi == dlo) & ((pos[idx] & 1) == 0))
+    code = np.where(pick_hi, pos[idx], pos[idx - 1]).astype(np.uint8)
+    exact0 = a == 0.0
+    code[exact0] = 0
+    sign = (np.signbit(v.ravel()) & (code != 0x7F)).astype(np.uint8) << 7
+    return (code | sign).reshape(v.shape)
+
+
+# ---------------------------------------------------------------------------
+# GEMM oracles (float64 accumulation at sampled output positions)
+# ---------------------------------------------------------------------------
+
+def gemm_nt_sample(A, sA, W, sW, rows=None, cols=None, ue8m0: bool = False) -> np.ndarray:
+    """D[rows][:, cols] of the block-scaled NT GEMM in float64.
+
+    A uint8 [M,K]; sA float32 [M,K/128] (any strides: a numpy view is made
+    contiguous here); W uint8 [N,K]; sW float32 [ceil(N/128), K/128].
+    ``ue8m0`` rounds every scale up to a power of two first (the UE8M0 cast
+    contract)."""
+    A = np.ascontiguousarray(A, dtype=np.uint8)
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    sA = np.ascontiguousarray(sA, dtype=np.float32)
+    sW = np.ascontiguousarray(sW, dtype=np.float32)
+    M, K = A.shape
+    N = W.shape[0]
+    rows = np.arange(M, dtype=np.int64) if rows is None else np.ascontiguousarray(rows, dtype=np.int64)
+    cols = np.arange(N, dtype=np.int64) if cols is None else np.ascontiguousarray(cols, dtype=np.int64)
+    out = np.empty((len(rows), len(cols)), dtype=np.float64)
+    rc = lib().orc_gemm_nt_sample(_ptr(A), K, _ptr(sA), sA.shape[1], 1, _ptr(W), K, _ptr(sW), sW.shape[1],
+                                  M, N, K, _ptr(rows), len(rows), _ptr(cols), len(cols), _ptr(out), int(ue8m0))
+    if rc:
+        raise ValueError(f"orc_gemm_nt_sample failed ({rc})")
+    return out
+
+
+def grouped_gemm_nt_sample(A, sA, B, sB, expert_ids, rows=None, cols=None, ue8m0: bool = False) -> np.ndarray:
+    """Contiguous grouped GEMM at sampled rows/cols (NaN for rows with id -1).
+
+    A uint8 [M_sum,K]; sA float32 [M_sum,K/128]; B uint8 [E,N,K];
+    sB float32 [E,ceil(N/128),K/128]; expert_ids int32 [M_sum]."""
+    A = np.ascontiguousarray(A, dtype=np.uint8)
+    B = np.ascontiguousarray(B, dtype=np.uint8)
+    sA = np.ascontiguousarray(sA, dtype=np.float32)
+    sB = np.ascontiguousarray(sB, dtype=np.float32)
+    ids = np.ascontiguousarray(expert_ids, dtype=np.int32)
+    M_sum, K = A.shape
+    E, N, _ = B.shape
+    rows = np.arange(M_sum, dtype=np.int64) if rows is None else np.ascontiguousarray(rows, dtype=np.int64)
+    cols = np.arange(N, dtype=np.int64) if cols is None else np.ascontiguousarray(cols, dtype=np.int64)
+    out = np.empty((len(rows), len(cols)), dtype=np.float64)
+    rc = lib().orc_grouped_gemm_nt_sample(_ptr(A), _ptr(sA), sA.shape[1], 1, _ptr(B), _ptr(sB), _ptr(ids),
+                                          M_sum, N, K, E, _ptr(rows), len(rows), _ptr(cols), len(cols),
+                                          _ptr(out), int(ue8m0))
+    if rc:
+        raise ValueError(f"orc_grouped_gemm_nt_sample failed ({rc})")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Contiguous MoE layout (tasks/baseline/L2/fused_experts.py:32-136)
+# ---------------------------------------------------------------------------
+
+def compute_aligned_M(M: int, num_topk: int, num_experts: int, alignment: int) -> int:
+    """fused_experts.py:32-39: M_sum = roundup(M*k + E*(align-1), align)."""
+    m_sum = M * num_topk + num_experts * (alignment - 1)
+    rem = m_sum % alignment
+    return m_sum + (alignment - rem if rem else 0)
+
+
+def permute_contiguous(topk_ids: np.ndarray, num_experts: int, alignment: int):
+    """fused_experts.py:42-116 restated: returns (expert_ids int32 [M_sum],
+    dest int64 [M*k] destination row of each (token, slot), M_sum).
+
+    Expert e owns rows [off[e], off[e] + roundup(count[e], align)); the first
+    count[e] of them hold its tokens in (token, slot) order (stable sort) and
+    carry id e, the rest are padding with id -1."""
+    ids = np.asarray(topk_ids, dtype=np.int64)
+    M, k = ids.shape
+    flat = ids.reshape(-1)
+    M_sum = compute_aligned_M(M, k, num_experts, alignment)
+    counts = np.bincount(flat, minlength=num_experts).astype(np.int64)
+    aligned = (counts + alignment - 1) // alignment * alignment
+    off = np.zeros(num_experts + 1, dtype=np.int64)
+    off[1:] = np.cumsum(aligned)
+    expert_ids = np.full(M_sum, -1, dtype=np.int32)
+    for e in range(num_experts):
+        expert_ids[off[e]:off[e] + counts[e]] = e
+    order = np.argsort(flat, kind="stable")
+    within = np.empty_like(flat)
+    seen = np.zeros(num_experts, dtype=np.int64)
+    for pos in order:
+        e = flat[pos]
+        within[pos] = seen[e]
+        seen[e] += 1
+    dest = off[flat] + within
+    return expert_ids, dest, M_sum
+
+
+def unpermute_and_reduce(mm2_out_f32: np.ndarray, inv_perm: np.ndarray, topk_weights: np.ndarray) -> np.ndarray:
+    """fused_experts.py:119-136: out[m] = sum_j w[m,j] * mm2_out[inv_perm[m,j]]."""
+    g = mm2_out_f32[np.asarray(inv_perm, dtype=np.int64)]
+    return (g * np.asarray(topk_weights, dtype=np.float32)[..., None]).sum(axis=1)

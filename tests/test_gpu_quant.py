@@ -1,0 +1,170 @@
+"""GPU parity of the quant kernels against the C oracle: bit-exact codes and
+scales (tasks/baseline/L1/fp8_linear.py:181-215,
+tasks/baseline/L1/silu_mul_quant_fp8.py:23-143)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests._util import bf16_bits, fp8_codes, from_bits, seeded_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def _quant_gpu(x, col_major=False, use_ue8m0=True, eps=1e-10):
+    from kb_nano_amd import _ops
+    from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
+    M, K = x.shape
+    q = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=x.device)
+    s = _alloc_colmajor_scale(M, K // 128, x.device) if col_major else \
+        torch.empty(M, K // 128, dtype=torch.float32, device=x.device)
+    _ops.per_token_group_quant_fp8(x, q, s, use_ue8m0=use_ue8m0, eps=eps)
+    torch.cuda.synchronize()
+    return q, s
+
+
+def test_e4m3_conversion_exhaustive(gpu_device):
+    """Groups whose absmax is exactly 448 get scale 1, so q = e4m3(x): every
+    finite bf16 value in [-448, 448] goes through the hardware convert."""
+    allb = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    vals = oracle.bf16_bits_to_f32(allb)
+    keep = np.isfinite(vals) & (np.abs(vals) <= 448.0)
+    pool = allb[keep]
+    per = 127
+    G = -(-len(pool) // per)
+    pool = np.concatenate([pool, np.zeros(G * per - len(pool), dtype=np.uint16)])
+    x = np.empty((G, 128), dtype=np.uint16)
+    x[:, 0] = 0x43E0  # 448.0
+    x[:, 1:] = pool.reshape(G, per)
+    x = x.reshape(-1, 1024) if G % 8 == 0 else x.reshape(G, 128)
+    qo, so = oracle.quant_group128(x)
+    assert np.all(so == 1.0)
+    q, s = _quant_gpu(from_bits(x, gpu_device))
+    assert np.array_equal(s.cpu().numpy(), so)
+    assert np.array_equal(fp8_codes(q), qo)
+
+
+@pytest.mark.parametrize("M,K", [(1, 128), (3, 2048), (64, 2048), (130, 7168), (257, 1536), (8, 28672)])
+@pytest.mark.parametrize("col_major", [False, True])
+def test_quant_matches_oracle(gpu_device, M, K, col_major):
+    x = seeded_bf16((M, K), seed=M * 7 + K, outlier_frac=1e-3)
+    if M > 2:
+        x[1, :] = 0            # all-zero groups -> 2^-42
+        x[2, :128] = 1e-38     # subnormal-range inputs
+    qo, so = oracle.quant_group128(bf16_bits(x))
+    q, s = _quant_gpu(x.to(gpu_device), col_major=col_major)
+    assert np.array_equal(s.cpu().numpy(), so)
+    assert np.array_equal(fp8_codes(q), qo)
+    if col_major:
+        assert s.stride() == (1, M)
+
+
+def test_quant_plain_fp32_scales(gpu_device):
+    x = seeded_bf16((96, 1024), seed=11, outlier_frac=1e-2)
+    qo, so = oracle.quant_group128(bf16_bits(x), use_ue8m0=False)
+    q, s = _quant_gpu(x.to(gpu_device), use_ue8m0=False)
+    assert np.array_equal(s.cpu().numpy(), so)
+    assert np.array_equal(fp8_codes(q), qo)
+
+
+def test_quant_strided_rows(gpu_device):
+    big = seeded_bf16((40, 1024 + 256), seed=3).to(gpu_device)
+    x = big[:, 128:1152]
+    assert x.stride(0) == 1280
+    qo, so = oracle.quant_group128(bf16_bits(x))
+    q, s = _quant_gpu(x)
+    assert np.array_equal(fp8_codes(q), qo) and np.array_equal(s.cpu().numpy(), so)
+
+
+def test_quant_module_and_op(gpu_device):
+    from kb_nano_amd import PerTokenGroupQuantFp8
+    x = seeded_bf16((33, 512), seed=5).to(gpu_device)
+    q = torch.empty(33, 512, dtype=torch.float8_e4m3fn, device=gpu_device)
+    s = torch.empty(33, 4, dtype=torch.float32, device=gpu_device)
+    PerTokenGroupQuantFp8()(x.t().contiguous().t(), q, s)   # non-contiguous input is made contiguous
+    torch.cuda.synchronize()
+    qo, so = oracle.quant_group128(bf16_bits(x))
+    assert np.array_equal(fp8_codes(q), qo) and np.array_equal(s.cpu().numpy(), so)
+
+
+def test_quant_rejects_bad_args(gpu_device):
+    from kb_nano_amd import _ops
+    x = torch.zeros(4, 200, dtype=torch.bfloat16, device=gpu_device)
+    with pytest.raises(ValueError):
+        _ops.per_token_group_quant_fp8(x, torch.empty(4, 200, dtype=torch.float8_e4m3fn, device=gpu_device),
+                                       torch.empty(4, 2, device=gpu_device))
+    with pytest.raises(RuntimeError):
+        _ops.per_token_group_quant_fp8(x.cpu(), torch.empty(4, 200, dtype=torch.float8_e4m3fn),
+                                       torch.empty(4, 2))
+
+
+def test_quant_empty(gpu_device):
+    q, s = _quant_gpu(torch.empty(0, 256, dtype=torch.bfloat16, device=gpu_device))
+    assert q.shape == (0, 256) and s.shape == (0, 2)
+
+
+# ------------------------------------------------------------ SiLU + quant
+
+def test_silu_exhaustive(gpu_device):
+    """All 65,536 bf16 gate values through the kernels' silu vs the oracle's
+    correctly rounded table (itself pinned against 50-digit decimal)."""
+    from kb_nano_amd import _ops
+    g = torch.arange(65536, dtype=torch.int32).to(torch.int16).to(gpu_device)
+    out = torch.empty_like(g)
+    _ops.debug_silu_bf16(g, out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().astype(np.uint16)
+    want = oracle.silu_bf16_table()
+    allb = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    finite = (allb & 0x7F80) != 0x7F80
+    mism = np.nonzero((got != want) & finite)[0]
+    assert mism.size == 0, [(hex(i), hex(got[i]), hex(want[i])) for i in mism[:10]]
+
+
+def _silu_gpu(inp, col_major=True, use_ue8m0=True):
+    from kb_nano_amd import _ops
+    M, N = inp.shape
+    q = torch.empty(M, N // 2, dtype=torch.float8_e4m3fn, device=inp.device)
+    s = torch.empty(N // 256, M, dtype=torch.float32, device=inp.device).t() if col_major else \
+        torch.empty(M, N // 256, dtype=torch.float32, device=inp.device)
+    _ops.silu_mul_quant_fp8(inp, q, s, use_ue8m0=use_ue8m0)
+    torch.cuda.synchronize()
+    return q, s
+
+
+@pytest.mark.parametrize("M,Nh", [(8, 128), (128, 1024), (136, 2048), (256, 4608)])
+@pytest.mark.parametrize("use_ue8m0", [True, False])
+def test_silu_mul_quant_matches_oracle(gpu_device, M, Nh, use_ue8m0):
+    x = seeded_bf16((M, 2 * Nh), seed=M + Nh, outlier_frac=1e-3)
+    x[0, :Nh] = 0.0
+    qo, so = oracle.silu_mul_quant(bf16_bits(x), use_ue8m0=use_ue8m0)
+    q, s = _silu_gpu(x.to(gpu_device), use_ue8m0=use_ue8m0)
+    assert np.array_equal(s.cpu().numpy(), so)
+    assert np.array_equal(fp8_codes(q), qo)
+
+
+def test_silu_mul_quant_module(gpu_device):
+    from kb_nano_amd import SiluMulQuantFp8
+    x = seeded_bf16((128, 1024), seed=21, outlier_frac=1e-3).to(gpu_device)
+    out = torch.empty(128, 512, dtype=torch.float8_e4m3fn, device=gpu_device)
+    q, s = SiluMulQuantFp8()(x, output=out)
+    torch.cuda.synchronize()
+    assert q.data_ptr() == out.data_ptr()
+    assert s.shape == (128, 4) and s.stride() == (1, 128)
+    qo, so = oracle.silu_mul_quant(bf16_bits(x))
+    assert np.array_equal(fp8_codes(q), qo) and np.array_equal(s.cpu().numpy(), so)
+    with pytest.raises(AssertionError):
+        SiluMulQuantFp8()(x[:100])   # M % 128 != 0, as the reference asserts
+
+
+def test_silu_mul_quant_cfg2_full(gpu_device):
+    """BASELINE config 2 at full size: [8192, 36864] bf16 with 0.1% x50
+    outliers, checked bit-exact against the oracle on every row."""
+    M, Nh = 8192, 18432
+    x = seeded_bf16((M, 2 * Nh), seed=1, outlier_frac=1e-3)
+    xb = bf16_bits(x)
+    q, s = _silu_gpu(x.to(gpu_device))
+    del x
+    qo, so = oracle.silu_mul_quant(xb)
+    assert np.array_equal(s.cpu().numpy(), so)
+    assert np.array_equal(fp8_codes(q), qo)

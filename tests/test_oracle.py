@@ -1,0 +1,342 @@
+"""Pins the CPU oracle against independent checks (no GPU needed).
+
+Each test compares the oracle with something it does not share code with:
+torch's own fp8 cast and log2/ceil/pow formula (the reference's CPU path,
+tasks/reference/L1/fp8_linear.py:41-64 and bench/kernels/scenario_registry.py:
+54-55, 147-221), 40-digit decimal arithmetic, float64 brute force and closed
+forms.  A plausible slip in the oracle (wrong rounding tie, dropped scale,
+transposed operand, wrong gate/up column) fails at least one of them.
+"""
+import decimal
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+ALL_BF16 = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+
+
+def _bf16_tensor(bits: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(bits.astype(np.int16)).view(torch.bfloat16)
+
+
+def _finite_mask(bits):
+    return (bits & 0x7F80) != 0x7F80
+
+
+# --------------------------------------------------------------------- e4m3
+
+def test_e4m3_encode_exhaustive_vs_torch():
+    bits = ALL_BF16[_finite_mask(ALL_BF16)]
+    x = _bf16_tensor(bits).float()
+    want = x.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    got = oracle.e4m3_encode(x.numpy())
+    # torch keeps the sign on NaN codes; compare NaN-ness for those
+    nan_w = (want & 0x7F) == 0x7F
+    nan_g = (got & 0x7F) == 0x7F
+    assert np.array_equal(nan_w, nan_g)
+    assert np.array_equal(want[~nan_w], got[~nan_w])
+
+
+def test_e4m3_known_answers():
+    # RNE ties, subnormals and saturation boundaries (hand-derived)
+    cases = {1.0625: 0x38, 1.1875: 0x3A, 2.0 ** -10: 0x00, 1.5 * 2.0 ** -9: 0x02,
+             2.0 ** -9: 0x01, 448.0: 0x7E, 464.0: 0x7E, -448.0: 0xFE, 0.0: 0x00,
+             2.0 ** -6: 0x08, 7.5 * 2.0 ** -9: 0x08, 6.5 * 2.0 ** -9: 0x06}
+    for v, code in cases.items():
+        assert oracle.e4m3_encode(np.float32(v)) == code, v
+    assert oracle.e4m3_encode(np.float32(465.0)) & 0x7F == 0x7F
+
+
+def test_e4m3_decode_roundtrip():
+    codes = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], dtype=np.uint8)
+    vals = oracle.e4m3_decode(codes)
+    want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(vals, want)
+    assert np.array_equal(oracle.e4m3_encode(vals), np.where(vals == 0, 0, codes) | (codes & 0x80))
+
+
+def test_fast_encoder_matches_scalar():
+    rng = np.random.default_rng(0)
+    v = np.concatenate([rng.standard_normal(20000).astype(np.float32) * 100,
+                        oracle.e4m3_decode(np.arange(127, dtype=np.uint8)),
+                        (oracle.e4m3_decode(np.arange(126, dtype=np.uint8)) +
+                         oracle.e4m3_decode(np.arange(1, 127, dtype=np.uint8))) / 2])
+    v = np.clip(v, -448, 448).astype(np.float32)
+    assert np.array_equal(oracle._encode_fast(v), oracle.e4m3_encode(v))
+
+
+# -------------------------------------------------------------------- UE8M0
+
+def test_ue8m0_exhaustive_vs_reference_formula():
+    bits = ALL_BF16[(ALL_BF16 < 0x7F80)]          # +0 .. max finite, subnormals included
+    amax = _bf16_tensor(bits).float()
+    ratio = amax.clamp_min(1e-10) / 448.0
+    want = torch.pow(2.0, torch.ceil(torch.log2(ratio))).numpy()
+    got = oracle.ue8m0_from_ratio(ratio.numpy())
+    assert np.array_equal(got, want)
+    # all-zero group: 2^ceil(log2(1e-10/448)) = 2^-42
+    assert oracle.ue8m0_from_ratio(np.float32(np.float32(1e-10) / np.float32(448.0))) == 2.0 ** -42
+
+
+def test_ue8m0_powers_of_two_are_fixed_points():
+    p = np.float32(2.0) ** np.arange(-126, 127, dtype=np.float32)
+    assert np.array_equal(oracle.ue8m0_from_ratio(p), p)
+    assert np.array_equal(oracle.ue8m0_from_ratio(p * np.float32(1.0000001)), p * 2)
+
+
+# --------------------------------------------------------------------- silu
+
+def _silu_decimal(g: float) -> float:
+    with decimal.localcontext() as ctx:
+        ctx.prec = 40
+        d = decimal.Decimal(g)
+        return float(d / (1 + (-d).exp()))
+
+
+def _bf16_round_exact(v_str_decimal) -> int:
+    """Correctly round a Decimal to bf16 bits (independent of the C code)."""
+    d = v_str_decimal
+    if d == 0:
+        return 0x8000 if d.is_signed() else 0
+    sign = 0x8000 if d < 0 else 0
+    a = abs(d)
+    e = a.adjusted()  # rough decimal exponent
+    # binary exponent: find k with 2^k <= a < 2^(k+1)
+    k = int(math.floor(float(a.ln() / decimal.Decimal(2).ln()))) if a > 0 else 0
+    while decimal.Decimal(2) ** k > a:
+        k -= 1
+    while decimal.Decimal(2) ** (k + 1) <= a:
+        k += 1
+    q = max(k - 7, -133)
+    scaled = a / (decimal.Decimal(2) ** q)
+    r = int(scaled.to_integral_value(rounding=decimal.ROUND_HALF_EVEN))
+    v = float(r) * 2.0 ** q
+    if v >= 2.0 ** 128:
+        return sign | 0x7F80
+    return sign | int(np.float32(v).view(np.uint32) >> 16)
+
+
+def test_silu_table_vs_decimal_exhaustive():
+    table = oracle.silu_bf16_table()
+    bits = ALL_BF16[_finite_mask(ALL_BF16)]
+    g = oracle.bf16_bits_to_f32(bits).astype(np.float64)
+    mism = []
+    with decimal.localcontext() as ctx:
+        ctx.prec = 50
+        for b, gv in zip(bits.tolist(), g.tolist()):
+            if gv > 200.0:
+                want = b  # silu(g) = g * (1 - ~e^-200): rounds back to g
+            elif gv < -200.0:
+                want = 0x8000  # |silu| < 1e-84: below half the min bf16 subnormal
+            else:
+                d = decimal.Decimal(gv)
+                want = _bf16_round_exact(d / (1 + (-d).exp()))
+            if int(table[b]) != want:
+                mism.append((b, gv, int(table[b]), want))
+    assert not mism, mism[:10]
+
+
+def test_silu_literal_torch_mismatch_rate_is_small():
+    """Informational pin: the literal fp32 restatement F.silu(g).bf16 differs
+    from the correctly rounded table only near bf16 rounding midpoints."""
+    bits = ALL_BF16[_finite_mask(ALL_BF16)]
+    g = _bf16_tensor(bits).float()
+    lit = torch.nn.functional.silu(g).bfloat16().view(torch.int16).numpy().astype(np.uint16)
+    table = oracle.silu_bf16_table()[bits]
+    rate = np.mean(lit != table)
+    assert rate < 0.01
+
+
+# ------------------------------------------------------------------- quant
+
+def _torch_reference_quant(x_bf16: torch.Tensor, use_ue8m0=True, eps=1e-10):
+    """tasks/reference/L1/fp8_linear.py:41-64 (the reference CPU path)."""
+    info = torch.finfo(torch.float8_e4m3fn)
+    flat = x_bf16.float()
+    M, K = flat.shape
+    grouped = flat.view(M, K // 128, 128)
+    scale = grouped.abs().amax(dim=-1).clamp_min(eps) / info.max
+    if use_ue8m0:
+        scale = torch.pow(2.0, torch.ceil(torch.log2(scale)))
+    expanded = scale.repeat_interleave(128, dim=-1)
+    q = torch.clamp(flat / expanded, info.min, info.max).to(torch.float8_e4m3fn)
+    return q.view(torch.uint8).numpy(), scale.numpy()
+
+
+def _edge_tensor(rows=16):
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(rows, 1024, generator=g)
+    x[0] = 0.0                                    # all-zero groups -> 2^-42
+    x[1, :128] = 448.0 * torch.linspace(-1, 1, 128)
+    x[2, :] = torch.randn(1024, generator=g) * 1e-30   # tiny values, subnormal codes
+    x[3, ::7] *= 50.0                             # outliers
+    x[4, :] = 3.0e38 * torch.sign(torch.randn(1024, generator=g))  # near bf16 max
+    x[5, 128:256] = 1.0
+    x[5, 130] = 448.0 * 2 ** 3                    # amax exactly 448 * 2^k
+    return x.bfloat16()
+
+
+@pytest.mark.parametrize("use_ue8m0", [True, False])
+def test_quant_group128_vs_reference_formula(use_ue8m0):
+    x = torch.cat([_edge_tensor(), torch.randn(48, 1024, generator=torch.Generator().manual_seed(1)).bfloat16()])
+    bits = x.view(torch.int16).numpy().astype(np.uint16)
+    q, s = oracle.quant_group128(bits, use_ue8m0=use_ue8m0)
+    qw, sw = _torch_reference_quant(x, use_ue8m0)
+    assert np.array_equal(s, sw)
+    assert np.array_equal(q, qw)
+
+
+def test_quant_group128_rejects_ragged_k():
+    with pytest.raises(ValueError):
+        oracle.quant_group128(np.zeros((2, 100), dtype=np.uint16))
+
+
+# -------------------------------------------------------------- silu + quant
+
+def test_silu_mul_quant_composition():
+    """y = bf16(silu_bf16(gate) * up) then the reference quant; gate/up split
+    at N/2 (tasks/baseline/L1/silu_mul_quant_fp8.py:51-60)."""
+    g = torch.Generator().manual_seed(3)
+    M, Nh = 32, 512
+    x = torch.randn(M, 2 * Nh, generator=g)
+    x[torch.rand(M, 2 * Nh, generator=g) < 1e-2] *= 50
+    x[0, :Nh] = 0.0
+    xb = x.bfloat16()
+    bits = xb.view(torch.int16).numpy().astype(np.uint16)
+    q, s = oracle.silu_mul_quant(bits)
+    table = oracle.silu_bf16_table()
+    silu = _bf16_tensor(table[bits[:, :Nh]])
+    y = (silu.float() * xb[:, Nh:].float()).bfloat16()   # exact product, one RNE
+    qw, sw = _torch_reference_quant(y)
+    assert np.array_equal(s, sw)
+    assert np.array_equal(q, qw)
+    # swapping gate and up must change the result (catches a swapped split)
+    q2, _ = oracle.silu_mul_quant(np.concatenate([bits[:, Nh:], bits[:, :Nh]], axis=1))
+    assert not np.array_equal(q, q2)
+
+
+# --------------------------------------------------------------------- GEMM
+
+def _rand_fp8(shape, rng, scale=1.0):
+    v = np.clip(rng.standard_normal(shape).astype(np.float32) * scale, -448, 448)
+    return oracle._encode_fast(v)
+
+
+def test_gemm_bruteforce_tiny():
+    rng = np.random.default_rng(5)
+    M, N, K = 3, 130, 256
+    A = _rand_fp8((M, K), rng, 4)
+    W = _rand_fp8((N, K), rng, 4)
+    sA = (2.0 ** rng.integers(-6, 6, (M, K // 128))).astype(np.float32) * np.float32(1.3)
+    sW = (2.0 ** rng.integers(-6, 6, (2, K // 128))).astype(np.float32) * np.float32(0.7)
+    got = oracle.gemm_nt_sample(A, sA, W, sW)
+    a = oracle.e4m3_decode(A).astype(np.float64)
+    w = oracle.e4m3_decode(W).astype(np.float64)
+    for m in range(M):
+        for n in range(N):
+            ref = 0.0
+            for k in range(K):
+                ref += a[m, k] * sA[m, k // 128] * w[n, k] * sW[n // 128, k // 128]
+            assert abs(got[m, n] - ref) <= 1e-9 * max(1.0, abs(ref))
+
+
+def test_gemm_vs_torch_dequant_matmul():
+    """The fp32 dequantize-then-matmul form (tasks/reference/L1/fp8_linear.py:
+    26-38, 96-104, with A dequantized as well)."""
+    g = torch.Generator().manual_seed(0)
+    M, N, K = 64, 384, 1024
+    a = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.02)
+    qa, sa = oracle.quant_group128(a.view(torch.int16).numpy().astype(np.uint16))
+    qw, sw = oracle.quant_block128(w.numpy())
+    got = oracle.gemm_nt_sample(qa, sa, qw, sw)
+    A = torch.from_numpy(qa).view(torch.float8_e4m3fn).float() * torch.from_numpy(sa).repeat_interleave(128, 1)
+    sWx = torch.from_numpy(sw).repeat_interleave(128, 0).repeat_interleave(128, 1)[:N, :K]
+    W = torch.from_numpy(qw).view(torch.float8_e4m3fn).float() * sWx
+    ref = (A.double() @ W.double().T).numpy()
+    assert np.max(np.abs(got - ref)) <= 1e-9 * np.max(np.abs(ref))
+    ref32 = torch.nn.functional.linear(A, W).numpy()
+    assert np.max(np.abs(got - ref32)) / np.max(np.abs(ref)) < 1e-5
+
+
+def test_gemm_special_cases():
+    rng = np.random.default_rng(9)
+    M, N, K = 4, 256, 384
+    A = _rand_fp8((M, K), rng, 8)
+    W = np.zeros((N, K), dtype=np.uint8)
+    # identity-like weight: W[n, n] = 1.0 (code 0x38) inside the first K block
+    for n in range(128):
+        W[n, n] = 0x38
+    sA = np.full((M, K // 128), 0.5, dtype=np.float32)
+    sW = np.full((2, K // 128), 4.0, dtype=np.float32)
+    got = oracle.gemm_nt_sample(A, sA, W, sW)
+    a = oracle.e4m3_decode(A).astype(np.float64)
+    assert np.array_equal(got[:, :128], a[:, :128] * 2.0)
+    assert np.all(got[:, 128:] == 0)
+    # a single non-zero K block picks up only that block's scales
+    W2 = _rand_fp8((N, K), rng, 2)
+    W2[:, :128] = 0
+    W2[:, 256:] = 0
+    sW2 = np.array([[1.0, 8.0, 1e6], [1.0, 0.25, 1e6]], dtype=np.float32)
+    got2 = oracle.gemm_nt_sample(A, sA, W2, sW2)
+    w2 = oracle.e4m3_decode(W2).astype(np.float64)
+    ref = np.empty((M, N))
+    ref[:, :128] = (a[:, 128:256] @ w2[:128, 128:256].T) * 0.5 * 8.0
+    ref[:, 128:] = (a[:, 128:256] @ w2[128:, 128:256].T) * 0.5 * 0.25
+    assert np.allclose(got2, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_gemm_ue8m0_contract_rounds_scales_up():
+    rng = np.random.default_rng(11)
+    A = _rand_fp8((2, 128), rng)
+    W = _rand_fp8((128, 128), rng)
+    sA = np.array([[0.3], [0.25]], dtype=np.float32)
+    sW = np.array([[3.0]], dtype=np.float32)
+    got = oracle.gemm_nt_sample(A, sA, W, sW, ue8m0=True)
+    ref = oracle.gemm_nt_sample(A, np.array([[0.5], [0.25]], np.float32), W, np.array([[4.0]], np.float32))
+    assert np.array_equal(got, ref)
+
+
+def test_grouped_gemm_matches_dense_per_expert():
+    rng = np.random.default_rng(2)
+    E, N, K, M_sum = 3, 256, 256, 512
+    A = _rand_fp8((M_sum, K), rng)
+    sA = (2.0 ** rng.integers(-3, 3, (M_sum, K // 128))).astype(np.float32)
+    B = _rand_fp8((E, N, K), rng)
+    sB = (2.0 ** rng.integers(-3, 3, (E, 2, K // 128))).astype(np.float32)
+    ids = np.repeat(np.array([2, 0, -1, 1], dtype=np.int32), 128)
+    got = oracle.grouped_gemm_nt_sample(A, sA, B, sB, ids)
+    for blk, e in enumerate([2, 0, -1, 1]):
+        sl = slice(blk * 128, (blk + 1) * 128)
+        if e < 0:
+            assert np.all(np.isnan(got[sl]))
+        else:
+            assert np.array_equal(got[sl], oracle.gemm_nt_sample(A[sl], sA[sl], B[e], sB[e]))
+
+
+# ---------------------------------------------------------------- MoE layout
+
+def test_permute_contiguous_layout():
+    rng = np.random.default_rng(0)
+    M, k, E, align = 50, 4, 8, 16
+    topk = np.stack([rng.choice(E, k, replace=False) for _ in range(M)])
+    ids, dest, M_sum = oracle.permute_contiguous(topk, E, align)
+    assert M_sum == oracle.compute_aligned_M(M, k, E, align)
+    assert M_sum % align == 0 and M_sum >= M * k + E * (align - 1)
+    flat = topk.reshape(-1)
+    assert len(set(dest.tolist())) == M * k                  # injective
+    assert np.array_equal(ids[dest], flat.astype(np.int32))  # row carries its expert
+    assert np.sum(ids >= 0) == M * k
+    # segments start on alignment boundaries and keep (token, slot) order
+    for e in range(E):
+        rows_e = dest[flat == e]
+        assert rows_e[0] % align == 0
+        assert np.all(np.diff(rows_e) == 1)
+
+
+def test_compute_aligned_M_cfg4():
+    assert oracle.compute_aligned_M(4096, 8, 256, 128) == 65280
