@@ -36,9 +36,25 @@ def _hipcc() -> str:
     return path
 
 
+def _generate_silu_lut() -> None:
+    """Compile and run gen_silu_lut.cpp (host code) to write the bf16 SiLU
+    table that quant.hip includes."""
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("a host C++ compiler (g++) is needed to generate the SiLU table")
+    gen = os.path.join(OBJ_DIR, "gen_silu_lut")
+    src = os.path.join(CSRC, "gen_silu_lut.cpp")
+    r = subprocess.run([cxx, "-O2", "-std=c++17", "-o", gen, src], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"building {src} failed:\n{r.stderr}")
+    r = subprocess.run([gen, os.path.join(OBJ_DIR, "silu_lut.inc")], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"gen_silu_lut failed:\n{r.stderr}")
+
+
 def _compile(src: str, hipcc: str) -> str:
     obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
-    cmd = [hipcc, *HIPCC_FLAGS, "-I", CSRC, "-c", src, "-o", obj]
+    cmd = [hipcc, *HIPCC_FLAGS, "-I", CSRC, "-I", OBJ_DIR, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
@@ -49,6 +65,7 @@ def build(verbose: bool = False) -> str:
     """Compile all HIP sources and link ``libkbn_fp8.so``; returns its path."""
     hipcc = _hipcc()
     os.makedirs(OBJ_DIR, exist_ok=True)
+    _generate_silu_lut()
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")

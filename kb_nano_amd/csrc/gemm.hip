@@ -42,6 +42,7 @@ struct GemmArgs {
     int64_t lda;
     const float* sA;
     int64_t sA_sm, sA_sk;
+    int64_t sA_bytes;            // byte range of the scale buffer the kernel may read
     const uint8_t* W;            // [N, K] (dense) or [E, N, K] (grouped)
     int64_t ldw;
     int64_t w_estride;           // bytes between experts (grouped)
@@ -55,21 +56,36 @@ struct GemmArgs {
     int tiles_m, tiles_n;
 };
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-    uint32_t n = bytes <= 0 ? 0u : (bytes >= 0xFFFFFFFFLL ? 0xFFFFFFFFu : (uint32_t)bytes);
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, (int)kRsrcWord3);
+// Raw buffer descriptor (base, byte range) built from uniform values so it
+// lives in SGPRs.  Loads past `bytes` return zero.
+__device__ __forceinline__ v4i make_desc(const void* base, int64_t bytes) {
+    const uint64_t p = reinterpret_cast<uint64_t>(base);
+    const uint32_t n = bytes <= 0 ? 0u : (bytes >= 0xFFFFFFFFLL ? 0xFFFFFFFFu : (uint32_t)bytes);
+    v4i r;
+    r[0] = (int)(uint32_t)p;
+    r[1] = (int)((p >> 32) & 0xFFFFu);
+    r[2] = (int)n;
+    r[3] = (int)kRsrcWord3;
+    return r;
 }
 
-// One DMA instruction: 64 lanes x 16 B = 8 rows x 128 B into LDS at `lds`
-// (wave-uniform).  Lane i fills LDS chunk i: row r0 + i/8, slot i%8, which
-// holds global chunk (slot ^ (row & 7)) of that row.
-__device__ __forceinline__ void dma_rows8(__amdgpu_buffer_rsrc_t rsrc, int64_t ld, int r0, int k0, uint8_t* lds,
-                                          int lane) {
-    const int r = r0 + (lane >> 3);
-    const int c = (lane & 7) ^ (r & 7);
-    const int voff = (int)(r * ld) + k0 + c * 16;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+// Direct global->LDS DMA.  Issued as inline asm so the compiler's waitcnt
+// pass does not serialise every LDS read behind the in-flight DMA of the
+// other stage; completion is awaited explicitly (wait_dma) before the
+// barrier that publishes a stage.  Lane i writes LDS bytes
+// [lds + 16*i, lds + 16*i + 16) (dwordx4) or [lds + 4*i, lds + 4*i + 4) (dword).
+__device__ __forceinline__ void dma_b128(const v4i& desc, uint32_t lds, int voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(desc)
+                 : "memory");
 }
+__device__ __forceinline__ void dma_b32(const v4i& desc, uint32_t lds, int voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(desc)
+                 : "memory");
+}
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+constexpr int kOob = (int)0x80000000;  // offset beyond any range: reads zero
 
 // 32 bytes of K (chunks c0, c0+1) of LDS row `r` as one MFMA operand.
 __device__ __forceinline__ v8i lds_frag(const uint8_t* tile, int r, int c0) {
@@ -77,8 +93,6 @@ __device__ __forceinline__ v8i lds_frag(const uint8_t* tile, int r, int c0) {
     const v4i hi = *reinterpret_cast<const v4i*>(tile + r * 128 + (((c0 + 1) ^ (r & 7)) << 4));
     return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
-
-__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // XCD-aware tile order.  Consecutive workgroup ids are dispatched round-robin
 // over the 8 XCDs; give each XCD a contiguous range of the tile sequence so
@@ -100,24 +114,30 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, i
     tn = w / gm;
 }
 
+// LDS stage layout: [A: BM x 128 B][W: BN x 128 B][sA: 256 fp32][sW: 4 x 64 fp32]
+// (one 64-entry weight-scale slot per wavefront, so every wavefront issues the
+// same DMA sequence and the main loop has no wave-dependent branches)
 template <int BM, int BN, int WM, int WN, bool kUe8m0, bool kGrouped>
 __global__ __launch_bounds__(kThreads, 1) void gemm_bs_kernel(const GemmArgs a) {
     constexpr int TM = BM / WM, TN = BN / WN;   // wavefront tile
     constexpr int FM = TM / 32, FN = TN / 32;   // 32x32 fragments per wavefront
     static_assert(WM * WN == 4, "four wavefronts");
     static_assert(FM >= 1 && FN >= 1 && TM % 32 == 0 && TN % 32 == 0, "fragment tiling");
-    static_assert(BM % 32 == 0 && BN % 32 == 0, "DMA covers 8 rows per wave instruction");
+    static_assert(BM % 64 == 0 && BN % 32 == 0 && BM <= 256 && BN <= 8192, "DMA tiling");
     static_assert(128 % TN == 0 || TN % 128 == 0, "wave N tile must not straddle a scale block");
-    constexpr int kStageBytes = (BM + BN) * kBK;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStageBytes];
+    constexpr int kA = BM * kBK, kB = BN * kBK, kSA = 256 * 4, kSW = 4 * 64 * 4;
+    constexpr int kStage = kA + kB + kSA + kSW;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStage];
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)smem);
 
     int tm, tn;
     tile_coords(a.tiles_m, a.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WN, wn = wave % WN;
     const int KB = a.K / kBK;
+    const int NB = (a.N + kGroup - 1) / kGroup;
 
     const uint8_t* Wbase = a.W;
     const float* sWbase = a.sW;
@@ -129,29 +149,46 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bs_kernel(const GemmArgs a) 
         sWbase += (int64_t)expert * a.sW_estride;
     }
 
-    const __amdgpu_buffer_rsrc_t rA = make_rsrc(a.A + (int64_t)m0 * a.lda, (int64_t)(a.M - m0 - 1) * a.lda + a.K);
-    const __amdgpu_buffer_rsrc_t rW = make_rsrc(Wbase + (int64_t)n0 * a.ldw, (int64_t)(a.N - n0 - 1) * a.ldw + a.K);
+    const v4i dA = make_desc(a.A + (int64_t)m0 * a.lda, (int64_t)(a.M - m0 - 1) * a.lda + a.K);
+    const v4i dW = make_desc(Wbase + (int64_t)n0 * a.ldw, (int64_t)(a.N - n0 - 1) * a.ldw + a.K);
+    const v4i dSA = make_desc(a.sA, a.sA_bytes);
+    const v4i dSW = make_desc(sWbase, (int64_t)NB * a.sW_ld * 4);
 
-    auto issue_stage = [&](int kt, int stage) {
-        uint8_t* sa = smem + stage * kStageBytes;
-        uint8_t* sb = sa + BM * kBK;
+    // Per-lane DMA offsets (32-bit; the host checks every range fits) that do
+    // not depend on the K step, so the loop only adds k0 and selects.
+    const int a_lane = (int)((lane >> 3) * a.lda) + (((lane & 7) ^ (lane >> 3)) << 4);
+    const int w_lane = (int)((lane >> 3) * a.ldw) + (((lane & 7) ^ (lane >> 3)) << 4);
+    const int a_wave = (int)(wave * (BM / 32) * 8 * a.lda);
+    const int w_wave = (int)(wave * (BN / 32) * 8 * a.ldw);
+    constexpr int kScaleInstr = BM / 64;                             // 64 scale rows per dword DMA
+    const int sa_row = wave * 64 + lane;
+    const bool sa_live = (wave < kScaleInstr) & (m0 + sa_row < a.M); // rows past BM land in unused slots
+    const int sa_off0 = sa_live ? (int)((int64_t)(m0 + sa_row) * a.sA_sm * 4) : kOob;
+    const int sa_kstep = sa_live ? (int)(a.sA_sk * 4) : 0;
+    const bool sw_live = (lane < (BN + 127) / 128) & (n0 / 128 + lane < NB);
+    const int sw_off0 = sw_live ? (n0 / 128 + lane) * (int)a.sW_ld * 4 : kOob;
+    const int sw_kstep = sw_live ? 4 : 0;
+
+    // Stage kt -> LDS stage st.  `live` false turns every load into an
+    // out-of-range (zero) read, so the caller never branches around it.
+    auto issue_stage = [&](int kt, int st, bool live) {
+        const uint32_t base = lds0 + st * kStage;
         const int k0 = kt * kBK;
 #pragma unroll
         for (int i = 0; i < BM / 32; ++i) {
-            const int r0 = (wave * (BM / 32) + i) * 8;
-            dma_rows8(rA, a.lda, r0, k0, sa + r0 * 128, lane);
+            const int off = a_lane + a_wave + (int)(i * 8 * a.lda) + k0;
+            dma_b128(dA, base + (wave * (BM / 32) + i) * 8 * 128, live ? off : kOob);
         }
 #pragma unroll
         for (int i = 0; i < BN / 32; ++i) {
-            const int r0 = (wave * (BN / 32) + i) * 8;
-            dma_rows8(rW, a.ldw, r0, k0, sb + r0 * 128, lane);
+            const int off = w_lane + w_wave + (int)(i * 8 * a.ldw) + k0;
+            dma_b128(dW, base + kA + (wave * (BN / 32) + i) * 8 * 128, live ? off : kOob);
         }
+        dma_b32(dSA, base + kA + kB + wave * 256, live ? sa_off0 + kt * sa_kstep : kOob);
+        dma_b32(dSW, base + kA + kB + kSA + wave * 256, live ? sw_off0 + kt * sw_kstep : kOob);
     };
 
-    // rows of this lane's A operands and the scale rows they need
-    const int arow_base = wm * TM + (lane & 31);
-    const int ncol_base = n0 + wn * TN;
-    const int64_t sW_row = (int64_t)min(ncol_base / 128, (a.N - 1) / 128) * a.sW_ld;
+    const int nb_local = (wn * TN) / 128;  // this wavefront's weight-scale block within the tile
 
     v16f acc[FM][FN];
 #pragma unroll
@@ -159,96 +196,98 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bs_kernel(const GemmArgs a) 
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = v16f{};
 
-    // per-stage scales
-    float sa_cur[kUe8m0 ? FM : 1];
-    float sw_cur = 0.f;
-    auto load_scales_ue8m0 = [&](int kt, float (&sa)[kUe8m0 ? FM : 1], float& sw) {
+    v8i fa0[FM], fb0[FN], fa1[FM], fb1[FN];
+    int ea[FM];
+    int eb = 0;
+    float sa_row_scale[kUe8m0 ? 1 : FM][kUe8m0 ? 1 : 16];
+    float swv = 0.f;
+
+    auto read_frags = [&](const uint8_t* st, int ks, v8i (&af)[FM], v8i (&bf)[FN]) {
+        const int c0 = ks * 4 + (lane >> 5) * 2;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) af[i] = lds_frag(st, wm * TM + i * 32 + (lane & 31), c0);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) bf[j] = lds_frag(st + kA, wn * TN + j * 32 + (lane & 31), c0);
+    };
+    auto read_scales = [&](const uint8_t* st) {
+        const float* ssa = reinterpret_cast<const float*>(st + kA + kB);
+        const float* ssw = reinterpret_cast<const float*>(st + kA + kB + kSA + wave * 256);
         if constexpr (kUe8m0) {
 #pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                const int m = min(m0 + arow_base + i * 32, a.M - 1);
-                sa[i] = a.sA[(int64_t)m * a.sA_sm + (int64_t)kt * a.sA_sk];
-            }
-            sw = sWbase[sW_row + kt];
+            for (int i = 0; i < FM; ++i) ea[i] = ue8m0_ceil_byte(ssa[wm * TM + i * 32 + (lane & 31)]);
+            eb = ue8m0_ceil_byte(ssw[nb_local]);
+        } else {
+            // output row of accumulator register r: 8*(r/4) + 4*(lane/32) + r%4
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    sa_row_scale[i][r] = ssa[wm * TM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)];
+            swv = ssw[nb_local];
         }
     };
+    auto mfma_step = [&](v8i (&af)[FM], v8i (&bf)[FN], v16f (&c)[FM][FN], bool fresh) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                if constexpr (kUe8m0)
+                    c[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf[j], c[i][j], 0, 0, 0, ea[i],
+                                                                              0, eb);
+                else
+                    c[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf[j], fresh ? v16f{} : c[i][j],
+                                                                              0, 0, 0, 0, 0, 0);
+            }
+    };
 
-    issue_stage(0, 0);
-    load_scales_ue8m0(0, sa_cur, sw_cur);
+    // prologue: stages 0 and 1 in flight, wait for both, fragments of step 0
+    issue_stage(0, 0, true);
+    issue_stage(1, 1, KB > 1);
+    wait_dma();
+    __syncthreads();
+    read_frags(smem, 0, fa0, fb0);
+    read_scales(smem);
 
+    v16f part[kUe8m0 ? 1 : FM][kUe8m0 ? 1 : FN];
     for (int kt = 0; kt < KB; ++kt) {
-        wait_vmem();
-        __syncthreads();
-        float sa_nxt[kUe8m0 ? FM : 1];
-        float sw_nxt = 0.f;
-        if (kt + 1 < KB) {
-            issue_stage(kt + 1, (kt + 1) & 1);
-            load_scales_ue8m0(kt + 1, sa_nxt, sw_nxt);
-        }
-        const uint8_t* ta = smem + (kt & 1) * kStageBytes;
-        const uint8_t* tb = ta + BM * kBK;
-
+        const uint8_t* cur = smem + (kt & 1) * kStage;
+        const uint8_t* nxt = smem + ((kt + 1) & 1) * kStage;
+        // first half of the K step on fragments read earlier
         if constexpr (kUe8m0) {
-            int ea[FM];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) ea[i] = ue8m0_ceil_byte(sa_cur[i]);
-            const int eb = ue8m0_ceil_byte(sw_cur);
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const int c0 = ks * 4 + (lane >> 5) * 2;
-                v8i af[FM], bf[FN];
-#pragma unroll
-                for (int i = 0; i < FM; ++i) af[i] = lds_frag(ta, wm * TM + i * 32 + (lane & 31), c0);
-#pragma unroll
-                for (int j = 0; j < FN; ++j) bf[j] = lds_frag(tb, wn * TN + j * 32 + (lane & 31), c0);
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf[j], acc[i][j], 0, 0, 0,
-                                                                                   ea[i], 0, eb);
-            }
+            mfma_step(fa0, fb0, acc, false);
         } else {
-            v16f part[FM][FN];
+            mfma_step(fa0, fb0, part, true);
+        }
+        read_frags(cur, 1, fa1, fb1);
+        if constexpr (kUe8m0) {
+            mfma_step(fa1, fb1, acc, false);
+        } else {
+            mfma_step(fa1, fb1, part, false);
+            // promotion: acc += part * sA[row] * sW[block]
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const int c0 = ks * 4 + (lane >> 5) * 2;
-                v8i af[FM], bf[FN];
-#pragma unroll
-                for (int i = 0; i < FM; ++i) af[i] = lds_frag(ta, wm * TM + i * 32 + (lane & 31), c0);
-#pragma unroll
-                for (int j = 0; j < FN; ++j) bf[j] = lds_frag(tb, wn * TN + j * 32 + (lane & 31), c0);
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-                        part[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                            af[i], bf[j], ks == 0 ? v16f{} : part[i][j], 0, 0, 0, 0, 0, 0);
-            }
-            // promotion: acc += part * sA[row] * sW[block]; output row of
-            // register r is 8*(r/4) + 4*(lane/32) + r%4 within the fragment
-            const float sw = sWbase[sW_row + kt];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
+            for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int m = min(m0 + wm * TM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), a.M - 1);
-                    const float f = a.sA[(int64_t)m * a.sA_sm + (int64_t)kt * a.sA_sk] * sw;
+                    const float f = sa_row_scale[i][r] * swv;
 #pragma unroll
                     for (int j = 0; j < FN; ++j) acc[i][j][r] = fmaf(part[i][j][r], f, acc[i][j][r]);
                 }
-            }
         }
-        if constexpr (kUe8m0) {
-            if (kt + 1 < KB) {
-#pragma unroll
-                for (int i = 0; i < FM; ++i) sa_cur[i] = sa_nxt[i];
-                sw_cur = sw_nxt;
-            }
-        }
+        // The MFMAs above keep the matrix pipe busy across this barrier.  It
+        // publishes stage kt+1 and frees stage kt for the DMA of kt+2; the
+        // last iteration's extra barrier/read is harmless.
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lds();
+        wait_dma();
+        __syncthreads();
+        issue_stage(kt + 2, kt & 1, kt + 2 < KB);
+        read_frags(nxt, 0, fa0, fb0);
+        read_scales(nxt);
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     // epilogue: fp32 -> bf16 (RNE), masked 2-byte stores
+    const int ncol_base = n0 + wn * TN;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -298,6 +337,21 @@ static int check_common(const char* what, const void* A, int64_t lda, const void
     return 0;
 }
 
+// Bytes spanned by a [rows, kb] fp32 scale view with the given strides.
+static int64_t scale_bytes(int64_t rows, int64_t kb, int64_t sm, int64_t sk) {
+    if (rows <= 0 || kb <= 0) return 0;
+    return ((rows - 1) * sm + (kb - 1) * sk + 1) * 4;
+}
+
+// The kernels address scales with 32-bit byte offsets from the buffer base.
+static int check_scale_ranges(const char* what, int64_t M, int64_t K, int64_t sm, int64_t sk, int64_t nb,
+                              int64_t sw_ld) {
+    KBN_CHECK_ARG(sm >= 0 && sk >= 0, "%s: negative activation-scale stride", what);
+    KBN_CHECK_ARG(scale_bytes(M, K / kGroup, sm, sk) < 0x7FFFFFFFLL, "%s: activation scales span >= 2 GiB", what);
+    KBN_CHECK_ARG(nb * sw_ld * 4 < 0x7FFFFFFFLL, "%s: weight scales span >= 2 GiB", what);
+    return 0;
+}
+
 extern "C" int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
                                int64_t sA_stride_k, const void* W, int64_t ldw, const float* sW, int64_t sW_ld,
                                void* D_bf16, int64_t ldd, int64_t M, int64_t N, int64_t K, int scale_ue8m0,
@@ -310,7 +364,10 @@ extern "C" int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int6
     KBN_CHECK_ARG(sW_ld >= K / kGroup, "%s: weight-scale row stride %lld < K/128", what, (long long)sW_ld);
     GemmArgs a{};
     a.A = (const uint8_t*)A; a.lda = lda;
+    if (int rc = check_scale_ranges(what, M, K, sA_stride_m, sA_stride_k, (N + kGroup - 1) / kGroup, sW_ld))
+        return rc;
     a.sA = sA; a.sA_sm = sA_stride_m; a.sA_sk = sA_stride_k;
+    a.sA_bytes = scale_bytes(M, K / kGroup, sA_stride_m, sA_stride_k);
     a.W = (const uint8_t*)W; a.ldw = ldw; a.w_estride = 0;
     a.sW = sW; a.sW_ld = sW_ld; a.sW_estride = 0;
     a.D = (uint16_t*)D_bf16; a.ldd = ldd;
@@ -321,7 +378,6 @@ extern "C" int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int6
         if (M > 128) return launch_gemm<256, 256, 2, 2, true, false>(a, st, what);
         return launch_gemm<128, 128, 2, 2, true, false>(a, st, what);
     }
-    if (M > 128) return launch_gemm<256, 128, 2, 2, false, false>(a, st, what);
     return launch_gemm<128, 128, 2, 2, false, false>(a, st, what);
 }
 
@@ -339,7 +395,9 @@ extern "C" int kbn_fp8_grouped_gemm_nt_contiguous(const void* A, int64_t lda, co
     const int64_t NB = (N + kGroup - 1) / kGroup, KB = K / kGroup;
     GemmArgs a{};
     a.A = (const uint8_t*)A; a.lda = lda;
+    if (int rc = check_scale_ranges(what, M_sum, K, sA_stride_m, sA_stride_k, NB, KB)) return rc;
     a.sA = sA; a.sA_sm = sA_stride_m; a.sA_sk = sA_stride_k;
+    a.sA_bytes = scale_bytes(M_sum, KB, sA_stride_m, sA_stride_k);
     a.W = (const uint8_t*)B; a.ldw = K; a.w_estride = N * K;
     a.sW = sB; a.sW_ld = KB; a.sW_estride = NB * KB;
     a.D = (uint16_t*)C_bf16; a.ldd = ldc;

@@ -137,6 +137,10 @@ def _silu_gpu(inp, col_major=True, use_ue8m0=True):
 def test_silu_mul_quant_matches_oracle(gpu_device, M, Nh, use_ue8m0):
     x = seeded_bf16((M, 2 * Nh), seed=M + Nh, outlier_frac=1e-3)
     x[0, :Nh] = 0.0
+    # tiny gate and up values: fp32-subnormal products must round like IEEE
+    x[1] = (x[1].float() * 1e-19).bfloat16()
+    if M > 2:
+        x[2, Nh:] = (x[2, Nh:].float() * 3e-38).bfloat16()
     qo, so = oracle.silu_mul_quant(bf16_bits(x), use_ue8m0=use_ue8m0)
     q, s = _silu_gpu(x.to(gpu_device), use_ue8m0=use_ue8m0)
     assert np.array_equal(s.cpu().numpy(), so)
