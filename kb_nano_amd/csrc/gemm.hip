@@ -87,10 +87,16 @@ __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)"
 
 constexpr int kOob = (int)0x80000000;  // offset beyond any range: reads zero
 
+// LDS swizzle of a 128-B row: 16-B chunk c of row r lives in slot
+// c ^ ((r >> 1) & 7).  A ds_read_b128 is served 16 lanes (256 B, all 64
+// banks) per cycle; 16 consecutive rows alternate bank halves by row parity
+// and take 8 distinct slots by (r >> 1), so they never share a bank.
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+
 // 32 bytes of K (chunks c0, c0+1) of LDS row `r` as one MFMA operand.
 __device__ __forceinline__ v8i lds_frag(const uint8_t* tile, int r, int c0) {
-    const v4i lo = *reinterpret_cast<const v4i*>(tile + r * 128 + ((c0 ^ (r & 7)) << 4));
-    const v4i hi = *reinterpret_cast<const v4i*>(tile + r * 128 + (((c0 + 1) ^ (r & 7)) << 4));
+    const v4i lo = *reinterpret_cast<const v4i*>(tile + r * 128 + ((c0 ^ swz(r)) << 4));
+    const v4i hi = *reinterpret_cast<const v4i*>(tile + r * 128 + (((c0 + 1) ^ swz(r)) << 4));
     return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
@@ -156,8 +162,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bs_kernel(const GemmArgs a) 
 
     // Per-lane DMA offsets (32-bit; the host checks every range fits) that do
     // not depend on the K step, so the loop only adds k0 and selects.
-    const int a_lane = (int)((lane >> 3) * a.lda) + (((lane & 7) ^ (lane >> 3)) << 4);
-    const int w_lane = (int)((lane >> 3) * a.ldw) + (((lane & 7) ^ (lane >> 3)) << 4);
+    // lane -> (row r0 + lane/8, LDS slot lane%8) holds global chunk slot ^ swz(row);
+    // r0 is a multiple of 8, so swz(row) = swz(r0) ^ ... is folded per instruction below
+    const int a_row = lane >> 3;
+    // The 8-row group index (wave * rows/32 + i) is even or odd with i, so two
+    // per-lane offsets cover every DMA instruction: swz(row) = (4*(group&1) + row/2) & 7.
+    const int chunk0 = ((lane & 7) ^ swz(a_row)) << 4;
+    const int chunk1 = ((lane & 7) ^ swz(a_row + 8)) << 4;
+    const int a_lane0 = (int)(a_row * a.lda) + chunk0, a_lane1 = (int)(a_row * a.lda) + chunk1;
+    const int w_lane0 = (int)(a_row * a.ldw) + chunk0, w_lane1 = (int)(a_row * a.ldw) + chunk1;
+    static_assert((BM / 32) % 2 == 0 && (BN / 32) % 2 == 0, "each wave's first 8-row group is even");
     const int a_wave = (int)(wave * (BM / 32) * 8 * a.lda);
     const int w_wave = (int)(wave * (BN / 32) * 8 * a.ldw);
     constexpr int kScaleInstr = BM / 64;                             // 64 scale rows per dword DMA
@@ -176,12 +190,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bs_kernel(const GemmArgs a) 
         const int k0 = kt * kBK;
 #pragma unroll
         for (int i = 0; i < BM / 32; ++i) {
-            const int off = a_lane + a_wave + (int)(i * 8 * a.lda) + k0;
+            const int off = (i & 1 ? a_lane1 : a_lane0) + a_wave + (int)(i * 8 * a.lda) + k0;
             dma_b128(dA, base + (wave * (BM / 32) + i) * 8 * 128, live ? off : kOob);
         }
 #pragma unroll
         for (int i = 0; i < BN / 32; ++i) {
-            const int off = w_lane + w_wave + (int)(i * 8 * a.ldw) + k0;
+            const int off = (i & 1 ? w_lane1 : w_lane0) + w_wave + (int)(i * 8 * a.ldw) + k0;
             dma_b128(dW, base + kA + (wave * (BN / 32) + i) * 8 * 128, live ? off : kOob);
         }
         dma_b32(dSA, base + kA + kB + wave * 256, live ? sa_off0 + kt * sa_kstep : kOob);

@@ -1,14 +1,17 @@
 // Per-token-group (1x128) FP8 quantization and the fused SiLU*Mul + FP8
 // quantization, as persistent gfx950 bandwidth kernels.
 //
-// Work decomposition (both kernels): a 1x128 group is owned by 16 lanes of a
-// wavefront, 8 elements (16 bytes of bf16) per lane; one wavefront covers 4
-// groups per pass and every lane carries kUnroll groups, all loads issued
-// before any arithmetic.  The grid is sized to the CU count and each
-// workgroup strides over the flattened (row, group) space; the (row, group)
-// position advances by a precomputed quotient/remainder, so there is no
-// per-group integer division.  The absmax of a group is a 4-step DPP max over
-// its 16-lane row; codes leave as one 8-byte non-temporal store per lane.
+// Work decomposition (both ops, one kernel template): a 1x128 group is owned
+// by 16 lanes of a wavefront, 8 elements (16 bytes of bf16) per lane.  The
+// grid is sized to the CU count.  Each of the 8 XCDs owns a contiguous slice
+// of rows (a multiple of 32, so every 128-B line of column-major scales is
+// written through a single L2), and the XCD's workgroups walk its slice in
+// flattened (row, group) order: one pass covers a contiguous range, each
+// wavefront loading kUnroll consecutive 1 KB blocks (4 groups) per operand
+// before any arithmetic; positions advance by a precomputed quotient and
+// remainder, so there is no per-group division.  The absmax of a group is a
+// 4-step DPP max over its 16-lane row; codes leave as one 8-byte
+// non-temporal store per lane.
 //
 // Numerics follow tasks/baseline/L1/fp8_linear.py:195-215 and
 // tasks/baseline/L1/silu_mul_quant_fp8.py:51-76:
@@ -37,11 +40,30 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kUnroll = 4;           // groups per lane per pass
-constexpr int kQuantThreads = 512;
-constexpr int kSiluThreads = 1024;   // one workgroup per CU (the table fills 128 KB of LDS)
+// Launch shape (tunable at build time; defaults are the measured best on MI355X).
+#ifndef KBN_QUANT_PER_CU
+#define KBN_QUANT_PER_CU 2
+#endif
+constexpr int kThreads = 1024;       // 16 wavefronts
+constexpr int kUnroll = 2;           // 4-group blocks per wavefront per pass
+constexpr int kXcds = 8;             // MI355X: workgroups are dealt round-robin to 8 XCDs
+constexpr int kLineRows = 32;        // rows sharing one 128-B line of column-major scales
 
-// Position of a lane's group in the flattened (row, group) space.
+struct QuantArgs {
+    const uint16_t* x;      // bf16 input rows
+    int64_t ld_x;           // row stride (elements)
+    int64_t up_off;         // SiLU kernel: column offset of the up half
+    uint8_t* q;
+    int64_t ld_q;
+    float* s;
+    int64_t s_sm, s_sg;
+    int M, G;
+    int rows_per_xcd;       // contiguous rows owned by one XCD (multiple of kLineRows)
+    int step_q, step_r;     // per-pass stride inside an XCD's rows, as (rows, groups)
+    float eps;
+};
+
+// Position of a lane's group in the (row, group) space.
 struct GroupCursor {
     int row, g;
     __device__ __forceinline__ void advance(int q, int r, int G) {
@@ -52,11 +74,31 @@ struct GroupCursor {
             row += 1;
         }
     }
+    __device__ __forceinline__ void step4(int G) {  // next block of 4 groups
+        g += 4;
+        while (g >= G) {
+            g -= G;
+            row += 1;
+        }
+    }
 };
 
+// bf16(silu(g)) * up for the two bf16 values of each word, rounded to bf16
+// by v_cvt_pk_bf16_f32 and widened back to fp32.
+__device__ __forceinline__ void silu_mul_pair(const uint16_t* __restrict__ lut, uint32_t gw, uint32_t uw, float& y0,
+                                              float& y1) {
+    const float s0 = __uint_as_float((uint32_t)lut[gw & 0xFFFFu] << 16);
+    const float s1 = __uint_as_float((uint32_t)lut[gw >> 16] << 16);
+    const bf16x2 p = __builtin_convertvector((f32x2{s0 * bf16lo(uw), s1 * bf16hi(uw)}), bf16x2);
+    const uint32_t pw = __builtin_bit_cast(uint32_t, p);
+    y0 = bf16lo(pw);
+    y1 = bf16hi(pw);
+}
+
+// Quantize 8 values owned by this lane (16 lanes per group); returns the
+// group scale (valid in every lane of the group).
 template <bool kUe8m0>
-__device__ __forceinline__ void quant8_store(const float (&v)[8], float eps, int sub, uint8_t* __restrict__ qptr,
-                                             float* __restrict__ sptr) {
+__device__ __forceinline__ float quant8_store(const float (&v)[8], float eps, int sub, uint8_t* __restrict__ qptr) {
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -74,101 +116,63 @@ __device__ __forceinline__ void quant8_store(const float (&v)[8], float eps, int
         hi = pack4_e4m3(clamp_fp8(v[4] / sc), clamp_fp8(v[5] / sc), clamp_fp8(v[6] / sc), clamp_fp8(v[7] / sc));
     }
     __builtin_nontemporal_store(u32x2{lo, hi}, reinterpret_cast<u32x2*>(qptr + sub * 8));
-    if (sub == 0) *sptr = sc;
+    return sc;
 }
 
-struct QuantArgs {
-    const uint16_t* x;      // bf16 input rows
-    int64_t ld_x;           // row stride (elements)
-    int64_t up_off;         // SiLU kernel: column offset of the up half
-    uint8_t* q;
-    int64_t ld_q;
-    float* s;
-    int64_t s_sm, s_sg;
-    int M, G;
-    int step_q, step_r;     // stride over the flattened group space as (rows, groups)
-    float eps;
-};
-
-template <bool kUe8m0>
-__global__ __launch_bounds__(kQuantThreads) void quant_group128_kernel(const QuantArgs a) {
-    const int sub = threadIdx.x & 15;
-    constexpr int kSlots = kQuantThreads / 16;
-    const int64_t gid0 = (int64_t)blockIdx.x * kSlots + (threadIdx.x >> 4);
-    GroupCursor c{(int)(gid0 / a.G), (int)(gid0 % a.G)};
-    while (c.row < a.M) {
-        u32x4 raw[kUnroll];
-        GroupCursor cu[kUnroll];
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            cu[u] = c;
-            if (c.row < a.M)
-                raw[u] = __builtin_nontemporal_load(
-                    reinterpret_cast<const u32x4*>(a.x + (int64_t)c.row * a.ld_x + c.g * kGroup + sub * 8));
-            c.advance(a.step_q, a.step_r, a.G);
-        }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            if (cu[u].row >= a.M) break;  // uniform over the group's 16 lanes
-            const float v[8] = {bf16lo(raw[u].x), bf16hi(raw[u].x), bf16lo(raw[u].y), bf16hi(raw[u].y),
-                                bf16lo(raw[u].z), bf16hi(raw[u].z), bf16lo(raw[u].w), bf16hi(raw[u].w)};
-            quant8_store<kUe8m0>(v, a.eps, sub, a.q + (int64_t)cu[u].row * a.ld_q + cu[u].g * kGroup,
-                                 a.s + (int64_t)cu[u].row * a.s_sm + (int64_t)cu[u].g * a.s_sg);
-        }
-    }
-}
-
-// bf16(silu(g)) * up for the two bf16 values of each word, rounded to bf16
-// by v_cvt_pk_bf16_f32 and widened back to fp32.
-__device__ __forceinline__ void silu_mul_pair(const uint16_t* __restrict__ lut, uint32_t gw, uint32_t uw, float& y0,
-                                              float& y1) {
-    const float s0 = __uint_as_float((uint32_t)lut[gw & 0xFFFFu] << 16);
-    const float s1 = __uint_as_float((uint32_t)lut[gw >> 16] << 16);
-    const bf16x2 p = __builtin_convertvector((f32x2{s0 * bf16lo(uw), s1 * bf16hi(uw)}), bf16x2);
-    const uint32_t pw = __builtin_bit_cast(uint32_t, p);
-    y0 = bf16lo(pw);
-    y1 = bf16hi(pw);
-}
-
-template <bool kUe8m0>
-__global__ __launch_bounds__(kSiluThreads) void silu_mul_quant_kernel(const QuantArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t lut[65536];
-    const int sub = threadIdx.x & 15;
-    constexpr int kSlots = kSiluThreads / 16;
-    const int64_t gid0 = (int64_t)blockIdx.x * kSlots + (threadIdx.x >> 4);
-    GroupCursor c{(int)(gid0 / a.G), (int)(gid0 % a.G)};
-
-    {  // stage the table: 8192 x 16 B
+// One persistent kernel for both ops.  Each XCD owns a contiguous slice of
+// rows (a multiple of 32, so every 128-B line of column-major scales is
+// written through one L2 and merges there); inside the slice the XCD's
+// workgroups walk the flattened (row, group) space so that one pass covers a
+// contiguous range, each wavefront reading kUnroll consecutive blocks of 4
+// groups (1 KB of bf16 per operand and block) before any arithmetic.
+template <bool kSilu, bool kUe8m0>
+__global__ __launch_bounds__(kThreads) void group_quant_kernel(const QuantArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t lut[kSilu ? 65536 : 8];
+    if constexpr (kSilu) {  // stage the bf16 SiLU table: 8192 x 16 B
         const u32x4* src = reinterpret_cast<const u32x4*>(kSiluLut);
         u32x4* dst = reinterpret_cast<u32x4*>(lut);
 #pragma unroll
-        for (int i = 0; i < 8192 / kSiluThreads; ++i) dst[threadIdx.x + i * kSiluThreads] = src[threadIdx.x + i * kSiluThreads];
+        for (int i = 0; i < 8192 / kThreads; ++i) dst[threadIdx.x + i * kThreads] = src[threadIdx.x + i * kThreads];
+        __syncthreads();
     }
-    __syncthreads();
-
-    while (c.row < a.M) {
-        u32x4 graw[kUnroll], uraw[kUnroll];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane & 15;
+    const int xcd = blockIdx.x % kXcds, local = blockIdx.x / kXcds;
+    const int row_begin = xcd * a.rows_per_xcd;
+    const int row_end = min(a.M, row_begin + a.rows_per_xcd);
+    const int64_t t0 = ((int64_t)local * (kThreads / 64) + wave) * (4 * kUnroll) + (lane >> 4);
+    GroupCursor c{row_begin + (int)(t0 / a.G), (int)(t0 % a.G)};
+    while (c.row < row_end) {
         GroupCursor cu[kUnroll];
+        cu[0] = c;
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            cu[u] = c;
-            if (c.row < a.M) {
-                const uint16_t* p = a.x + (int64_t)c.row * a.ld_x + c.g * kGroup + sub * 8;
-                graw[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-                uraw[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + a.up_off));
-            }
-            c.advance(a.step_q, a.step_r, a.G);
+        for (int u = 1; u < kUnroll; ++u) {
+            cu[u] = cu[u - 1];
+            cu[u].step4(a.G);
         }
+        u32x4 xa[kUnroll], xb[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u)
+            if (cu[u].row < row_end) {
+                const uint16_t* p = a.x + (int64_t)cu[u].row * a.ld_x + (int64_t)cu[u].g * kGroup + sub * 8;
+                xa[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+                if constexpr (kSilu) xb[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + a.up_off));
+            }
+        c.advance(a.step_q, a.step_r, a.G);
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            if (cu[u].row >= a.M) break;
+            if (cu[u].row >= row_end) break;  // uniform over the group's 16 lanes; rows grow with u
             float v[8];
-            silu_mul_pair(lut, graw[u].x, uraw[u].x, v[0], v[1]);
-            silu_mul_pair(lut, graw[u].y, uraw[u].y, v[2], v[3]);
-            silu_mul_pair(lut, graw[u].z, uraw[u].z, v[4], v[5]);
-            silu_mul_pair(lut, graw[u].w, uraw[u].w, v[6], v[7]);
-            quant8_store<kUe8m0>(v, a.eps, sub, a.q + (int64_t)cu[u].row * a.ld_q + cu[u].g * kGroup,
-                                 a.s + (int64_t)cu[u].row * a.s_sm + (int64_t)cu[u].g * a.s_sg);
+            if constexpr (kSilu) {
+                silu_mul_pair(lut, xa[u].x, xb[u].x, v[0], v[1]);
+                silu_mul_pair(lut, xa[u].y, xb[u].y, v[2], v[3]);
+                silu_mul_pair(lut, xa[u].z, xb[u].z, v[4], v[5]);
+                silu_mul_pair(lut, xa[u].w, xb[u].w, v[6], v[7]);
+            } else {
+                v[0] = bf16lo(xa[u].x); v[1] = bf16hi(xa[u].x); v[2] = bf16lo(xa[u].y); v[3] = bf16hi(xa[u].y);
+                v[4] = bf16lo(xa[u].z); v[5] = bf16hi(xa[u].z); v[6] = bf16lo(xa[u].w); v[7] = bf16hi(xa[u].w);
+            }
+            const float sc = quant8_store<kUe8m0>(v, a.eps, sub, a.q + (int64_t)cu[u].row * a.ld_q + (int64_t)cu[u].g * kGroup);
+            if (sub == 0) a.s[(int64_t)cu[u].row * a.s_sm + (int64_t)cu[u].g * a.s_sg] = sc;
         }
     }
 }
@@ -191,18 +195,18 @@ static int cu_count() {
     return cache[dev];
 }
 
-// Grid over the flattened group space: at most `per_cu` workgroups per CU,
-// never more than the work needs.
-static int plan(QuantArgs& a, int threads, int per_cu) {
-    const int64_t total = (int64_t)a.M * a.G;
-    const int slots = threads / 16;
-    const int64_t need = (total + (int64_t)slots * kUnroll - 1) / ((int64_t)slots * kUnroll);
-    int blocks = (int)std::min<int64_t>(need, (int64_t)cu_count() * per_cu);
-    if (blocks < 1) blocks = 1;
-    const int64_t stride = (int64_t)blocks * slots;
+// Row slices per XCD (multiples of 32 rows) and the number of workgroups
+// per XCD: at most `per_cu` per CU, never more than the slice needs.
+static int plan(QuantArgs& a, int per_cu) {
+    const int slice = (a.M + kXcds - 1) / kXcds;
+    a.rows_per_xcd = (slice + kLineRows - 1) / kLineRows * kLineRows;
+    const int64_t per_block = (int64_t)(kThreads / 64) * 4 * kUnroll;  // groups per workgroup pass
+    const int64_t need = ((int64_t)a.rows_per_xcd * a.G + per_block - 1) / per_block;
+    const int per_xcd = (int)std::max<int64_t>(1, std::min<int64_t>(need, (int64_t)cu_count() / kXcds * per_cu));
+    const int64_t stride = (int64_t)per_xcd * per_block;
     a.step_q = (int)(stride / a.G);
     a.step_r = (int)(stride % a.G);
-    return blocks;
+    return per_xcd * kXcds;
 }
 
 }  // namespace kbn
@@ -232,13 +236,13 @@ extern "C" int kbn_per_token_group_quant_fp8(const void* x_bf16, int64_t M, int6
     if (M == 0 || K == 0) return 0;
     KBN_CHECK_ARG(ld_x >= K, "%s: input row stride smaller than K", what);
     QuantArgs a{(const uint16_t*)x_bf16, ld_x, 0, (uint8_t*)q_fp8, ld_q, scale, s_stride_m, s_stride_g,
-                (int)M, (int)(K / kGroup), 0, 0, eps};
-    const int blocks = plan(a, kQuantThreads, 4);
+                (int)M, (int)(K / kGroup), 0, 0, 0, eps};
+    const int blocks = plan(a, KBN_QUANT_PER_CU);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (use_ue8m0)
-        quant_group128_kernel<true><<<blocks, kQuantThreads, 0, st>>>(a);
+        group_quant_kernel<false, true><<<blocks, kThreads, 0, st>>>(a);
     else
-        quant_group128_kernel<false><<<blocks, kQuantThreads, 0, st>>>(a);
+        group_quant_kernel<false, false><<<blocks, kThreads, 0, st>>>(a);
     KBN_CHECK_LAUNCH(what);
     return 0;
 }
@@ -251,13 +255,13 @@ extern "C" int kbn_silu_mul_quant_fp8(const void* in_bf16, int64_t M, int64_t N_
     if (M == 0 || N_half == 0) return 0;
     KBN_CHECK_ARG(ld_in >= 2 * N_half, "%s: input row stride smaller than 2*N/2", what);
     QuantArgs a{(const uint16_t*)in_bf16, ld_in, N_half, (uint8_t*)q_fp8, ld_q, scale, s_stride_m, s_stride_g,
-                (int)M, (int)(N_half / kGroup), 0, 0, eps};
-    const int blocks = plan(a, kSiluThreads, 1);
+                (int)M, (int)(N_half / kGroup), 0, 0, 0, eps};
+    const int blocks = plan(a, 1);  // the LDS table allows one workgroup per CU
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (use_ue8m0)
-        silu_mul_quant_kernel<true><<<blocks, kSiluThreads, 0, st>>>(a);
+        group_quant_kernel<true, true><<<blocks, kThreads, 0, st>>>(a);
     else
-        silu_mul_quant_kernel<false><<<blocks, kSiluThreads, 0, st>>>(a);
+        group_quant_kernel<true, false><<<blocks, kThreads, 0, st>>>(a);
     KBN_CHECK_LAUNCH(what);
     return 0;
 }
