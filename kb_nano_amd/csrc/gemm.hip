@@ -17,12 +17,12 @@
 //    running sum with one FMA per element and stage.
 //
 // Dataflow per workgroup (256 lanes = 4 wavefronts, one per SIMD):
-//   HBM --buffer_load_dwordx4 ... lds (direct DMA)--> LDS (2 stages x (BM+BN) x 128 B)
+//   HBM --buffer_load_dwordx4 ... lds (direct DMA)--> LDS (4 stages x (BM+BN) x 64 B)
 //   LDS --ds_read_b128--> VGPR fragments --MFMA 32x32x64--> fp32 accumulators
-// Each LDS row is 128 B (one 128-K stage); its eight 16-B chunks are XOR-
-// swizzled by (row & 7) so the 32 rows read by one ds_read_b128 hit distinct
-// banks.  The swizzle is applied on the global side of the DMA (lane i of a
-// load instruction always writes LDS chunk i), so no extra LDS pass is needed.
+// Each LDS row is 64 B (one 64-K stage); its four 16-B chunks are XOR-
+// swizzled so the rows read by one ds_read_b128 hit distinct banks.  The
+// swizzle is applied on the global side of the DMA (lane i of a load
+// instruction always writes LDS chunk i), so no extra LDS pass is needed.
 // Out-of-range rows read as zero through the buffer descriptor's range check.
 
 #include "kbn_common.h"
@@ -34,7 +34,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int kBK = 128;           // K per stage == scale block
-constexpr int kThreads = 256;      // 4 wavefronts
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit dword format (gfx9 family)
 
 struct GemmArgs {
@@ -83,20 +82,28 @@ __device__ __forceinline__ void dma_b32(const v4i& desc, uint32_t lds, int voff)
                  : "memory");
 }
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Wait until at most N vector-memory loads of this wavefront are outstanding
+// (loads complete in issue order, so everything older than the last N has landed).
+template <int N>
+__device__ __forceinline__ void wait_dma_n() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 constexpr int kOob = (int)0x80000000;  // offset beyond any range: reads zero
 
-// LDS swizzle of a 128-B row: 16-B chunk c of row r lives in slot
-// c ^ ((r >> 1) & 7).  A ds_read_b128 is served 16 lanes (256 B, all 64
-// banks) per cycle; 16 consecutive rows alternate bank halves by row parity
-// and take 8 distinct slots by (r >> 1), so they never share a bank.
-__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+// LDS row layout.  A stage holds 64 K per row (64 B = four 16-B chunks);
+// chunk c of row r lives in slot c ^ ((r >> 2) & 3).  A ds_read_b128 is served
+// 16 lanes (256 B, all 64 banks) per cycle; the 16 rows read by 16 lanes span
+// four 256-B bank lines (r % 4) with four distinct slots each (r >> 2), so
+// fragment reads are conflict-free.
+__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
 
 // 32 bytes of K (chunks c0, c0+1) of LDS row `r` as one MFMA operand.
 __device__ __forceinline__ v8i lds_frag(const uint8_t* tile, int r, int c0) {
-    const v4i lo = *reinterpret_cast<const v4i*>(tile + r * 128 + ((c0 ^ swz(r)) << 4));
-    const v4i hi = *reinterpret_cast<const v4i*>(tile + r * 128 + (((c0 + 1) ^ swz(r)) << 4));
+    const v4i lo = *reinterpret_cast<const v4i*>(tile + r * 64 + ((c0 ^ swz(r)) << 4));
+    const v4i hi = *reinterpret_cast<const v4i*>(tile + r * 64 + (((c0 + 1) ^ swz(r)) << 4));
     return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
@@ -120,20 +127,31 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, i
     tn = w / gm;
 }
 
-// LDS stage layout: [A: BM x 128 B][W: BN x 128 B][sA: 256 fp32][sW: 4 x 64 fp32]
-// (one 64-entry weight-scale slot per wavefront, so every wavefront issues the
-// same DMA sequence and the main loop has no wave-dependent branches)
+constexpr int kKS = 64;      // K per LDS stage (one 32x32x64 MFMA deep)
+constexpr int kStages = 4;   // LDS buffers: three stages in flight while one is read
+
+// Block-scaled GEMM tile kernel.
+// LDS stage layout: [A: BM x 64 B][W: BN x 64 B][sA: 64 fp32 per wavefront][sW: 64 fp32 per wavefront]
+// Pipeline (stage s = K range [64 s, 64 s + 64), scale block s / 2):
+//   prologue: DMA stages 0..3; wait stage 0; fragments of stage 0 -> registers
+//   iteration s: wait until stage s+1 landed (s+2, s+3 may still fly) and
+//     this wavefront's reads of stage s finished, barrier (publishes s+1 and
+//     frees buffer s, whose fragments now sit in registers), DMA stage s+4
+//     into it, then the MFMAs of stage s interleaved with the LDS reads of
+//     the stage s+1 fragments.  Three stages (96 KB for a 256x256 tile) stay
+//     in flight per CU, which is what covers the L2/MALL latency.
 template <int BM, int BN, int WM, int WN, bool kUe8m0, bool kGrouped>
-__global__ __launch_bounds__(kThreads, 1) void gemm_bs_kernel(const GemmArgs a) {
+__global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bs_kernel(const GemmArgs a) {
+    constexpr int kWaves = WM * WN;
     constexpr int TM = BM / WM, TN = BN / WN;   // wavefront tile
     constexpr int FM = TM / 32, FN = TN / 32;   // 32x32 fragments per wavefront
-    static_assert(WM * WN == 4, "four wavefronts");
+    static_assert(kWaves == 4, "four wavefronts");
     static_assert(FM >= 1 && FN >= 1 && TM % 32 == 0 && TN % 32 == 0, "fragment tiling");
-    static_assert(BM % 64 == 0 && BN % 32 == 0 && BM <= 256 && BN <= 8192, "DMA tiling");
+    static_assert(BM % 64 == 0 && BN % 64 == 0 && BM <= 256, "DMA tiling");
     static_assert(128 % TN == 0 || TN % 128 == 0, "wave N tile must not straddle a scale block");
-    constexpr int kA = BM * kBK, kB = BN * kBK, kSA = 256 * 4, kSW = 4 * 64 * 4;
+    constexpr int kA = BM * kKS, kB = BN * kKS, kSA = kWaves * 256, kSW = kWaves * 256;
     constexpr int kStage = kA + kB + kSA + kSW;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStage];
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)smem);
 
     int tm, tn;
@@ -142,7 +160,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bs_kernel(const GemmArgs a) 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WN, wn = wave % WN;
-    const int KB = a.K / kBK;
+    const int KS = a.K / kKS;                    // stages
     const int NB = (a.N + kGroup - 1) / kGroup;
 
     const uint8_t* Wbase = a.W;
@@ -160,46 +178,41 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bs_kernel(const GemmArgs a) 
     const v4i dSA = make_desc(a.sA, a.sA_bytes);
     const v4i dSW = make_desc(sWbase, (int64_t)NB * a.sW_ld * 4);
 
-    // Per-lane DMA offsets (32-bit; the host checks every range fits) that do
-    // not depend on the K step, so the loop only adds k0 and selects.
-    // lane -> (row r0 + lane/8, LDS slot lane%8) holds global chunk slot ^ swz(row);
-    // r0 is a multiple of 8, so swz(row) = swz(r0) ^ ... is folded per instruction below
-    const int a_row = lane >> 3;
-    // The 8-row group index (wave * rows/32 + i) is even or odd with i, so two
-    // per-lane offsets cover every DMA instruction: swz(row) = (4*(group&1) + row/2) & 7.
-    const int chunk0 = ((lane & 7) ^ swz(a_row)) << 4;
-    const int chunk1 = ((lane & 7) ^ swz(a_row + 8)) << 4;
-    const int a_lane0 = (int)(a_row * a.lda) + chunk0, a_lane1 = (int)(a_row * a.lda) + chunk1;
-    const int w_lane0 = (int)(a_row * a.ldw) + chunk0, w_lane1 = (int)(a_row * a.ldw) + chunk1;
-    static_assert((BM / 32) % 2 == 0 && (BN / 32) % 2 == 0, "each wave's first 8-row group is even");
-    const int a_wave = (int)(wave * (BM / 32) * 8 * a.lda);
-    const int w_wave = (int)(wave * (BN / 32) * 8 * a.ldw);
-    constexpr int kScaleInstr = BM / 64;                             // 64 scale rows per dword DMA
+    // DMA lane mapping: one instruction = 16 rows x 64 B; lane i fills LDS
+    // slot i%4 of row r0 + i/4 with global chunk (i%4) ^ swz(row), and since
+    // r0 is a multiple of 16, swz(row) = i/16.
+    const int drow = lane >> 2;
+    const int dchunk = ((lane & 3) ^ (lane >> 4)) << 4;
+    const int a_lane = (int)(drow * a.lda) + dchunk;
+    const int w_lane = (int)(drow * a.ldw) + dchunk;
+    constexpr int kAInstr = BM / 16 / kWaves, kBInstr = BN / 16 / kWaves;  // 16-row DMAs per wave
+    const int a_wave = (int)(wave * kAInstr * 16 * a.lda);
+    const int w_wave = (int)(wave * kBInstr * 16 * a.ldw);
+    constexpr int kScaleInstr = BM / 64;                              // 64 scale rows per dword DMA
     const int sa_row = wave * 64 + lane;
-    const bool sa_live = (wave < kScaleInstr) & (m0 + sa_row < a.M); // rows past BM land in unused slots
+    const bool sa_live = (wave < kScaleInstr) & (m0 + sa_row < a.M);  // rows past BM land in unused slots
     const int sa_off0 = sa_live ? (int)((int64_t)(m0 + sa_row) * a.sA_sm * 4) : kOob;
     const int sa_kstep = sa_live ? (int)(a.sA_sk * 4) : 0;
     const bool sw_live = (lane < (BN + 127) / 128) & (n0 / 128 + lane < NB);
     const int sw_off0 = sw_live ? (n0 / 128 + lane) * (int)a.sW_ld * 4 : kOob;
     const int sw_kstep = sw_live ? 4 : 0;
+    constexpr int kDmaPerStage = kAInstr + kBInstr + 2;  // per wave
 
-    // Stage kt -> LDS stage st.  `live` false turns every load into an
-    // out-of-range (zero) read, so the caller never branches around it.
-    auto issue_stage = [&](int kt, int st, bool live) {
-        const uint32_t base = lds0 + st * kStage;
-        const int k0 = kt * kBK;
+    // Stage s -> LDS buffer s % kStages.  `live` false turns every load into
+    // an out-of-range (zero) read, so the loop never branches around it.
+    auto issue_stage = [&](int s, bool live) {
+        const uint32_t base = lds0 + (s % kStages) * kStage;
+        const int k0 = s * kKS, kb = s >> 1;
 #pragma unroll
-        for (int i = 0; i < BM / 32; ++i) {
-            const int off = (i & 1 ? a_lane1 : a_lane0) + a_wave + (int)(i * 8 * a.lda) + k0;
-            dma_b128(dA, base + (wave * (BM / 32) + i) * 8 * 128, live ? off : kOob);
-        }
+        for (int i = 0; i < kAInstr; ++i)
+            dma_b128(dA, base + (wave * kAInstr + i) * 16 * 64,
+                     live ? a_lane + a_wave + (int)(i * 16 * a.lda) + k0 : kOob);
 #pragma unroll
-        for (int i = 0; i < BN / 32; ++i) {
-            const int off = (i & 1 ? w_lane1 : w_lane0) + w_wave + (int)(i * 8 * a.ldw) + k0;
-            dma_b128(dW, base + kA + (wave * (BN / 32) + i) * 8 * 128, live ? off : kOob);
-        }
-        dma_b32(dSA, base + kA + kB + wave * 256, live ? sa_off0 + kt * sa_kstep : kOob);
-        dma_b32(dSW, base + kA + kB + kSA + wave * 256, live ? sw_off0 + kt * sw_kstep : kOob);
+        for (int i = 0; i < kBInstr; ++i)
+            dma_b128(dW, base + kA + (wave * kBInstr + i) * 16 * 64,
+                     live ? w_lane + w_wave + (int)(i * 16 * a.ldw) + k0 : kOob);
+        dma_b32(dSA, base + kA + kB + wave * 256, live ? sa_off0 + kb * sa_kstep : kOob);
+        dma_b32(dSW, base + kA + kB + kSA + wave * 256, live ? sw_off0 + kb * sw_kstep : kOob);
     };
 
     const int nb_local = (wn * TN) / 128;  // this wavefront's weight-scale block within the tile
@@ -210,94 +223,115 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bs_kernel(const GemmArgs a) 
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = v16f{};
 
+    // Fragment / scale register sets for two consecutive stages (ping-pong:
+    // the loop below is unrolled by two stages so no set is ever copied).
     v8i fa0[FM], fb0[FN], fa1[FM], fb1[FN];
-    int ea[FM];
-    int eb = 0;
+    float sa0[FM], sa1[FM];
+    float sw0 = 0.f, sw1 = 0.f;
     float sa_row_scale[kUe8m0 ? 1 : FM][kUe8m0 ? 1 : 16];
     float swv = 0.f;
 
-    auto read_frags = [&](const uint8_t* st, int ks, v8i (&af)[FM], v8i (&bf)[FN]) {
-        const int c0 = ks * 4 + (lane >> 5) * 2;
+    auto stage_ptr = [&](int s) -> const uint8_t* { return smem + (s % kStages) * kStage; };
+    auto read_frags = [&](const uint8_t* st, v8i (&af)[FM], v8i (&bf)[FN]) {
+        const int c0 = (lane >> 5) * 2;
 #pragma unroll
         for (int i = 0; i < FM; ++i) af[i] = lds_frag(st, wm * TM + i * 32 + (lane & 31), c0);
 #pragma unroll
         for (int j = 0; j < FN; ++j) bf[j] = lds_frag(st + kA, wn * TN + j * 32 + (lane & 31), c0);
     };
-    auto read_scales = [&](const uint8_t* st) {
+    // raw fp32 scales of a stage (converted to E8M0 only when consumed, so no
+    // LDS wait lands in the middle of the MFMA stream)
+    auto read_scales = [&](const uint8_t* st, float (&sa)[FM], float& sw) {
         const float* ssa = reinterpret_cast<const float*>(st + kA + kB);
         const float* ssw = reinterpret_cast<const float*>(st + kA + kB + kSA + wave * 256);
-        if constexpr (kUe8m0) {
 #pragma unroll
-            for (int i = 0; i < FM; ++i) ea[i] = ue8m0_ceil_byte(ssa[wm * TM + i * 32 + (lane & 31)]);
-            eb = ue8m0_ceil_byte(ssw[nb_local]);
-        } else {
-            // output row of accumulator register r: 8*(r/4) + 4*(lane/32) + r%4
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    sa_row_scale[i][r] = ssa[wm * TM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)];
-            swv = ssw[nb_local];
-        }
+        for (int i = 0; i < FM; ++i) sa[i] = ssa[wm * TM + i * 32 + (lane & 31)];
+        sw = ssw[nb_local];
     };
-    auto mfma_step = [&](v8i (&af)[FM], v8i (&bf)[FN], v16f (&c)[FM][FN], bool fresh) {
+    auto read_fp32_scales = [&](const uint8_t* st) {
+        // output row of accumulator register r: 8*(r/4) + 4*(lane/32) + r%4
+        const float* ssa = reinterpret_cast<const float*>(st + kA + kB);
+        const float* ssw = reinterpret_cast<const float*>(st + kA + kB + kSA + wave * 256);
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                if constexpr (kUe8m0)
-                    c[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf[j], c[i][j], 0, 0, 0, ea[i],
-                                                                              0, eb);
-                else
-                    c[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf[j], fresh ? v16f{} : c[i][j],
-                                                                              0, 0, 0, 0, 0, 0);
-            }
+            for (int r = 0; r < 16; ++r)
+                sa_row_scale[i][r] = ssa[wm * TM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)];
+        swv = ssw[nb_local];
     };
 
-    // prologue: stages 0 and 1 in flight, wait for both, fragments of step 0
-    issue_stage(0, 0, true);
-    issue_stage(1, 1, KB > 1);
-    wait_dma();
-    __syncthreads();
-    read_frags(smem, 0, fa0, fb0);
-    read_scales(smem);
-
     v16f part[kUe8m0 ? 1 : FM][kUe8m0 ? 1 : FN];
-    for (int kt = 0; kt < KB; ++kt) {
-        const uint8_t* cur = smem + (kt & 1) * kStage;
-        const uint8_t* nxt = smem + ((kt + 1) & 1) * kStage;
-        // first half of the K step on fragments read earlier
+    // One stage: publish stage s+1, refill buffer s with stage s+4, then the
+    // MFMAs of stage s (operands in fa/fb/sa/sw) interleaved with the LDS reads
+    // of stage s+1 into na/nb/nsa/nsw.
+    auto stage = [&](int s, v8i (&fa)[FM], v8i (&fb)[FN], float (&sa)[FM], float& sw, v8i (&na)[FM],
+                     v8i (&nb)[FN], float (&nsa)[FM], float& nsw) {
+        wait_dma_n<2 * kDmaPerStage>();   // stage s+1 landed
+        wait_lds();                        // this wavefront's reads of stage s are done
+        __syncthreads();
+        issue_stage(s + 4, s + 4 < KS);
+        const uint8_t* nxt = stage_ptr(s + 1);
+        read_scales(nxt, nsa, nsw);
+        read_frags(nxt, na, nb);
         if constexpr (kUe8m0) {
-            mfma_step(fa0, fb0, acc, false);
-        } else {
-            mfma_step(fa0, fb0, part, true);
-        }
-        read_frags(cur, 1, fa1, fb1);
-        if constexpr (kUe8m0) {
-            mfma_step(fa1, fb1, acc, false);
-        } else {
-            mfma_step(fa1, fb1, part, false);
-            // promotion: acc += part * sA[row] * sW[block]
+            int ea[FM];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) ea[i] = ue8m0_ceil_byte(sa[i]);
+            const int eb = ue8m0_ceil_byte(sw);
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const float f = sa_row_scale[i][r] * swv;
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fb[j], acc[i][j], 0, 0, 0,
+                                                                                ea[i], 0, eb);
+        } else {
+            // the promotion at the end of odd stage s+1 uses its block's
+            // scales; read them now, while buffer s+1 is guaranteed intact
+            if ((s & 1) == 0) read_fp32_scales(nxt);
+            const bool first_half = (s & 1) == 0;
 #pragma unroll
-                    for (int j = 0; j < FN; ++j) acc[i][j][r] = fmaf(part[i][j][r], f, acc[i][j][r]);
-                }
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    part[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        fa[i], fb[j], first_half ? v16f{} : part[i][j], 0, 0, 0, 0, 0, 0);
+            if (!first_half) {
+                // promotion after both halves of the scale block:
+                // acc += part * sA[row] * sW[block]
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const float f = sa_row_scale[i][r] * swv;
+#pragma unroll
+                        for (int j = 0; j < FN; ++j) acc[i][j][r] = fmaf(part[i][j][r], f, acc[i][j][r]);
+                    }
+            }
         }
-        // The MFMAs above keep the matrix pipe busy across this barrier.  It
-        // publishes stage kt+1 and frees stage kt for the DMA of kt+2; the
-        // last iteration's extra barrier/read is harmless.
-        __builtin_amdgcn_sched_barrier(0);
-        wait_lds();
-        wait_dma();
-        __syncthreads();
-        issue_stage(kt + 2, kt & 1, kt + 2 < KB);
-        read_frags(nxt, 0, fa0, fb0);
-        read_scales(nxt);
-        __builtin_amdgcn_sched_barrier(0);
+        // Interleave the stage-s MFMAs with the LDS reads of stage s+1 (two
+        // 16-B reads between consecutive MFMAs) so the reads complete under
+        // the matrix pipe.
+#pragma unroll
+        for (int i = 0; i < FM * FN; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two LDS reads
+        }
+    };
+
+    // prologue
+    issue_stage(0, true);
+    issue_stage(1, KS > 1);
+    issue_stage(2, KS > 2);
+    issue_stage(3, KS > 3);
+    wait_dma_n<3 * kDmaPerStage>();
+    __syncthreads();
+    read_scales(stage_ptr(0), sa0, sw0);
+    read_frags(stage_ptr(0), fa0, fb0);
+
+    // KS is even (K is a multiple of 128)
+    for (int s = 0; s < KS; s += 2) {
+        stage(s, fa0, fb0, sa0, sw0, fa1, fb1, sa1, sw1);
+        stage(s + 1, fa1, fb1, sa1, sw1, fa0, fb0, sa0, sw0);
     }
 
     // epilogue: fp32 -> bf16 (RNE), masked 2-byte stores
@@ -327,7 +361,7 @@ static int launch_gemm(GemmArgs a, hipStream_t st, const char* what) {
     a.tiles_n = (a.N + BN - 1) / BN;
     const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n;
     KBN_CHECK_ARG(blocks <= 0x7FFFFFFFLL, "%s: too many tiles", what);
-    gemm_bs_kernel<BM, BN, WM, WN, kUe8m0, kGrouped><<<dim3((unsigned)blocks), dim3(kThreads), 0, st>>>(a);
+    gemm_bs_kernel<BM, BN, WM, WN, kUe8m0, kGrouped><<<dim3((unsigned)blocks), dim3(64 * WM * WN), 0, st>>>(a);
     KBN_CHECK_LAUNCH(what);
     return 0;
 }
