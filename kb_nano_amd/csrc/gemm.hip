@@ -17,15 +17,17 @@
 //    running sum with one FMA per element and stage.
 //
 // Dataflow per workgroup (256 lanes = 4 wavefronts, one per SIMD):
-//   HBM --buffer_load_dwordx4 ... lds (direct DMA)--> LDS (4 stages x (BM+BN) x 64 B)
+//   HBM --buffer_load_dwordx4 ... lds (direct DMA)--> LDS (kStages x (BM+BN) x 128 B)
 //   LDS --ds_read_b128--> VGPR fragments --MFMA 32x32x64--> fp32 accumulators
-// Each LDS row is 64 B (one 64-K stage); its four 16-B chunks are XOR-
-// swizzled so the rows read by one ds_read_b128 hit distinct banks.  The
+// Each LDS row is 128 B (one 128-K scale block); its eight 16-B chunks are
+// XOR-swizzled so the rows read by one ds_read_b128 hit distinct banks.  The
 // swizzle is applied on the global side of the DMA (lane i of a load
 // instruction always writes LDS chunk i), so no extra LDS pass is needed.
 // Out-of-range rows read as zero through the buffer descriptor's range check.
 
 #include "kbn_common.h"
+
+#include <algorithm>
 
 namespace kbn {
 
@@ -33,7 +35,6 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int kBK = 128;           // K per stage == scale block
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit dword format (gfx9 family)
 
 struct GemmArgs {
@@ -53,6 +54,7 @@ struct GemmArgs {
     const int32_t* expert_ids;   // grouped only
     int M, N, K, E;
     int tiles_m, tiles_n;
+    int vec_store;               // D rows allow aligned 16-B stores
 };
 
 // Raw buffer descriptor (base, byte range) built from uniform values so it
@@ -93,19 +95,15 @@ __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)"
 
 constexpr int kOob = (int)0x80000000;  // offset beyond any range: reads zero
 
-// LDS row layout.  A stage holds 64 K per row (64 B = four 16-B chunks);
-// chunk c of row r lives in slot c ^ ((r >> 2) & 3).  A ds_read_b128 is served
-// 16 lanes (256 B, all 64 banks) per cycle; the 16 rows read by 16 lanes span
-// four 256-B bank lines (r % 4) with four distinct slots each (r >> 2), so
+// LDS row layout.  A stage holds one 128-K scale block per row (128 B =
+// eight 16-B chunks); chunk c of row r lives in slot c ^ swz(r).  A
+// ds_read_b128 is served 16 lanes (256 B, all 64 banks) per cycle; the 16
+// consecutive rows read by 16 lanes alternate between the two halves of a
+// 256-B bank line (r % 2) and take 8 distinct slots per half (r >> 1), so
 // fragment reads are conflict-free.
-__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 
-// 32 bytes of K (chunks c0, c0+1) of LDS row `r` as one MFMA operand.
-__device__ __forceinline__ v8i lds_frag(const uint8_t* tile, int r, int c0) {
-    const v4i lo = *reinterpret_cast<const v4i*>(tile + r * 64 + ((c0 ^ swz(r)) << 4));
-    const v4i hi = *reinterpret_cast<const v4i*>(tile + r * 64 + (((c0 + 1) ^ swz(r)) << 4));
-    return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
+constexpr int kRowB = 128;   // LDS row bytes = K per stage = one scale block
 
 // XCD-aware tile order.  Consecutive workgroup ids are dispatched round-robin
 // over the 8 XCDs; give each XCD a contiguous range of the tile sequence so
@@ -127,30 +125,43 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, i
     tn = w / gm;
 }
 
-constexpr int kKS = 64;      // K per LDS stage (one 32x32x64 MFMA deep)
-constexpr int kStages = 4;   // LDS buffers: three stages in flight while one is read
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-// Block-scaled GEMM tile kernel.
-// LDS stage layout: [A: BM x 64 B][W: BN x 64 B][sA: 64 fp32 per wavefront][sW: 64 fp32 per wavefront]
-// Pipeline (stage s = K range [64 s, 64 s + 64), scale block s / 2):
-//   prologue: DMA stages 0..3; wait stage 0; fragments of stage 0 -> registers
-//   iteration s: wait until stage s+1 landed (s+2, s+3 may still fly) and
-//     this wavefront's reads of stage s finished, barrier (publishes s+1 and
-//     frees buffer s, whose fragments now sit in registers), DMA stage s+4
-//     into it, then the MFMAs of stage s interleaved with the LDS reads of
-//     the stage s+1 fragments.  Three stages (96 KB for a 256x256 tile) stay
-//     in flight per CU, which is what covers the L2/MALL latency.
-template <int BM, int BN, int WM, int WN, bool kUe8m0, bool kGrouped>
-__global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bs_kernel(const GemmArgs a) {
-    constexpr int kWaves = WM * WN;
-    constexpr int TM = BM / WM, TN = BN / WN;   // wavefront tile
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    const bf16x2 p = __builtin_convertvector((f32x2{lo, hi}), bf16x2);  // v_cvt_pk_bf16_f32, RNE
+    return __builtin_bit_cast(uint32_t, p);
+}
+// Block-scaled GEMM tile kernel: BM x BN output tile, four wavefronts in a
+// 2 x 2 grid, each owning a (BM/2) x (BN/2) block of 32x32 MFMA fragments.
+//
+// LDS stage layout (one stage = one 128-K block):
+//   [A: BM x 128 B][W: BN x 128 B][sA: 4 x 64 fp32][sW: 4 x 64 fp32]
+// Every load is a 16-B (or 4-B) direct global->LDS DMA; one A/W instruction
+// moves eight full 128-B rows, so every request the vector cache sends to L2
+// is a whole 128-B line.
+//
+// Pipeline over K blocks kb (LDS buffer kb % kStages), per wavefront:
+//   sub-step 0: MFMAs of K half 0 of block kb, interleaved with the LDS reads
+//               of K half 1 of block kb;
+//   hand-off:   wait until block kb+1 has landed and this wavefront's reads of
+//               block kb are done; barrier (publishes kb+1, frees buffer kb);
+//               DMA block kb+kStages into the freed buffer;
+//   sub-step 1: MFMAs of K half 1 of block kb, interleaved with the LDS reads
+//               of K half 0 (and the scales) of block kb+1.
+// So kStages-1 blocks are in flight while one is consumed, and no fragment
+// register set is ever copied.
+template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped>
+__global__ __launch_bounds__(256, 1) void gemm_bs_kernel(const GemmArgs a) {
+    constexpr int WN = 2;
+    constexpr int TM = BM / 2, TN = BN / 2;     // wavefront tile
     constexpr int FM = TM / 32, FN = TN / 32;   // 32x32 fragments per wavefront
-    static_assert(kWaves == 4, "four wavefronts");
     static_assert(FM >= 1 && FN >= 1 && TM % 32 == 0 && TN % 32 == 0, "fragment tiling");
-    static_assert(BM % 64 == 0 && BN % 64 == 0 && BM <= 256, "DMA tiling");
+    static_assert(BM <= 256 && BM % 64 == 0 && BN % 64 == 0, "DMA tiling");
     static_assert(128 % TN == 0 || TN % 128 == 0, "wave N tile must not straddle a scale block");
-    constexpr int kA = BM * kKS, kB = BN * kKS, kSA = kWaves * 256, kSW = kWaves * 256;
+    constexpr int kA = BM * kRowB, kB = BN * kRowB, kSA = 4 * 256, kSW = 4 * 256;
     constexpr int kStage = kA + kB + kSA + kSW;
+    static_assert(kStages >= 2 && kStages * kStage <= 160 * 1024, "LDS budget");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStage];
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)smem);
 
@@ -160,7 +171,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bs_kernel(const GemmArgs
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WN, wn = wave % WN;
-    const int KS = a.K / kKS;                    // stages
+    const int KB = a.K / kRowB;                  // K blocks
     const int NB = (a.N + kGroup - 1) / kGroup;
 
     const uint8_t* Wbase = a.W;
@@ -178,44 +189,54 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bs_kernel(const GemmArgs
     const v4i dSA = make_desc(a.sA, a.sA_bytes);
     const v4i dSW = make_desc(sWbase, (int64_t)NB * a.sW_ld * 4);
 
-    // DMA lane mapping: one instruction = 16 rows x 64 B; lane i fills LDS
-    // slot i%4 of row r0 + i/4 with global chunk (i%4) ^ swz(row), and since
-    // r0 is a multiple of 16, swz(row) = i/16.
-    const int drow = lane >> 2;
-    const int dchunk = ((lane & 3) ^ (lane >> 4)) << 4;
-    const int a_lane = (int)(drow * a.lda) + dchunk;
-    const int w_lane = (int)(drow * a.ldw) + dchunk;
-    constexpr int kAInstr = BM / 16 / kWaves, kBInstr = BN / 16 / kWaves;  // 16-row DMAs per wave
-    const int a_wave = (int)(wave * kAInstr * 16 * a.lda);
-    const int w_wave = (int)(wave * kBInstr * 16 * a.ldw);
-    constexpr int kScaleInstr = BM / 64;                              // 64 scale rows per dword DMA
+    // DMA lane mapping: one instruction = 8 rows x 128 B starting at row
+    // r0 = 8 q; lane i fills slot i % 8 of row r0 + i / 8 with global chunk
+    // (i % 8) ^ swz(r0 + i / 8) = (i % 8) ^ ((i >> 4) | 4 (q & 1)).
+    constexpr int kAInstr = BM / 32, kBInstr = BN / 32;   // 8-row DMAs per wave
+    static_assert(kAInstr % 2 == 0 && kBInstr % 2 == 0, "even instruction counts keep q & 1 == i & 1");
+    const int drow = lane >> 3;
+    const int ch_e = ((lane & 7) ^ (lane >> 4)) << 4;
+    const int ch_o = ((lane & 7) ^ ((lane >> 4) | 4)) << 4;
+    const int a_e = (int)((wave * kAInstr * 8 + drow) * a.lda) + ch_e;
+    const int a_o = a_e - ch_e + ch_o;
+    const int w_e = (int)((wave * kBInstr * 8 + drow) * a.ldw) + ch_e;
+    const int w_o = w_e - ch_e + ch_o;
     const int sa_row = wave * 64 + lane;
-    const bool sa_live = (wave < kScaleInstr) & (m0 + sa_row < a.M);  // rows past BM land in unused slots
+    const bool sa_live = (sa_row < BM) & (m0 + sa_row < a.M);
     const int sa_off0 = sa_live ? (int)((int64_t)(m0 + sa_row) * a.sA_sm * 4) : kOob;
     const int sa_kstep = sa_live ? (int)(a.sA_sk * 4) : 0;
     const bool sw_live = (lane < (BN + 127) / 128) & (n0 / 128 + lane < NB);
     const int sw_off0 = sw_live ? (n0 / 128 + lane) * (int)a.sW_ld * 4 : kOob;
     const int sw_kstep = sw_live ? 4 : 0;
-    constexpr int kDmaPerStage = kAInstr + kBInstr + 2;  // per wave
+    constexpr int kDma = kAInstr + kBInstr + 2;  // DMA instructions per wave per stage
 
-    // Stage s -> LDS buffer s % kStages.  `live` false turns every load into
-    // an out-of-range (zero) read, so the loop never branches around it.
-    auto issue_stage = [&](int s, bool live) {
+    // DMA instruction d (0 <= d < kDma) of K block s -> LDS buffer s % kStages:
+    // the two scale vectors, then the A rows, then the W rows.  `live` false
+    // turns the load into an out-of-range (zero) read, so the loop never
+    // branches around it and every stage issues the same number of loads.
+    auto issue_one = [&](int s, bool live, int d) {
         const uint32_t base = lds0 + (s % kStages) * kStage;
-        const int k0 = s * kKS, kb = s >> 1;
-#pragma unroll
-        for (int i = 0; i < kAInstr; ++i)
-            dma_b128(dA, base + (wave * kAInstr + i) * 16 * 64,
-                     live ? a_lane + a_wave + (int)(i * 16 * a.lda) + k0 : kOob);
-#pragma unroll
-        for (int i = 0; i < kBInstr; ++i)
-            dma_b128(dW, base + kA + (wave * kBInstr + i) * 16 * 64,
-                     live ? w_lane + w_wave + (int)(i * 16 * a.ldw) + k0 : kOob);
-        dma_b32(dSA, base + kA + kB + wave * 256, live ? sa_off0 + kb * sa_kstep : kOob);
-        dma_b32(dSW, base + kA + kB + kSA + wave * 256, live ? sw_off0 + kb * sw_kstep : kOob);
+        const int k0 = s * kRowB;
+        if (d == 0) {
+            dma_b32(dSA, base + kA + kB + wave * 256, live ? sa_off0 + s * sa_kstep : kOob);
+        } else if (d == 1) {
+            dma_b32(dSW, base + kA + kB + kSA + wave * 256, live ? sw_off0 + s * sw_kstep : kOob);
+        } else if (d < 2 + kAInstr) {
+            const int i = d - 2;
+            dma_b128(dA, base + (wave * kAInstr + i) * 1024,
+                     live ? ((i & 1) ? a_o : a_e) + (int)(i * 8 * a.lda) + k0 : kOob);
+        } else {
+            const int i = d - 2 - kAInstr;
+            dma_b128(dW, base + kA + (wave * kBInstr + i) * 1024,
+                     live ? ((i & 1) ? w_o : w_e) + (int)(i * 8 * a.ldw) + k0 : kOob);
+        }
     };
 
     const int nb_local = (wn * TN) / 128;  // this wavefront's weight-scale block within the tile
+    // per-lane fragment offsets: row (lane & 31) of a 32-row fragment, chunk
+    // c = 4 kk + 2 (lane >> 5) + h for 16-B half h; swz(row) = (lane >> 1) & 7
+    const int fs = (lane >> 1) & 7;
+    const int frow = (lane & 31) * kRowB;
 
     v16f acc[FM][FN];
 #pragma unroll
@@ -223,24 +244,22 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bs_kernel(const GemmArgs
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = v16f{};
 
-    // Fragment / scale register sets for two consecutive stages (ping-pong:
-    // the loop below is unrolled by two stages so no set is ever copied).
-    v8i fa0[FM], fb0[FN], fa1[FM], fb1[FN];
-    float sa0[FM], sa1[FM];
-    float sw0 = 0.f, sw1 = 0.f;
-    float sa_row_scale[kUe8m0 ? 1 : FM][kUe8m0 ? 1 : 16];
-    float swv = 0.f;
-
     auto stage_ptr = [&](int s) -> const uint8_t* { return smem + (s % kStages) * kStage; };
-    auto read_frags = [&](const uint8_t* st, v8i (&af)[FM], v8i (&bf)[FN]) {
-        const int c0 = (lane >> 5) * 2;
-#pragma unroll
-        for (int i = 0; i < FM; ++i) af[i] = lds_frag(st, wm * TM + i * 32 + (lane & 31), c0);
-#pragma unroll
-        for (int j = 0; j < FN; ++j) bf[j] = lds_frag(st + kA, wn * TN + j * 32 + (lane & 31), c0);
+    // 16-B read q (0 <= q < 2 (FM + FN)) of K half kk: half q % 2 of fragment
+    // q / 2, A fragments first
+    auto read_half = [&](const uint8_t* st, int kk, int q, v8i (&af)[FM], v8i (&bf)[FN]) {
+        const int f = q >> 1, h = q & 1;
+        const int c = 4 * kk + 2 * (lane >> 5) + h;
+        const uint8_t* tile = f < FM ? st + (wm * TM + f * 32) * kRowB : st + kA + (wn * TN + (f - FM) * 32) * kRowB;
+        const v4i v = *reinterpret_cast<const v4i*>(tile + frow + ((c ^ fs) << 4));
+        if (f < FM) {
+            if (h) af[f].hi = v; else af[f].lo = v;
+        } else {
+            if (h) bf[f - FM].hi = v; else bf[f - FM].lo = v;
+        }
     };
-    // raw fp32 scales of a stage (converted to E8M0 only when consumed, so no
-    // LDS wait lands in the middle of the MFMA stream)
+    // raw fp32 scales of a stage: per fragment row (lane & 31) and the
+    // wavefront's weight block (converted to E8M0 only when consumed)
     auto read_scales = [&](const uint8_t* st, float (&sa)[FM], float& sw) {
         const float* ssa = reinterpret_cast<const float*>(st + kA + kB);
         const float* ssw = reinterpret_cast<const float*>(st + kA + kB + kSA + wave * 256);
@@ -248,120 +267,178 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_bs_kernel(const GemmArgs
         for (int i = 0; i < FM; ++i) sa[i] = ssa[wm * TM + i * 32 + (lane & 31)];
         sw = ssw[nb_local];
     };
-    auto read_fp32_scales = [&](const uint8_t* st) {
-        // output row of accumulator register r: 8*(r/4) + 4*(lane/32) + r%4
-        const float* ssa = reinterpret_cast<const float*>(st + kA + kB);
-        const float* ssw = reinterpret_cast<const float*>(st + kA + kB + kSA + wave * 256);
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                sa_row_scale[i][r] = ssa[wm * TM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)];
-        swv = ssw[nb_local];
+    v8i fa0[FM], fb0[FN], fa1[FM], fb1[FN];
+    float sa[FM], sw = 0.f, nsa[FM], nsw = 0.f;
+    v16f part[kUe8m0 ? 1 : FM][kUe8m0 ? 1 : FN];
+    int ea[FM], eb = 0, nea[FM], neb = 0;
+    // MFMA t (0 <= t < FM FN) of a sub-step.  The product is formed as
+    // D^T = W A^T (W fragment as the MFMA's A operand), so accumulator
+    // register r of lane l holds output row (l % 32) of fragment i and column
+    // 8 (r / 4) + 4 (l / 32) + r % 4 of fragment j: every lane owns runs of
+    // four consecutive columns of one row, ready for packed stores.
+    auto mfma_at = [&](int t, const v8i (&fa)[FM], const v8i (&fb)[FN], bool first) {
+        const int i = t / FN, j = t % FN;
+        if constexpr (kUe8m0)
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], acc[i][j], 0, 0, 0, eb, 0, ea[i]);
+        else
+            part[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], first ? v16f{} : part[i][j], 0,
+                                                                         0, 0, 0, 0, 0);
     };
 
-    v16f part[kUe8m0 ? 1 : FM][kUe8m0 ? 1 : FN];
-    // One stage: publish stage s+1, refill buffer s with stage s+4, then the
-    // MFMAs of stage s (operands in fa/fb/sa/sw) interleaved with the LDS reads
-    // of stage s+1 into na/nb/nsa/nsw.
-    auto stage = [&](int s, v8i (&fa)[FM], v8i (&fb)[FN], float (&sa)[FM], float& sw, v8i (&na)[FM],
-                     v8i (&nb)[FN], float (&nsa)[FM], float& nsw) {
-        wait_dma_n<2 * kDmaPerStage>();   // stage s+1 landed
-        wait_lds();                        // this wavefront's reads of stage s are done
+    // Each sub-step is laid out as FM*FN issue slots: one MFMA, then this
+    // slot's share of the LDS fragment reads and (sub-step 1) of the next
+    // stage's DMAs.  sched_barrier keeps the slots in order, so the single
+    // texture-address unit of the CU sees a steady trickle of DMAs from each
+    // wavefront instead of a burst that stalls the MFMA issue behind it.
+    constexpr int kT = FM * FN;           // MFMAs per sub-step
+    constexpr int kR = 2 * (FM + FN);     // 16-B fragment reads per sub-step
+
+    // prologue: blocks 0 .. kStages-1 in flight, block 0 published
+#pragma unroll
+    for (int s = 0; s < kStages; ++s)
+#pragma unroll
+        for (int d = 0; d < kDma; ++d) issue_one(s, s < KB, d);
+    wait_dma_n<(kStages - 1) * kDma>();
+    __syncthreads();
+    read_scales(stage_ptr(0), sa, sw);
+#pragma unroll
+    for (int q = 0; q < kR; ++q) read_half(stage_ptr(0), 0, q, fa0, fb0);
+
+    if constexpr (kUe8m0) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) ea[i] = ue8m0_ceil_byte(sa[i]);
+        eb = ue8m0_ceil_byte(sw);
+    }
+
+    for (int kb = 0; kb < KB; ++kb) {
+        const uint8_t* cur = stage_ptr(kb);
+        // ---- sub-step 0: K half 0 of block kb; read K half 1
+#pragma unroll
+        for (int t = 0; t < kT; ++t) {
+            mfma_at(t, fa0, fb0, true);
+#pragma unroll
+            for (int q = t * kR / kT; q < (t + 1) * kR / kT; ++q) read_half(cur, 1, q, fa1, fb1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+
+        // ---- hand-off: publish block kb+1, free buffer kb for block kb+kStages
+        wait_dma_n<(kStages - 2) * kDma>();
+        wait_lds();
         __syncthreads();
-        issue_stage(s + 4, s + 4 < KS);
-        const uint8_t* nxt = stage_ptr(s + 1);
-        read_scales(nxt, nsa, nsw);
-        read_frags(nxt, na, nb);
-        if constexpr (kUe8m0) {
-            int ea[FM];
+
+        // ---- sub-step 1: K half 1 of block kb; read K half 0 of block kb+1
+        // (past the last block this reads a zero-filled buffer, unused) and
+        // DMA block kb+kStages into the freed buffer
+        const uint8_t* nxt = stage_ptr(kb + 1);
+        const int snext = kb + kStages;
+        const bool live = snext < KB;
 #pragma unroll
-            for (int i = 0; i < FM; ++i) ea[i] = ue8m0_ceil_byte(sa[i]);
-            const int eb = ue8m0_ceil_byte(sw);
+        for (int t = 0; t < kT; ++t) {
+            mfma_at(t, fa1, fb1, false);
+            if (t == 0) read_scales(nxt, nsa, nsw);
+            if constexpr (kUe8m0) {
+                // E8M0 bytes of block kb+1, half a sub-step after their reads
+                if (t == kT / 2) {
 #pragma unroll
-            for (int i = 0; i < FM; ++i)
+                    for (int i = 0; i < FM; ++i) nea[i] = ue8m0_ceil_byte(nsa[i]);
+                    neb = ue8m0_ceil_byte(nsw);
+                }
+            }
+#pragma unroll
+            for (int q = t * kR / kT; q < (t + 1) * kR / kT; ++q) read_half(nxt, 0, q, fa0, fb0);
+#pragma unroll
+            for (int d = t * kDma / kT; d < (t + 1) * kDma / kT; ++d) issue_one(snext, live, d);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (!kUe8m0) {
+            // promotion of the block: acc += part * sA[row] * sW[block]
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const float f = sa[i] * sw;
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fb[j], acc[i][j], 0, 0, 0,
-                                                                                ea[i], 0, eb);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(part[i][j][r], f, acc[i][j][r]);
+                sa[i] = nsa[i];
+            }
+            sw = nsw;
         } else {
-            // the promotion at the end of odd stage s+1 uses its block's
-            // scales; read them now, while buffer s+1 is guaranteed intact
-            if ((s & 1) == 0) read_fp32_scales(nxt);
-            const bool first_half = (s & 1) == 0;
 #pragma unroll
-            for (int i = 0; i < FM; ++i)
+            for (int i = 0; i < FM; ++i) ea[i] = nea[i];
+            eb = neb;
+        }
+    }
+    // the trailing (out-of-range) loads still target this workgroup's LDS
+    wait_dma();
+
+    // Epilogue of a tile: fp32 -> bf16 (RNE), written with raw buffer stores
+    // whose range ends at the last row of D, so rows past M (and any offset
+    // set to kOob) are dropped by the hardware and no store is branched
+    // around.  Lanes l and l + 32 hold the two 4-column halves of each
+    // 8-column run of a row; one permlane32 swap per dword pair gives each
+    // lane a whole 16-B run.  D rows that are not 16-B aligned (or N not a
+    // multiple of 8 on a ragged tile) take 2-B element stores instead.
+    auto epilogue = [&]() {
+        const int64_t bytes = std::min<int64_t>((int64_t)(a.M - m0 - 1) * a.ldd * 2 + (int64_t)a.N * 2,
+                                                (int64_t)BM * a.ldd * 2);
+        const __amdgpu_buffer_rsrc_t dD =
+            __builtin_amdgcn_make_buffer_rsrc(a.D + (int64_t)m0 * a.ldd, (short)0, (int)bytes, (int)kRsrcWord3);
+        const int h = lane >> 5;
+        const int ncol = n0 + wn * TN + 8 * h;
+        const bool vec = a.vec_store && (n0 + BN <= a.N || a.N % 8 == 0);
+        if (vec) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const bool ok = kGrouped ? a.expert_ids[m0 + wm * TM + i * 32 + (lane & 31)] == expert : true;
+                const int roff = (wm * TM + i * 32 + (lane & 31)) * (int)a.ldd * 2;
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                    for (int p = 0; p < 4; p += 2) {
+                        // dwords of runs p (X) and p + 1 (Y): columns 8 p + 4 h + {0..3}
+                        const uint32_t x0 = pack_bf16(acc[i][j][4 * p], acc[i][j][4 * p + 1]);
+                        const uint32_t x1 = pack_bf16(acc[i][j][4 * p + 2], acc[i][j][4 * p + 3]);
+                        const uint32_t y0 = pack_bf16(acc[i][j][4 * p + 4], acc[i][j][4 * p + 5]);
+                        const uint32_t y1 = pack_bf16(acc[i][j][4 * p + 6], acc[i][j][4 * p + 7]);
+                        // lanes < 32 end with run p (own half, then lane + 32's);
+                        // lanes >= 32 with run p + 1 (lane - 32's half, then own)
+                        const auto s0 = __builtin_amdgcn_permlane32_swap(x0, y0, false, false);
+                        const auto s1 = __builtin_amdgcn_permlane32_swap(x1, y1, false, false);
+                        const int n = ncol + j * 32 + 8 * p;
+                        const int voff = (ok && n < a.N) ? roff + n * 2 : kOob;
+                        const u32x4 v = {(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
+                        __builtin_amdgcn_raw_buffer_store_b128(v, dD, voff, 0, 0);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const bool ok = kGrouped ? a.expert_ids[m0 + wm * TM + i * 32 + (lane & 31)] == expert : true;
+                const int roff = (wm * TM + i * 32 + (lane & 31)) * (int)a.ldd * 2;
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
-                    part[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        fa[i], fb[j], first_half ? v16f{} : part[i][j], 0, 0, 0, 0, 0, 0);
-            if (!first_half) {
-                // promotion after both halves of the scale block:
-                // acc += part * sA[row] * sW[block]
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        const float f = sa_row_scale[i][r] * swv;
-#pragma unroll
-                        for (int j = 0; j < FN; ++j) acc[i][j][r] = fmaf(part[i][j][r], f, acc[i][j][r]);
+                        const int n = n0 + wn * TN + j * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                        const int voff = (ok && n < a.N) ? roff + n * 2 : kOob;
+                        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(pack_bf16(acc[i][j][r], 0.f) & 0xFFFFu), dD,
+                                                              voff, 0, 0);
                     }
             }
         }
-        // Interleave the stage-s MFMAs with the LDS reads of stage s+1 (two
-        // 16-B reads between consecutive MFMAs) so the reads complete under
-        // the matrix pipe.
-#pragma unroll
-        for (int i = 0; i < FM * FN; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two LDS reads
-        }
     };
 
-    // prologue
-    issue_stage(0, true);
-    issue_stage(1, KS > 1);
-    issue_stage(2, KS > 2);
-    issue_stage(3, KS > 3);
-    wait_dma_n<3 * kDmaPerStage>();
-    __syncthreads();
-    read_scales(stage_ptr(0), sa0, sw0);
-    read_frags(stage_ptr(0), fa0, fb0);
-
-    // KS is even (K is a multiple of 128)
-    for (int s = 0; s < KS; s += 2) {
-        stage(s, fa0, fb0, sa0, sw0, fa1, fb1, sa1, sw1);
-        stage(s + 1, fa1, fb1, sa1, sw1, fa0, fb0, sa0, sw0);
-    }
-
-    // epilogue: fp32 -> bf16 (RNE), masked 2-byte stores
-    const int ncol_base = n0 + wn * TN;
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int m = m0 + wm * TM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (m >= a.M) continue;
-            if constexpr (kGrouped) {
-                if (a.expert_ids[m] != expert) continue;
-            }
-            uint16_t* drow = a.D + (int64_t)m * a.ldd;
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const int n = ncol_base + j * 32 + (lane & 31);
-                if (n < a.N) drow[n] = (uint16_t)f32_to_bf16_rne(acc[i][j][r]);
-            }
-        }
-    }
+    epilogue();
 }
 
-template <int BM, int BN, int WM, int WN, bool kUe8m0, bool kGrouped>
+template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped>
 static int launch_gemm(GemmArgs a, hipStream_t st, const char* what) {
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
     const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n;
     KBN_CHECK_ARG(blocks <= 0x7FFFFFFFLL, "%s: too many tiles", what);
-    gemm_bs_kernel<BM, BN, WM, WN, kUe8m0, kGrouped><<<dim3((unsigned)blocks), dim3(64 * WM * WN), 0, st>>>(a);
+    gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a);
     KBN_CHECK_LAUNCH(what);
     return 0;
 }
@@ -380,8 +457,8 @@ static int check_common(const char* what, const void* A, int64_t lda, const void
                   "%s: A and W rows must be 16-byte aligned", what);
     KBN_CHECK_ARG(((reinterpret_cast<uintptr_t>(D) & 1u) == 0), "%s: D must be 2-byte aligned", what);
     // every per-tile byte offset handed to the buffer unit must fit 32 bits
-    KBN_CHECK_ARG(lda * 256 + K < 0x7FFFFFFFLL && ldw * 256 + K < 0x7FFFFFFFLL, "%s: leading dimension too large",
-                  what);
+    KBN_CHECK_ARG(lda * 256 + K < 0x7FFFFFFFLL && ldw * 256 + K < 0x7FFFFFFFLL && ldd * 2 * 256 < 0x7FFFFFFFLL,
+                  "%s: leading dimension too large", what);
     return 0;
 }
 
@@ -419,14 +496,15 @@ extern "C" int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int6
     a.W = (const uint8_t*)W; a.ldw = ldw; a.w_estride = 0;
     a.sW = sW; a.sW_ld = sW_ld; a.sW_estride = 0;
     a.D = (uint16_t*)D_bf16; a.ldd = ldd;
+    a.vec_store = (reinterpret_cast<uintptr_t>(D_bf16) % 16 == 0) && (ldd % 8 == 0);
     a.expert_ids = nullptr;
     a.M = (int)M; a.N = (int)N; a.K = (int)K; a.E = 1;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (scale_ue8m0) {
-        if (M > 128) return launch_gemm<256, 256, 2, 2, true, false>(a, st, what);
-        return launch_gemm<128, 128, 2, 2, true, false>(a, st, what);
+        if (M > 128) return launch_gemm<256, 256, 2, true, false>(a, st, what);
+        return launch_gemm<128, 128, 4, true, false>(a, st, what);
     }
-    return launch_gemm<128, 128, 2, 2, false, false>(a, st, what);
+    return launch_gemm<128, 128, 4, false, false>(a, st, what);
 }
 
 extern "C" int kbn_fp8_grouped_gemm_nt_contiguous(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
@@ -449,10 +527,11 @@ extern "C" int kbn_fp8_grouped_gemm_nt_contiguous(const void* A, int64_t lda, co
     a.W = (const uint8_t*)B; a.ldw = K; a.w_estride = N * K;
     a.sW = sB; a.sW_ld = KB; a.sW_estride = NB * KB;
     a.D = (uint16_t*)C_bf16; a.ldd = ldc;
+    a.vec_store = (reinterpret_cast<uintptr_t>(C_bf16) % 16 == 0) && (ldc % 8 == 0);
     a.expert_ids = expert_ids;
     KBN_CHECK_ARG(E <= 0x7FFFFFFFLL, "%s: too many experts", what);
     a.M = (int)M_sum; a.N = (int)N; a.K = (int)K; a.E = (int)E;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (scale_ue8m0) return launch_gemm<128, 256, 2, 2, true, true>(a, st, what);
-    return launch_gemm<128, 128, 2, 2, false, true>(a, st, what);
+    if (scale_ue8m0) return launch_gemm<128, 256, 3, true, true>(a, st, what);
+    return launch_gemm<128, 128, 4, false, true>(a, st, what);
 }

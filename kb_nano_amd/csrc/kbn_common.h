@@ -35,6 +35,19 @@ void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Compute units of the current device (cached per device).
+inline int cu_count() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cache[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cache[dev] = n;
+    }
+    return cache[dev];
+}
+
 // ------------------------------------------------------------ constants ---
 
 constexpr int kGroup = 128;          // 1x128 activation groups, 128x128 weight blocks

@@ -182,18 +182,6 @@ __global__ void silu_bf16_debug_kernel(const uint16_t* __restrict__ g, uint16_t*
     if (i < n) out[i] = kSiluLut[g[i]];
 }
 
-// Compute units of the current device (cached per device).
-static int cu_count() {
-    static int cache[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cache[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cache[dev] = n;
-    }
-    return cache[dev];
-}
 
 // Row slices per XCD (multiples of 32 rows) and the number of workgroups
 // per XCD: at most `per_cu` per CU, never more than the slice needs.
