@@ -207,6 +207,35 @@ def bench_moe(steps, warmup, dev):
     return res
 
 
+PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "silu_mul_quant_cfg2.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the headline kernel, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (each counter scaled by what it
+    reads for a plain 1 GiB copy); None when the summary is absent."""
+    try:
+        with open(PROFILE_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
+def copy_calibration(iters=3):
+    """A plain 1 GiB device-to-device copy, the known-size reference for the
+    FETCH_SIZE/WRITE_SIZE scale factors (run under rocprofv3 --pmc)."""
+    import torch
+    x = torch.empty(1 << 30, dtype=torch.uint8, device="cuda:0")
+    y = torch.empty_like(x)
+    for _ in range(iters):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(f"copied {iters} x {1 << 30} bytes", flush=True)
+
+
 def cpu_baseline_silu():
     """The C oracle (a port of the reference algorithm) on the host cores,
     over the full config-2 workload; median of 3 runs."""
@@ -241,6 +270,8 @@ def main():
     ap.add_argument("--only", default="all",
                     help="comma list of extra sections: quant,dsv3,moe,decode (default all; 'none' = headline only)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run three 1 GiB device copies (reference for rocprofv3 byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): this build covers the "
@@ -253,6 +284,9 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     from kb_nano_amd._lib import require_gfx950
     require_gfx950(0)
 
@@ -301,7 +335,7 @@ def main():
                                "fp8 [8192, 18432] + fp32 column-major scales [8192, 144]",
                    "M": 8192, "N_half": 18432, "algorithmic_bytes": head["bytes"]},
         "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "extra": extra,
     }
