@@ -83,6 +83,26 @@ int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int64_t sA_stri
                     int scale_ue8m0, void* stream);
 
 /*
+ * kbn_fp8_gemm_nt with a caller-provided workspace: shapes whose tile grid
+ * would leave CUs idle (small M, or few N tiles) split K across workgroups,
+ * write fp32 partial sums into `workspace` and reduce them in a second
+ * launch on the same stream (in a fixed order, so results are deterministic
+ * and equal for any split count up to fp32 summation order).
+ * kbn_fp8_gemm_nt_workspace_bytes returns the bytes this needs for a shape on
+ * the current device (0: no split, workspace unused).  A null or smaller
+ * workspace runs the unsplit kernel.  The workspace must be 16-byte aligned
+ * and must not be used by another call that may run concurrently.
+ * No counterpart in the reference (DeepGEMM allocates internally); this is
+ * the entry point the Python op kb_nano_fp8::fp8_gemm_nt calls, with a
+ * workspace from the PyTorch caching allocator.
+ */
+int64_t kbn_fp8_gemm_nt_workspace_bytes(int64_t M, int64_t N, int64_t K, int scale_ue8m0);
+int kbn_fp8_gemm_nt_ws(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m, int64_t sA_stride_k,
+                       const void* W, int64_t ldw, const float* sW, int64_t sW_ld,
+                       void* D_bf16, int64_t ldd, int64_t M, int64_t N, int64_t K,
+                       int scale_ue8m0, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Contiguous-layout grouped FP8 GEMM (MoE experts).
  * Replaces op kb_nano_fp8_moe::m_grouped_gemm_nt_contiguous ->
  * deep_gemm.m_grouped_fp8_gemm_nt_contiguous

@@ -24,6 +24,9 @@ SIGNATURES = {
     "kbn_per_token_group_quant_fp8": ([_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _F, _I, _P], _I),
     "kbn_silu_mul_quant_fp8": ([_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _F, _I, _P], _I),
     "kbn_fp8_gemm_nt": ([_P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _P], _I),
+    "kbn_fp8_gemm_nt_workspace_bytes": ([_I64, _I64, _I64, _I], _I64),
+    "kbn_fp8_gemm_nt_ws": (
+        [_P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P], _I),
     "kbn_fp8_grouped_gemm_nt_contiguous": (
         [_P, _I64, _P, _I64, _I64, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _P], _I),
     "kbn_debug_silu_bf16": ([_P, _P, _I64, _P], _I),

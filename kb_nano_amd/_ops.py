@@ -137,10 +137,32 @@ def fp8_gemm_nt(q_input: torch.Tensor, input_scale: torch.Tensor, weight: torch.
     if q_input.stride(1) != 1 or weight.stride(1) != 1 or output.stride(1) != 1 or weight_scale.stride(1) != 1:
         raise ValueError(f"{what}: operands must be contiguous along K (and N for the output)")
     ue8m0 = is_e8m0_used() if use_ue8m0 is None else bool(use_ue8m0)
-    check(lib().kbn_fp8_gemm_nt(
+    if M == 0 or N == 0:
+        return
+    L = lib()
+    # small-M / few-tile shapes split K over more workgroups; the fp32
+    # partials live in a workspace from the caching allocator (stream-ordered
+    # on the launch stream, so concurrent streams never share one)
+    ws_bytes = _gemm_workspace_bytes(L, output.device, M, N, K, ue8m0)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=output.device) if ws_bytes else None
+    check(L.kbn_fp8_gemm_nt_ws(
         q_input.data_ptr(), q_input.stride(0), input_scale.data_ptr(), input_scale.stride(0), input_scale.stride(1),
         weight.data_ptr(), weight.stride(0), weight_scale.data_ptr(), weight_scale.stride(0),
-        output.data_ptr(), output.stride(0), M, N, K, int(ue8m0), _stream(output)), what)
+        output.data_ptr(), output.stride(0), M, N, K, int(ue8m0),
+        ws.data_ptr() if ws is not None else None, ws_bytes, _stream(output)), what)
+
+
+_WS_CACHE: dict = {}
+
+
+def _gemm_workspace_bytes(L, device, M, N, K, ue8m0) -> int:
+    key = (device.index, M, N, K, ue8m0)
+    n = _WS_CACHE.get(key)
+    if n is None:
+        with torch.cuda.device(device):
+            n = int(L.kbn_fp8_gemm_nt_workspace_bytes(M, N, K, int(ue8m0)))
+        _WS_CACHE[key] = n
+    return n
 
 
 def m_grouped_gemm_nt_contiguous(a_fp8: torch.Tensor, a_scale: torch.Tensor, b_fp8: torch.Tensor,

@@ -55,6 +55,12 @@ struct GemmArgs {
     int M, N, K, E;
     int tiles_m, tiles_n;
     int vec_store;               // D rows allow aligned 16-B stores
+    // split-K: workgroup (tile, split) accumulates K blocks
+    // [split * kb_per_split, +kb_per_split) into fp32 partials
+    // P[split][m][n] (row stride ldp), summed by splitk_reduce_kernel
+    float* P;
+    int64_t ldp;
+    int splits, kb_per_split;
 };
 
 // Raw buffer descriptor (base, byte range) built from uniform values so it
@@ -106,16 +112,19 @@ __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 constexpr int kRowB = 128;   // LDS row bytes = K per stage = one scale block
 
 // XCD-aware tile order.  Consecutive workgroup ids are dispatched round-robin
-// over the 8 XCDs; give each XCD a contiguous range of the tile sequence so
-// the tiles resident on one XCD (and its L2) share A row panels and W panels,
-// and walk that sequence in column groups of kGroupM row tiles.
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
+// over the 8 XCDs; give each XCD a contiguous range of the (tile, split)
+// sequence so the tiles resident on one XCD (and its L2) share A row panels
+// and W panels, and walk that sequence in column groups of kGroupM row tiles
+// (the K splits of one tile are neighbours).
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int splits, int& tm, int& tn, int& split) {
     constexpr int kGroupM = 4;
     const int nblk = gridDim.x;
     const int bid = blockIdx.x;
     const int xcd = bid & 7, i = bid >> 3;
     const int per = nblk >> 3, rem = nblk & 7;
-    const int t = xcd * per + (xcd < rem ? xcd : rem) + i;
+    const int ts = xcd * per + (xcd < rem ? xcd : rem) + i;
+    const int t = ts / splits;
+    split = ts - t * splits;
     const int group = kGroupM * tiles_n;
     const int g = t / group;
     const int first_m = g * kGroupM;
@@ -151,7 +160,7 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 //               of K half 0 (and the scales) of block kb+1.
 // So kStages-1 blocks are in flight while one is consumed, and no fragment
 // register set is ever copied.
-template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped>
+template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, bool kSplitK>
 __global__ __launch_bounds__(256, 1) void gemm_bs_kernel(const GemmArgs a) {
     constexpr int WN = 2;
     constexpr int TM = BM / 2, TN = BN / 2;     // wavefront tile
@@ -165,13 +174,15 @@ __global__ __launch_bounds__(256, 1) void gemm_bs_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStage];
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)smem);
 
-    int tm, tn;
-    tile_coords(a.tiles_m, a.tiles_n, tm, tn);
+    int tm, tn, split = 0;
+    tile_coords(a.tiles_m, a.tiles_n, kSplitK ? a.splits : 1, tm, tn, split);
     const int m0 = tm * BM, n0 = tn * BN;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WN, wn = wave % WN;
-    const int KB = a.K / kRowB;                  // K blocks
+    // K blocks of this workgroup: [kb0, kb0 + KB)
+    const int kb0 = kSplitK ? split * a.kb_per_split : 0;
+    const int KB = kSplitK ? min(a.K / kRowB - kb0, a.kb_per_split) : a.K / kRowB;
     const int NB = (a.N + kGroup - 1) / kGroup;
 
     const uint8_t* Wbase = a.W;
@@ -197,17 +208,17 @@ __global__ __launch_bounds__(256, 1) void gemm_bs_kernel(const GemmArgs a) {
     const int drow = lane >> 3;
     const int ch_e = ((lane & 7) ^ (lane >> 4)) << 4;
     const int ch_o = ((lane & 7) ^ ((lane >> 4) | 4)) << 4;
-    const int a_e = (int)((wave * kAInstr * 8 + drow) * a.lda) + ch_e;
+    const int a_e = (int)((wave * kAInstr * 8 + drow) * a.lda) + ch_e + kb0 * kRowB;
     const int a_o = a_e - ch_e + ch_o;
-    const int w_e = (int)((wave * kBInstr * 8 + drow) * a.ldw) + ch_e;
+    const int w_e = (int)((wave * kBInstr * 8 + drow) * a.ldw) + ch_e + kb0 * kRowB;
     const int w_o = w_e - ch_e + ch_o;
     const int sa_row = wave * 64 + lane;
     const bool sa_live = (sa_row < BM) & (m0 + sa_row < a.M);
-    const int sa_off0 = sa_live ? (int)((int64_t)(m0 + sa_row) * a.sA_sm * 4) : kOob;
     const int sa_kstep = sa_live ? (int)(a.sA_sk * 4) : 0;
+    const int sa_off0 = sa_live ? (int)((int64_t)(m0 + sa_row) * a.sA_sm * 4) + kb0 * sa_kstep : kOob;
     const bool sw_live = (lane < (BN + 127) / 128) & (n0 / 128 + lane < NB);
-    const int sw_off0 = sw_live ? (n0 / 128 + lane) * (int)a.sW_ld * 4 : kOob;
     const int sw_kstep = sw_live ? 4 : 0;
+    const int sw_off0 = sw_live ? (n0 / 128 + lane) * (int)a.sW_ld * 4 + kb0 * 4 : kOob;
     constexpr int kDma = kAInstr + kBInstr + 2;  // DMA instructions per wave per stage
 
     // DMA instruction d (0 <= d < kDma) of K block s -> LDS buffer s % kStages:
@@ -378,6 +389,30 @@ __global__ __launch_bounds__(256, 1) void gemm_bs_kernel(const GemmArgs a) {
     // 8-column run of a row; one permlane32 swap per dword pair gives each
     // lane a whole 16-B run.  D rows that are not 16-B aligned (or N not a
     // multiple of 8 on a ragged tile) take 2-B element stores instead.
+    // Split-K epilogue: the fp32 partial sums, one 16-B store per run of four
+    // columns, into this split's slab of P (same dropped-store masking).
+    auto epilogue_partial = [&]() {
+        // whole padded rows: a run that starts below N may end in the padding
+        const int64_t bytes = std::min<int64_t>((int64_t)(a.M - m0) * a.ldp * 4, (int64_t)BM * a.ldp * 4);
+        const __amdgpu_buffer_rsrc_t dP = __builtin_amdgcn_make_buffer_rsrc(
+            a.P + ((int64_t)split * a.M + m0) * a.ldp, (short)0, (int)bytes, (int)kRsrcWord3);
+        const int ncol = n0 + wn * TN + 4 * (lane >> 5);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int roff = (wm * TM + i * 32 + (lane & 31)) * (int)a.ldp * 4;
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const int n = ncol + j * 32 + 8 * p;
+                    const int voff = n < a.N ? roff + n * 4 : kOob;
+                    const v4i v = {__float_as_int(acc[i][j][4 * p]), __float_as_int(acc[i][j][4 * p + 1]),
+                                   __float_as_int(acc[i][j][4 * p + 2]), __float_as_int(acc[i][j][4 * p + 3])};
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), dP, voff, 0, 0);
+                }
+        }
+    };
+
     auto epilogue = [&]() {
         const int64_t bytes = std::min<int64_t>((int64_t)(a.M - m0 - 1) * a.ldd * 2 + (int64_t)a.N * 2,
                                                 (int64_t)BM * a.ldd * 2);
@@ -429,16 +464,85 @@ __global__ __launch_bounds__(256, 1) void gemm_bs_kernel(const GemmArgs a) {
         }
     };
 
-    epilogue();
+    if constexpr (kSplitK)
+        epilogue_partial();
+    else
+        epilogue();
+}
+
+// D[m, n] = bf16(sum_s P[s][m][n]), summed in split order (deterministic).
+// One thread per run of four columns.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ P, int64_t ldp, int splits,
+                                                            int M, int N, uint16_t* __restrict__ D, int64_t ldd,
+                                                            int vec_store) {
+    const int runs = (N + 3) >> 2;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)M * runs) return;
+    const int m = (int)(idx / runs);
+    const int n = (int)(idx - (int64_t)m * runs) * 4;
+    const int64_t slab = (int64_t)M * ldp;
+    const float* p = P + (int64_t)m * ldp + n;
+    float4 acc = *reinterpret_cast<const float4*>(p);
+    for (int sp = 1; sp < splits; ++sp) {
+        const float4 v = *reinterpret_cast<const float4*>(p + sp * slab);
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+    }
+    uint16_t* d = D + (int64_t)m * ldd + n;
+    const uint32_t lo = pack_bf16(acc.x, acc.y), hi = pack_bf16(acc.z, acc.w);
+    if (vec_store && n + 3 < N) {
+        *reinterpret_cast<uint2*>(d) = make_uint2(lo, hi);
+    } else {
+        if (n < N) d[0] = (uint16_t)lo;
+        if (n + 1 < N) d[1] = (uint16_t)(lo >> 16);
+        if (n + 2 < N) d[2] = (uint16_t)hi;
+        if (n + 3 < N) d[3] = (uint16_t)(hi >> 16);
+    }
+}
+
+// Split-K plan for a tile grid: the number of K splits that minimises the
+// estimated makespan (waves of one workgroup per CU, each costing its K
+// blocks plus a fixed pipeline fill of about two blocks).
+struct SplitPlan {
+    int splits = 1, kb_per_split = 0;
+};
+static SplitPlan plan_splits(int64_t tiles, int KB, int cus) {
+    SplitPlan best;
+    best.kb_per_split = KB;
+    if (tiles <= 0 || KB < 8 || tiles >= cus) return best;
+    double best_cost = 1e30;
+    for (int s = 1; s <= 32 && s <= KB / 4; ++s) {
+        const int kbps = (KB + s - 1) / s;
+        const int ss = (KB + kbps - 1) / kbps;
+        const int64_t wgs = tiles * ss;
+        const double cost = (double)((wgs + cus - 1) / cus) * (kbps + 2.0);
+        if (cost < best_cost - 1e-9) {
+            best_cost = cost;
+            best.splits = ss;
+            best.kb_per_split = kbps;
+        }
+    }
+    return best;
 }
 
 template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped>
 static int launch_gemm(GemmArgs a, hipStream_t st, const char* what) {
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
-    const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n;
+    const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
+    const int64_t blocks = tiles * (a.splits > 1 ? a.splits : 1);
     KBN_CHECK_ARG(blocks <= 0x7FFFFFFFLL, "%s: too many tiles", what);
-    gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a);
+    if (!kGrouped && a.splits > 1) {
+        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped && false, true><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a);
+        KBN_CHECK_LAUNCH(what);
+        const int64_t threads = (int64_t)a.M * ((a.N + 3) / 4);
+        splitk_reduce_kernel<<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st>>>(
+            a.P, a.ldp, a.splits, a.M, a.N, a.D, a.ldd, a.vec_store);
+    } else {
+        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped, false><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a);
+    }
     KBN_CHECK_LAUNCH(what);
     return 0;
 }
@@ -477,11 +581,30 @@ static int check_scale_ranges(const char* what, int64_t M, int64_t K, int64_t sm
     return 0;
 }
 
-extern "C" int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
-                               int64_t sA_stride_k, const void* W, int64_t ldw, const float* sW, int64_t sW_ld,
-                               void* D_bf16, int64_t ldd, int64_t M, int64_t N, int64_t K, int scale_ue8m0,
-                               void* stream) {
-    const char* what = "fp8_gemm_nt";
+// Tile configuration of the dense GEMM for a shape.  UE8M0: 256x256 tiles
+// (2 LDS stages) when M > 128, 128x128 (4 stages) for 64 < M <= 128 and
+// 64x256 (3 stages) for M <= 64, where the weights dominate the traffic and
+// a short M tile wastes the least MFMA work.  FP32 contract: 128x128.
+struct DenseCfg {
+    int bm, bn;
+};
+static DenseCfg dense_cfg(int64_t M, int ue8m0) {
+    if (!ue8m0) return {128, 128};
+    if (M > 128) return {256, 256};
+    if (M > 64) return {128, 128};
+    return {64, 256};
+}
+static int64_t round_up4(int64_t n) { return (n + 3) / 4 * 4; }
+static SplitPlan dense_plan(int64_t M, int64_t N, int64_t K, int ue8m0) {
+    const DenseCfg c = dense_cfg(M, ue8m0);
+    const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+    return plan_splits(tiles, (int)(K / kGroup), cu_count());
+}
+
+static int gemm_nt_impl(const char* what, const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
+                        int64_t sA_stride_k, const void* W, int64_t ldw, const float* sW, int64_t sW_ld, void* D_bf16,
+                        int64_t ldd, int64_t M, int64_t N, int64_t K, int scale_ue8m0, void* workspace,
+                        int64_t workspace_bytes, void* stream) {
     if (int rc = check_common(what, A, lda, W, ldw, D_bf16, ldd, M, N, K)) return rc;
     if (M == 0 || N == 0) return 0;
     KBN_CHECK_ARG(K > 0, "%s: K must be positive", what);
@@ -499,12 +622,49 @@ extern "C" int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int6
     a.vec_store = (reinterpret_cast<uintptr_t>(D_bf16) % 16 == 0) && (ldd % 8 == 0);
     a.expert_ids = nullptr;
     a.M = (int)M; a.N = (int)N; a.K = (int)K; a.E = 1;
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (scale_ue8m0) {
-        if (M > 128) return launch_gemm<256, 256, 2, true, false>(a, st, what);
-        return launch_gemm<128, 128, 4, true, false>(a, st, what);
+    a.splits = 1;
+    a.kb_per_split = (int)(K / kGroup);
+    if (workspace) {
+        const SplitPlan sp = dense_plan(M, N, K, scale_ue8m0);
+        const int64_t ldp = round_up4(N);
+        const int64_t need = (int64_t)sp.splits * M * ldp * 4;
+        if (sp.splits > 1 && workspace_bytes >= need) {
+            KBN_CHECK_ARG(aligned16(workspace), "%s: workspace must be 16-byte aligned", what);
+            KBN_CHECK_ARG(ldp * 4 * 256 < 0x7FFFFFFFLL, "%s: N too large for split-K", what);
+            a.P = (float*)workspace;
+            a.ldp = ldp;
+            a.splits = sp.splits;
+            a.kb_per_split = sp.kb_per_split;
+        }
     }
-    return launch_gemm<128, 128, 4, false, false>(a, st, what);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const DenseCfg c = dense_cfg(M, scale_ue8m0);
+    if (!scale_ue8m0) return launch_gemm<128, 128, 4, false, false>(a, st, what);
+    if (c.bm == 256) return launch_gemm<256, 256, 2, true, false>(a, st, what);
+    if (c.bm == 128) return launch_gemm<128, 128, 4, true, false>(a, st, what);
+    return launch_gemm<64, 256, 3, true, false>(a, st, what);
+}
+
+extern "C" int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
+                               int64_t sA_stride_k, const void* W, int64_t ldw, const float* sW, int64_t sW_ld,
+                               void* D_bf16, int64_t ldd, int64_t M, int64_t N, int64_t K, int scale_ue8m0,
+                               void* stream) {
+    return gemm_nt_impl("fp8_gemm_nt", A, lda, sA, sA_stride_m, sA_stride_k, W, ldw, sW, sW_ld, D_bf16, ldd, M, N,
+                        K, scale_ue8m0, nullptr, 0, stream);
+}
+
+extern "C" int64_t kbn_fp8_gemm_nt_workspace_bytes(int64_t M, int64_t N, int64_t K, int scale_ue8m0) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % kGroup != 0 || M > 0x7FFFFFFFLL || N > 0x7FFFFFFFLL) return 0;
+    const SplitPlan sp = dense_plan(M, N, K, scale_ue8m0);
+    return sp.splits > 1 ? (int64_t)sp.splits * M * round_up4(N) * 4 : 0;
+}
+
+extern "C" int kbn_fp8_gemm_nt_ws(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
+                                  int64_t sA_stride_k, const void* W, int64_t ldw, const float* sW, int64_t sW_ld,
+                                  void* D_bf16, int64_t ldd, int64_t M, int64_t N, int64_t K, int scale_ue8m0,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
+    return gemm_nt_impl("fp8_gemm_nt_ws", A, lda, sA, sA_stride_m, sA_stride_k, W, ldw, sW, sW_ld, D_bf16, ldd, M,
+                        N, K, scale_ue8m0, workspace, workspace_bytes, stream);
 }
 
 extern "C" int kbn_fp8_grouped_gemm_nt_contiguous(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,

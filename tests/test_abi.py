@@ -68,6 +68,28 @@ def test_gemm_rejects_bad_shapes():
     assert "aligned" in _err()
 
 
+def test_gemm_workspace_query():
+    """The split-K plan only asks for a workspace when the tile grid would
+    leave CUs idle, and then for whole [splits, M, roundup(N, 4)] fp32 slabs."""
+    from kb_nano_amd._lib import lib
+    L = lib()
+    assert L.kbn_fp8_gemm_nt_workspace_bytes(4096, 36864, 7168, 1) == 0   # 2304 tiles: no split
+    assert L.kbn_fp8_gemm_nt_workspace_bytes(8, 8192, 100, 1) == 0        # K not a multiple of 128
+    assert L.kbn_fp8_gemm_nt_workspace_bytes(0, 8192, 8192, 1) == 0
+    for M, N, K in ((128, 7168, 18432), (1, 8192, 28672), (77, 203, 2048)):
+        n = L.kbn_fp8_gemm_nt_workspace_bytes(M, N, K, 1)
+        slab = M * ((N + 3) // 4 * 4) * 4
+        assert n > 0 and n % slab == 0 and 2 <= n // slab <= 32, (M, N, K, n)
+
+
+def test_gemm_ws_rejects_bad_shapes():
+    from kb_nano_amd._lib import lib
+    L = lib()
+    assert L.kbn_fp8_gemm_nt_ws(None, 128, None, 1, 1, None, 128, None, 1, None, 128, 8, 128, 100, 1,
+                                None, 0, None) == 1
+    assert "multiple of 128" in _err()
+
+
 def test_grouped_rejects_unaligned_m_sum():
     from kb_nano_amd._lib import lib
     p = ctypes.c_void_p(4096)  # never dereferenced: validation fails first

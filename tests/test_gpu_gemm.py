@@ -108,6 +108,45 @@ def test_gemm_dsv3_shapes_sampled(gpu_device, name, N, K, M):
     assert_gemm_close(got, ref, f"{name} M={M}")
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 7168, 18432), (8, 8192, 8192), (64, 1024, 28672), (100, 7168, 16384),
+                                   (77, 203, 2048), (256, 768, 4096)])
+@pytest.mark.parametrize("ue8m0", [True, False])
+def test_gemm_split_k_matches_unsplit(gpu_device, M, N, K, ue8m0):
+    """Split-K (fp32 partials in a workspace + ordered reduction) against the
+    oracle and against the unsplit kernel (kbn_fp8_gemm_nt, no workspace):
+    both within tolerance, and equal up to fp32 summation order."""
+    import ctypes
+
+    from kb_nano_amd._lib import lib
+    from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
+    L = lib()
+    ws = L.kbn_fp8_gemm_nt_workspace_bytes(M, N, K, int(ue8m0))
+    assert ws > 0, "shape expected to split"
+    qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=N + K)
+    if not ue8m0:
+        sw = (sw * np.float32(1.37)).astype(np.float32)
+    cols = np.unique(np.concatenate([[0, N - 1], np.random.default_rng(K).integers(0, N, 94)]))
+    ref = oracle.gemm_nt_sample(qa, sa, qw, sw, ue8m0=ue8m0, cols=cols)
+    A = to_fp8(qa, gpu_device)
+    sA = _alloc_colmajor_scale(M, K // 128, gpu_device)
+    sA.copy_(torch.from_numpy(sa))
+    W, sW = to_fp8(qw, gpu_device), torch.from_numpy(sw).to(gpu_device)
+    outs = []
+    for split in (False, True):
+        D = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu_device)
+        buf = torch.empty(ws, dtype=torch.uint8, device=gpu_device) if split else None
+        rc = L.kbn_fp8_gemm_nt_ws(A.data_ptr(), K, sA.data_ptr(), 1, M, W.data_ptr(), K, sW.data_ptr(), K // 128,
+                                  D.data_ptr(), N, M, N, K, int(ue8m0),
+                                  ctypes.c_void_p(buf.data_ptr()) if split else None, ws if split else 0,
+                                  torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, L.kbn_last_error()
+        torch.cuda.synchronize()
+        assert_gemm_close(D[:, torch.from_numpy(cols).to(gpu_device)], ref, f"split={split} {M}x{N}x{K}")
+        outs.append(D.float())
+    diff = (outs[0] - outs[1]).abs()
+    assert torch.all(diff <= 1e-2 * outs[0].abs() + 1e-3), float(diff.max())
+
+
 # ------------------------------------------------------------- Fp8Linear
 
 def test_fp8_linear_end_to_end(gpu_device):
