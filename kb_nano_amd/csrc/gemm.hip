@@ -55,11 +55,12 @@ struct GemmArgs {
     int M, N, K, E;
     int tiles_m, tiles_n;
     int vec_store;               // D rows allow aligned 16-B stores
-    // split-K: workgroup (tile, split) accumulates K blocks
-    // [split * kb_per_split, +kb_per_split) into fp32 partials
-    // P[split][m][n] (row stride ldp), summed by splitk_reduce_kernel
+    // This launch covers tiles [tile_base, tile_base + tile_count) of the
+    // grouped tile order.  Split-K: workgroup (tile, split) accumulates K
+    // blocks [split * kb_per_split, +kb_per_split) into the fp32 slab
+    // P[split][tile - tile_base][BM][BN], summed by splitk_reduce_kernel.
+    int tile_base, tile_count;
     float* P;
-    int64_t ldp;
     int splits, kb_per_split;
 };
 
@@ -116,15 +117,17 @@ constexpr int kRowB = 128;   // LDS row bytes = K per stage = one scale block
 // sequence so the tiles resident on one XCD (and its L2) share A row panels
 // and W panels, and walk that sequence in column groups of kGroupM row tiles
 // (the K splits of one tile are neighbours).
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int splits, int& tm, int& tn, int& split) {
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int tile_base, int splits, int& tm, int& tn,
+                                            int& trel, int& split) {
     constexpr int kGroupM = 4;
     const int nblk = gridDim.x;
     const int bid = blockIdx.x;
     const int xcd = bid & 7, i = bid >> 3;
     const int per = nblk >> 3, rem = nblk & 7;
     const int ts = xcd * per + (xcd < rem ? xcd : rem) + i;
-    const int t = ts / splits;
-    split = ts - t * splits;
+    trel = ts / splits;
+    split = ts - trel * splits;
+    const int t = tile_base + trel;
     const int group = kGroupM * tiles_n;
     const int g = t / group;
     const int first_m = g * kGroupM;
@@ -161,7 +164,8 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 // So kStages-1 blocks are in flight while one is consumed, and no fragment
 // register set is ever copied.
 template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, bool kSplitK>
-__global__ __launch_bounds__(256, 1) void gemm_bs_kernel(const GemmArgs a) {
+__global__ __launch_bounds__(256, (kStages * (BM + BN) * 128 + kStages * 2048 <= 80 * 1024) ? 2 : 1) void
+gemm_bs_kernel(const GemmArgs a) {
     constexpr int WN = 2;
     constexpr int TM = BM / 2, TN = BN / 2;     // wavefront tile
     constexpr int FM = TM / 32, FN = TN / 32;   // 32x32 fragments per wavefront
@@ -174,8 +178,8 @@ __global__ __launch_bounds__(256, 1) void gemm_bs_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStage];
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)smem);
 
-    int tm, tn, split = 0;
-    tile_coords(a.tiles_m, a.tiles_n, kSplitK ? a.splits : 1, tm, tn, split);
+    int tm, tn, trel = 0, split = 0;
+    tile_coords(a.tiles_m, a.tiles_n, a.tile_base, kSplitK ? a.splits : 1, tm, tn, trel, split);
     const int m0 = tm * BM, n0 = tn * BN;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -390,22 +394,21 @@ __global__ __launch_bounds__(256, 1) void gemm_bs_kernel(const GemmArgs a) {
     // lane a whole 16-B run.  D rows that are not 16-B aligned (or N not a
     // multiple of 8 on a ragged tile) take 2-B element stores instead.
     // Split-K epilogue: the fp32 partial sums, one 16-B store per run of four
-    // columns, into this split's slab of P (same dropped-store masking).
+    // columns, into this (split, tile)'s BM x BN slab (rows past M dropped by
+    // the range).
     auto epilogue_partial = [&]() {
-        // whole padded rows: a run that starts below N may end in the padding
-        const int64_t bytes = std::min<int64_t>((int64_t)(a.M - m0) * a.ldp * 4, (int64_t)BM * a.ldp * 4);
+        const int64_t bytes = (int64_t)min(a.M - m0, BM) * BN * 4;
         const __amdgpu_buffer_rsrc_t dP = __builtin_amdgcn_make_buffer_rsrc(
-            a.P + ((int64_t)split * a.M + m0) * a.ldp, (short)0, (int)bytes, (int)kRsrcWord3);
-        const int ncol = n0 + wn * TN + 4 * (lane >> 5);
+            a.P + ((int64_t)split * a.tile_count + trel) * BM * BN, (short)0, (int)bytes, (int)kRsrcWord3);
+        const int ncol = wn * TN + 4 * (lane >> 5);
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
-            const int roff = (wm * TM + i * 32 + (lane & 31)) * (int)a.ldp * 4;
+            const int roff = (wm * TM + i * 32 + (lane & 31)) * BN * 4;
 #pragma unroll
             for (int j = 0; j < FN; ++j)
 #pragma unroll
                 for (int p = 0; p < 4; ++p) {
-                    const int n = ncol + j * 32 + 8 * p;
-                    const int voff = n < a.N ? roff + n * 4 : kOob;
+                    const int voff = roff + (ncol + j * 32 + 8 * p) * 4;
                     const v4i v = {__float_as_int(acc[i][j][4 * p]), __float_as_int(acc[i][j][4 * p + 1]),
                                    __float_as_int(acc[i][j][4 * p + 2]), __float_as_int(acc[i][j][4 * p + 3])};
                     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), dP, voff, 0, 0);
@@ -470,80 +473,146 @@ __global__ __launch_bounds__(256, 1) void gemm_bs_kernel(const GemmArgs a) {
         epilogue();
 }
 
-// D[m, n] = bf16(sum_s P[s][m][n]), summed in split order (deterministic).
-// One thread per run of four columns.
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ P, int64_t ldp, int splits,
-                                                            int M, int N, uint16_t* __restrict__ D, int64_t ldd,
-                                                            int vec_store) {
-    const int runs = (N + 3) >> 2;
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (int64_t)M * runs) return;
-    const int m = (int)(idx / runs);
-    const int n = (int)(idx - (int64_t)m * runs) * 4;
-    const int64_t slab = (int64_t)M * ldp;
-    const float* p = P + (int64_t)m * ldp + n;
-    float4 acc = *reinterpret_cast<const float4*>(p);
-    for (int sp = 1; sp < splits; ++sp) {
-        const float4 v = *reinterpret_cast<const float4*>(p + sp * slab);
-        acc.x += v.x;
-        acc.y += v.y;
-        acc.z += v.z;
-        acc.w += v.w;
+// Split-K reduction: D = bf16(sum_s slab[s]) summed in split order
+// (deterministic).  One workgroup per 8-row strip of a tile of the split
+// launch (blockIdx.x = tile * BM/8 + strip), one float4 run per lane.
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a) {
+    constexpr int kRuns = BN / 4, kRows = 256 / kRuns;   // rows per pass of the workgroup
+    constexpr int kStrips = BM / 8;
+    const int trel = blockIdx.x / kStrips, strip = blockIdx.x - trel * kStrips;
+    int tm, tn;
+    {
+        constexpr int kGroupM = 4;
+        const int t = a.tile_base + trel;
+        const int group = kGroupM * a.tiles_n;
+        const int g = t / group;
+        const int first_m = g * kGroupM;
+        const int gm = min(a.tiles_m - first_m, kGroupM);
+        const int w = t - g * group;
+        tm = first_m + w % gm;
+        tn = w / gm;
     }
-    uint16_t* d = D + (int64_t)m * ldd + n;
-    const uint32_t lo = pack_bf16(acc.x, acc.y), hi = pack_bf16(acc.z, acc.w);
-    if (vec_store && n + 3 < N) {
-        *reinterpret_cast<uint2*>(d) = make_uint2(lo, hi);
-    } else {
-        if (n < N) d[0] = (uint16_t)lo;
-        if (n + 1 < N) d[1] = (uint16_t)(lo >> 16);
-        if (n + 2 < N) d[2] = (uint16_t)hi;
-        if (n + 3 < N) d[3] = (uint16_t)(hi >> 16);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int64_t slab = (int64_t)a.tile_count * BM * BN;
+    const float* P = a.P + (int64_t)trel * BM * BN;
+    for (int r = strip * 8 + threadIdx.x / kRuns; r < strip * 8 + 8; r += kRows) {
+        if (m0 + r >= a.M) break;
+        const int c = (threadIdx.x % kRuns) * 4;
+        const float* p = P + r * BN + c;
+        float4 acc = *reinterpret_cast<const float4*>(p);
+        int sp = 1;
+        for (; sp + 3 < a.splits; sp += 4) {
+            const float4 v0 = *reinterpret_cast<const float4*>(p + sp * slab);
+            const float4 v1 = *reinterpret_cast<const float4*>(p + (sp + 1) * slab);
+            const float4 v2 = *reinterpret_cast<const float4*>(p + (sp + 2) * slab);
+            const float4 v3 = *reinterpret_cast<const float4*>(p + (sp + 3) * slab);
+            acc.x = (((acc.x + v0.x) + v1.x) + v2.x) + v3.x;
+            acc.y = (((acc.y + v0.y) + v1.y) + v2.y) + v3.y;
+            acc.z = (((acc.z + v0.z) + v1.z) + v2.z) + v3.z;
+            acc.w = (((acc.w + v0.w) + v1.w) + v2.w) + v3.w;
+        }
+        for (; sp < a.splits; ++sp) {
+            const float4 v = *reinterpret_cast<const float4*>(p + sp * slab);
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+        const int n = n0 + c;
+        uint16_t* d = a.D + (int64_t)(m0 + r) * a.ldd + n;
+        const uint32_t lo = pack_bf16(acc.x, acc.y), hi = pack_bf16(acc.z, acc.w);
+        if (a.vec_store && n + 3 < a.N) {
+            *reinterpret_cast<uint2*>(d) = make_uint2(lo, hi);
+        } else {
+            if (n < a.N) d[0] = (uint16_t)lo;
+            if (n + 1 < a.N) d[1] = (uint16_t)(lo >> 16);
+            if (n + 2 < a.N) d[2] = (uint16_t)hi;
+            if (n + 3 < a.N) d[3] = (uint16_t)(hi >> 16);
+        }
     }
 }
 
-// Split-K plan for a tile grid: the number of K splits that minimises the
-// estimated makespan (waves of one workgroup per CU, each costing its K
-// blocks plus a fixed pipeline fill of about two blocks).
-struct SplitPlan {
-    int splits = 1, kb_per_split = 0;
+// LDS bytes of a tile configuration; configurations that fit twice into a
+// CU's 160 KB run two workgroups per CU.
+constexpr int gemm_lds_bytes(int bm, int bn, int stages) { return stages * (bm * kRowB + bn * kRowB + 2048); }
+constexpr int gemm_occupancy(int bm, int bn, int stages) { return gemm_lds_bytes(bm, bn, stages) <= 80 * 1024 ? 2 : 1; }
+
+// Launch plan of a dense GEMM.  Whole waves of tiles run data-parallel in
+// one launch; when the last wave would be partly empty, its tiles (the
+// "tail") may instead run split-K in a second launch over all workgroup
+// slots, followed by the reduction.
+struct Schedule {
+    int bm = 0, bn = 0, stages = 0;
+    int64_t tiles = 0;
+    int64_t dp_tiles = 0;         // tiles [0, dp_tiles) data-parallel
+    int splits = 1, kb_per_split = 0;  // the tail [dp_tiles, tiles)
+    int64_t ws_bytes = 0;         // fp32 slabs of the tail
 };
-static SplitPlan plan_splits(int64_t tiles, int KB, int cus) {
-    SplitPlan best;
-    best.kb_per_split = KB;
-    if (tiles <= 0 || KB < 8 || tiles >= cus) return best;
-    double best_cost = 1e30;
-    for (int s = 1; s <= 32 && s <= KB / 4; ++s) {
-        const int kbps = (KB + s - 1) / s;
-        const int ss = (KB + kbps - 1) / kbps;
-        const int64_t wgs = tiles * ss;
-        const double cost = (double)((wgs + cus - 1) / cus) * (kbps + 2.0);
-        if (cost < best_cost - 1e-9) {
-            best_cost = cost;
-            best.splits = ss;
-            best.kb_per_split = kbps;
+
+// Only tails whose split workgroups fit in one wave are split.  Cost model
+// in K-block times of one workgroup slot: a pipeline fill of about two
+// blocks per workgroup, the fp32 partial slab store per split workgroup, and
+// the reduction's slab traffic spread over all CUs plus one launch.
+static void plan_tail(Schedule& s, int64_t M, int KBT) {
+    const int occ = gemm_occupancy(s.bm, s.bn, s.stages);
+    const int cus = cu_count();
+    const int64_t slots = (int64_t)occ * cus;
+    s.dp_tiles = s.tiles;
+    s.splits = 1;
+    s.kb_per_split = KBT;
+    const int64_t waves = s.tiles / slots, rem = s.tiles - waves * slots;
+    if (rem == 0 || KBT < 8) return;
+    const double fill = 2.0, kblock = (double)(s.bm + s.bn) * kRowB;
+    const double rows = (double)std::min<int64_t>(M, s.bm);
+    const double slab = rows * s.bn * 4 / kblock;               // one partial slab, in K-block times
+    double best = (double)(KBT + fill);                          // the tail as one more data-parallel wave
+    for (int sp = 2; sp <= 32 && sp <= KBT / 4; ++sp) {
+        const int kbps = (KBT + sp - 1) / sp;
+        const int ss = (KBT + kbps - 1) / kbps;
+        const int64_t wgs = rem * ss;
+        if (wgs > slots) break;   // a tail that needs more than one wave gains nothing from splitting
+        const double cost = (double)((wgs + slots - 1) / slots) * (kbps + fill + slab) +
+                            (double)ss * rem * slab / cus + 1.0;
+        if (cost < best - 1e-9) {
+            best = cost;
+            s.splits = ss;
+            s.kb_per_split = kbps;
         }
     }
-    return best;
+    if (s.splits > 1) {
+        s.dp_tiles = waves * slots;
+        s.ws_bytes = (int64_t)s.splits * rem * s.bm * s.bn * 4;
+    }
 }
 
 template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped>
-static int launch_gemm(GemmArgs a, hipStream_t st, const char* what) {
+static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const char* what) {
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
     const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
-    const int64_t blocks = tiles * (a.splits > 1 ? a.splits : 1);
-    KBN_CHECK_ARG(blocks <= 0x7FFFFFFFLL, "%s: too many tiles", what);
-    if (!kGrouped && a.splits > 1) {
+    KBN_CHECK_ARG(tiles <= 0x7FFFFFFFLL, "%s: too many tiles", what);
+    const int64_t dp = (!kGrouped && a.P && sc.splits > 1) ? sc.dp_tiles : tiles;
+    if (dp > 0) {
+        a.tile_base = 0;
+        a.tile_count = (int)dp;
+        a.splits = 1;
+        a.kb_per_split = a.K / kRowB;
+        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped, false><<<dim3((unsigned)dp), dim3(256), 0, st>>>(a);
+        KBN_CHECK_LAUNCH(what);
+    }
+    if (dp < tiles) {
+        a.tile_base = (int)dp;
+        a.tile_count = (int)(tiles - dp);
+        a.splits = sc.splits;
+        a.kb_per_split = sc.kb_per_split;
+        const int64_t blocks = (tiles - dp) * sc.splits;
+        KBN_CHECK_ARG(blocks <= 0x7FFFFFFFLL, "%s: too many tiles", what);
         gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped && false, true><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a);
         KBN_CHECK_LAUNCH(what);
-        const int64_t threads = (int64_t)a.M * ((a.N + 3) / 4);
-        splitk_reduce_kernel<<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st>>>(
-            a.P, a.ldp, a.splits, a.M, a.N, a.D, a.ldd, a.vec_store);
-    } else {
-        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped, false><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a);
+        splitk_reduce_kernel<BM, BN><<<dim3((unsigned)((tiles - dp) * (BM / 8))), dim3(256), 0, st>>>(a);
+        KBN_CHECK_LAUNCH(what);
     }
-    KBN_CHECK_LAUNCH(what);
     return 0;
 }
 
@@ -581,24 +650,26 @@ static int check_scale_ranges(const char* what, int64_t M, int64_t K, int64_t sm
     return 0;
 }
 
-// Tile configuration of the dense GEMM for a shape.  UE8M0: 256x256 tiles
-// (2 LDS stages) when M > 128, 128x128 (4 stages) for 64 < M <= 128 and
-// 64x256 (3 stages) for M <= 64, where the weights dominate the traffic and
-// a short M tile wastes the least MFMA work.  FP32 contract: 128x128.
-struct DenseCfg {
-    int bm, bn;
-};
-static DenseCfg dense_cfg(int64_t M, int ue8m0) {
-    if (!ue8m0) return {128, 128};
-    if (M > 128) return {256, 256};
-    if (M > 64) return {128, 128};
-    return {64, 256};
-}
-static int64_t round_up4(int64_t n) { return (n + 3) / 4 * 4; }
-static SplitPlan dense_plan(int64_t M, int64_t N, int64_t K, int ue8m0) {
-    const DenseCfg c = dense_cfg(M, ue8m0);
-    const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
-    return plan_splits(tiles, (int)(K / kGroup), cu_count());
+// Dense tile configuration: 256x256 (2 LDS stages) when M > 128, 128x128 (4
+// stages) for 64 < M <= 128, 64x128 (3 stages, two workgroups per CU) for
+// M <= 64, where the weights dominate the traffic; 128x128 for the FP32
+// scale contract.
+static Schedule dense_schedule(int64_t M, int64_t N, int64_t K, int ue8m0, bool allow_split) {
+    Schedule s;
+    if (!ue8m0) {
+        s.bm = 128; s.bn = 128; s.stages = 4;
+    } else if (M > 128) {
+        s.bm = 256; s.bn = 256; s.stages = 2;
+    } else if (M > 64) {
+        s.bm = 128; s.bn = 128; s.stages = 4;
+    } else {
+        s.bm = 64; s.bn = 128; s.stages = 3;
+    }
+    s.tiles = ((M + s.bm - 1) / s.bm) * ((N + s.bn - 1) / s.bn);
+    s.dp_tiles = s.tiles;
+    s.kb_per_split = (int)(K / kGroup);
+    if (allow_split) plan_tail(s, M, (int)(K / kGroup));
+    return s;
 }
 
 static int gemm_nt_impl(const char* what, const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
@@ -622,27 +693,20 @@ static int gemm_nt_impl(const char* what, const void* A, int64_t lda, const floa
     a.vec_store = (reinterpret_cast<uintptr_t>(D_bf16) % 16 == 0) && (ldd % 8 == 0);
     a.expert_ids = nullptr;
     a.M = (int)M; a.N = (int)N; a.K = (int)K; a.E = 1;
-    a.splits = 1;
-    a.kb_per_split = (int)(K / kGroup);
-    if (workspace) {
-        const SplitPlan sp = dense_plan(M, N, K, scale_ue8m0);
-        const int64_t ldp = round_up4(N);
-        const int64_t need = (int64_t)sp.splits * M * ldp * 4;
-        if (sp.splits > 1 && workspace_bytes >= need) {
+    Schedule sc = dense_schedule(M, N, K, scale_ue8m0, workspace != nullptr);
+    if (sc.splits > 1) {
+        if (workspace_bytes >= sc.ws_bytes) {
             KBN_CHECK_ARG(aligned16(workspace), "%s: workspace must be 16-byte aligned", what);
-            KBN_CHECK_ARG(ldp * 4 * 256 < 0x7FFFFFFFLL, "%s: N too large for split-K", what);
             a.P = (float*)workspace;
-            a.ldp = ldp;
-            a.splits = sp.splits;
-            a.kb_per_split = sp.kb_per_split;
+        } else {
+            sc = dense_schedule(M, N, K, scale_ue8m0, false);
         }
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const DenseCfg c = dense_cfg(M, scale_ue8m0);
-    if (!scale_ue8m0) return launch_gemm<128, 128, 4, false, false>(a, st, what);
-    if (c.bm == 256) return launch_gemm<256, 256, 2, true, false>(a, st, what);
-    if (c.bm == 128) return launch_gemm<128, 128, 4, true, false>(a, st, what);
-    return launch_gemm<64, 256, 3, true, false>(a, st, what);
+    if (!scale_ue8m0) return launch_gemm<128, 128, 4, false, false>(a, sc, st, what);
+    if (sc.bm == 256) return launch_gemm<256, 256, 2, true, false>(a, sc, st, what);
+    if (sc.bm == 128) return launch_gemm<128, 128, 4, true, false>(a, sc, st, what);
+    return launch_gemm<64, 128, 3, true, false>(a, sc, st, what);
 }
 
 extern "C" int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
@@ -655,8 +719,7 @@ extern "C" int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int6
 
 extern "C" int64_t kbn_fp8_gemm_nt_workspace_bytes(int64_t M, int64_t N, int64_t K, int scale_ue8m0) {
     if (M <= 0 || N <= 0 || K <= 0 || K % kGroup != 0 || M > 0x7FFFFFFFLL || N > 0x7FFFFFFFLL) return 0;
-    const SplitPlan sp = dense_plan(M, N, K, scale_ue8m0);
-    return sp.splits > 1 ? (int64_t)sp.splits * M * round_up4(N) * 4 : 0;
+    return dense_schedule(M, N, K, scale_ue8m0, true).ws_bytes;
 }
 
 extern "C" int kbn_fp8_gemm_nt_ws(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
@@ -692,6 +755,7 @@ extern "C" int kbn_fp8_grouped_gemm_nt_contiguous(const void* A, int64_t lda, co
     KBN_CHECK_ARG(E <= 0x7FFFFFFFLL, "%s: too many experts", what);
     a.M = (int)M_sum; a.N = (int)N; a.K = (int)K; a.E = (int)E;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (scale_ue8m0) return launch_gemm<128, 256, 3, true, true>(a, st, what);
-    return launch_gemm<128, 128, 4, false, true>(a, st, what);
+    Schedule sc;   // grouped: data-parallel, one workgroup per 128-row block x N tile
+    if (scale_ue8m0) return launch_gemm<128, 256, 3, true, true>(a, sc, st, what);
+    return launch_gemm<128, 128, 4, false, true>(a, sc, st, what);
 }

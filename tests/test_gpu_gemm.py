@@ -109,19 +109,20 @@ def test_gemm_dsv3_shapes_sampled(gpu_device, name, N, K, M):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 7168, 18432), (8, 8192, 8192), (64, 1024, 28672), (100, 7168, 16384),
-                                   (77, 203, 2048), (256, 768, 4096)])
+                                   (77, 203, 65536), (256, 768, 32768), (200, 2048, 16384)])
 @pytest.mark.parametrize("ue8m0", [True, False])
-def test_gemm_split_k_matches_unsplit(gpu_device, M, N, K, ue8m0):
-    """Split-K (fp32 partials in a workspace + ordered reduction) against the
-    oracle and against the unsplit kernel (kbn_fp8_gemm_nt, no workspace):
-    both within tolerance, and equal up to fp32 summation order."""
+def test_gemm_split_tail_matches_data_parallel(gpu_device, M, N, K, ue8m0):
+    """Split-K tail (the partly empty last wave of tiles split over K into
+    fp32 workspace slabs + ordered reduction) against the oracle and against
+    the data-parallel kernel (kbn_fp8_gemm_nt, no workspace): both within
+    tolerance, and equal up to fp32 summation order."""
     import ctypes
 
     from kb_nano_amd._lib import lib
     from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
     L = lib()
     ws = L.kbn_fp8_gemm_nt_workspace_bytes(M, N, K, int(ue8m0))
-    assert ws > 0, "shape expected to split"
+    assert ws > 0, "shape expected to split its tail"
     qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=N + K)
     if not ue8m0:
         sw = (sw * np.float32(1.37)).astype(np.float32)
