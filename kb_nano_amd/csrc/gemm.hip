@@ -61,6 +61,7 @@ struct GemmArgs {
     // P[split][tile - tile_base][BM][BN], summed by splitk_reduce_kernel.
     int tile_base, tile_count;
     float* P;
+    int64_t ws_bytes;            // bytes at P
     int splits, kb_per_split;
 };
 
@@ -602,6 +603,14 @@ static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const cha
         KBN_CHECK_LAUNCH(what);
     }
     if (dp < tiles) {
+        // the plan must be for this tile shape, and its slabs must fit the workspace
+        KBN_CHECK_ARG(sc.bm == BM && sc.bn == BN && sc.tiles == tiles, "%s: split plan does not match the %dx%d tiles",
+                      what, BM, BN);
+        const int64_t need = (int64_t)sc.splits * (tiles - dp) * BM * BN * 4;
+        KBN_CHECK_ARG(sc.splits >= 2 && sc.kb_per_split >= 1 && need <= a.ws_bytes,
+                      "%s: workspace of %lld bytes is smaller than the %lld the split plan writes", what,
+                      (long long)a.ws_bytes, (long long)need);
+        KBN_CHECK_ARG((int64_t)sc.splits * sc.kb_per_split >= a.K / kRowB, "%s: split plan does not cover K", what);
         a.tile_base = (int)dp;
         a.tile_count = (int)(tiles - dp);
         a.splits = sc.splits;
@@ -698,15 +707,18 @@ static int gemm_nt_impl(const char* what, const void* A, int64_t lda, const floa
         if (workspace_bytes >= sc.ws_bytes) {
             KBN_CHECK_ARG(aligned16(workspace), "%s: workspace must be 16-byte aligned", what);
             a.P = (float*)workspace;
+            a.ws_bytes = workspace_bytes;
         } else {
             sc = dense_schedule(M, N, K, scale_ue8m0, false);
         }
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (!scale_ue8m0) return launch_gemm<128, 128, 4, false, false>(a, sc, st, what);
-    if (sc.bm == 256) return launch_gemm<256, 256, 2, true, false>(a, sc, st, what);
-    if (sc.bm == 128) return launch_gemm<128, 128, 4, true, false>(a, sc, st, what);
-    return launch_gemm<64, 128, 3, true, false>(a, sc, st, what);
+    if (sc.bm == 256 && sc.bn == 256) return launch_gemm<256, 256, 2, true, false>(a, sc, st, what);
+    if (sc.bm == 128 && sc.bn == 128) return launch_gemm<128, 128, 4, true, false>(a, sc, st, what);
+    if (sc.bm == 64 && sc.bn == 128) return launch_gemm<64, 128, 3, true, false>(a, sc, st, what);
+    set_error("%s: no kernel for %dx%d tiles", what, sc.bm, sc.bn);
+    return 1;
 }
 
 extern "C" int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
