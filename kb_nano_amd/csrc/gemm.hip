@@ -164,16 +164,17 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 //               of K half 0 (and the scales) of block kb+1.
 // So kStages-1 blocks are in flight while one is consumed, and no fragment
 // register set is ever copied.
-template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, bool kSplitK>
-__global__ __launch_bounds__(256, (kStages * (BM + BN) * 128 + kStages * 2048 <= 80 * 1024) ? 2 : 1) void
+template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, bool kSplitK, int kWaves>
+__global__ __launch_bounds__(64 * kWaves, (kStages * (BM + BN) * 128 + kStages * 512 * kWaves <= 80 * 1024) ? 2 : 1) void
 gemm_bs_kernel(const GemmArgs a) {
-    constexpr int WN = 2;
-    constexpr int TM = BM / 2, TN = BN / 2;     // wavefront tile
+    static_assert(kWaves == 4 || kWaves == 8, "2x2 or 2x4 wavefronts");
+    constexpr int WM = 2, WN = kWaves / 2;
+    constexpr int TM = BM / WM, TN = BN / WN;   // wavefront tile
     constexpr int FM = TM / 32, FN = TN / 32;   // 32x32 fragments per wavefront
     static_assert(FM >= 1 && FN >= 1 && TM % 32 == 0 && TN % 32 == 0, "fragment tiling");
-    static_assert(BM <= 256 && BM % 64 == 0 && BN % 64 == 0, "DMA tiling");
+    static_assert(BM <= 64 * kWaves && BM % (16 * kWaves) == 0 && BN % (16 * kWaves) == 0, "DMA tiling");
     static_assert(128 % TN == 0 || TN % 128 == 0, "wave N tile must not straddle a scale block");
-    constexpr int kA = BM * kRowB, kB = BN * kRowB, kSA = 4 * 256, kSW = 4 * 256;
+    constexpr int kA = BM * kRowB, kB = BN * kRowB, kSA = kWaves * 256, kSW = kWaves * 256;
     constexpr int kStage = kA + kB + kSA + kSW;
     static_assert(kStages >= 2 && kStages * kStage <= 160 * 1024, "LDS budget");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStage];
@@ -208,7 +209,7 @@ gemm_bs_kernel(const GemmArgs a) {
     // DMA lane mapping: one instruction = 8 rows x 128 B starting at row
     // r0 = 8 q; lane i fills slot i % 8 of row r0 + i / 8 with global chunk
     // (i % 8) ^ swz(r0 + i / 8) = (i % 8) ^ ((i >> 4) | 4 (q & 1)).
-    constexpr int kAInstr = BM / 32, kBInstr = BN / 32;   // 8-row DMAs per wave
+    constexpr int kAInstr = BM / (8 * kWaves), kBInstr = BN / (8 * kWaves);   // 8-row DMAs per wave
     static_assert(kAInstr % 2 == 0 && kBInstr % 2 == 0, "even instruction counts keep q & 1 == i & 1");
     const int drow = lane >> 3;
     const int ch_e = ((lane & 7) ^ (lane >> 4)) << 4;
@@ -587,7 +588,7 @@ static void plan_tail(Schedule& s, int64_t M, int KBT) {
     }
 }
 
-template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped>
+template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, int kWaves = 4>
 static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const char* what) {
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
@@ -599,7 +600,7 @@ static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const cha
         a.tile_count = (int)dp;
         a.splits = 1;
         a.kb_per_split = a.K / kRowB;
-        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped, false><<<dim3((unsigned)dp), dim3(256), 0, st>>>(a);
+        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped, false, kWaves><<<dim3((unsigned)dp), dim3(64 * kWaves), 0, st>>>(a);
         KBN_CHECK_LAUNCH(what);
     }
     if (dp < tiles) {
@@ -617,7 +618,8 @@ static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const cha
         a.kb_per_split = sc.kb_per_split;
         const int64_t blocks = (tiles - dp) * sc.splits;
         KBN_CHECK_ARG(blocks <= 0x7FFFFFFFLL, "%s: too many tiles", what);
-        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped && false, true><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(a);
+        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped && false, true, kWaves>
+            <<<dim3((unsigned)blocks), dim3(64 * kWaves), 0, st>>>(a);
         KBN_CHECK_LAUNCH(what);
         splitk_reduce_kernel<BM, BN><<<dim3((unsigned)((tiles - dp) * (BM / 8))), dim3(256), 0, st>>>(a);
         KBN_CHECK_LAUNCH(what);
@@ -714,7 +716,12 @@ static int gemm_nt_impl(const char* what, const void* A, int64_t lda, const floa
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (!scale_ue8m0) return launch_gemm<128, 128, 4, false, false>(a, sc, st, what);
-    if (sc.bm == 256 && sc.bn == 256) return launch_gemm<256, 256, 2, true, false>(a, sc, st, what);
+    if (sc.bm == 256 && sc.bn == 256) {
+        // short K (few K blocks per tile): two wavefronts per SIMD hide the
+        // per-tile pipeline fill and epilogue better
+        if (K <= 2048) return launch_gemm<256, 256, 2, true, false, 8>(a, sc, st, what);
+        return launch_gemm<256, 256, 2, true, false>(a, sc, st, what);
+    }
     if (sc.bm == 128 && sc.bn == 128) return launch_gemm<128, 128, 4, true, false>(a, sc, st, what);
     if (sc.bm == 64 && sc.bn == 128) return launch_gemm<64, 128, 3, true, false>(a, sc, st, what);
     set_error("%s: no kernel for %dx%d tiles", what, sc.bm, sc.bn);
