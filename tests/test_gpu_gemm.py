@@ -148,6 +148,17 @@ def test_gemm_split_tail_matches_data_parallel(gpu_device, M, N, K, ue8m0):
     assert torch.all(diff <= 1e-2 * outs[0].abs() + 1e-3), float(diff.max())
 
 
+def test_gemm_cfg1_golden_fixture(gpu_device):
+    """BASELINE config 1 (M=64, N=K=2048, seed 0) against the committed
+    oracle slice (tests/golden/gemm_cfg1.npz), within the bf16 tolerance."""
+    import os
+    d = np.load(os.path.join(os.path.dirname(__file__), "golden", "gemm_cfg1.npz"), allow_pickle=False)
+    M, N, K = int(d["M"]), int(d["N"]), int(d["K"])
+    qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=int(d["seed"]))
+    D = _gemm_gpu(qa, sa, qw, sw, gpu_device)
+    assert_gemm_close(D[:16, :64], d["out_slice"], "cfg1 golden slice")
+
+
 # ------------------------------------------------------------- Fp8Linear
 
 def test_fp8_linear_end_to_end(gpu_device):

@@ -172,3 +172,25 @@ def test_silu_mul_quant_cfg2_full(gpu_device):
     qo, so = oracle.silu_mul_quant(xb)
     assert np.array_equal(s.cpu().numpy(), so)
     assert np.array_equal(fp8_codes(q), qo)
+
+
+# ------------------------------------------------------------ golden fixtures
+
+def test_quant_golden_fixture(gpu_device):
+    """The committed edge-case fixture (tests/golden/quant_edge.npz), both
+    scale contracts, bit-exact."""
+    import os
+    d = np.load(os.path.join(os.path.dirname(__file__), "golden", "quant_edge.npz"), allow_pickle=False)
+    x = from_bits(d["x_bits"], gpu_device)
+    for ue8m0, qk, sk in ((True, "q_ue8m0", "s_ue8m0"), (False, "q_fp32", "s_fp32")):
+        q, s = _quant_gpu(x, col_major=True, use_ue8m0=ue8m0)
+        assert np.array_equal(fp8_codes(q), d[qk]) and np.array_equal(s.cpu().numpy(), d[sk])
+
+
+def test_silu_mul_quant_golden_fixture(gpu_device):
+    import os
+    d = np.load(os.path.join(os.path.dirname(__file__), "golden", "silu_mul_quant.npz"), allow_pickle=False)
+    x = from_bits(d["x_bits"], gpu_device)
+    for ue8m0, qk, sk in ((True, "q_ue8m0", "s_ue8m0"), (False, "q_fp32", "s_fp32")):
+        q, s = _silu_gpu(x, use_ue8m0=ue8m0)
+        assert np.array_equal(fp8_codes(q), d[qk]) and np.array_equal(s.cpu().numpy(), d[sk])

@@ -9,6 +9,7 @@ transposed operand, wrong gate/up column) fails at least one of them.
 """
 import decimal
 import math
+import os
 
 import numpy as np
 import pytest
@@ -340,3 +341,49 @@ def test_permute_contiguous_layout():
 
 def test_compute_aligned_M_cfg4():
     assert oracle.compute_aligned_M(4096, 8, 256, 128) == 65280
+
+
+# ----------------------------------------------------------- golden fixtures
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _golden(name):
+    return np.load(os.path.join(GOLDEN, name), allow_pickle=False)
+
+
+def test_golden_quant_edge_fixture():
+    """The committed quant fixture (tests/golden/make_fixtures.py) is what
+    the oracle computes, and its e4m3 ties carry the known round-half-even
+    codes: 1.0625 -> 1.0 (0x38), 1.1875 -> 1.25 (0x3A), 3.125 -> 3.0 (0x44),
+    9/1024 -> 4 * 2^-9 (0x04), 448 -> 0x7E, negatives with the sign bit."""
+    d = _golden("quant_edge.npz")
+    for ue8m0, qk, sk in ((True, "q_ue8m0", "s_ue8m0"), (False, "q_fp32", "s_fp32")):
+        q, s = oracle.quant_group128(d["x_bits"], use_ue8m0=ue8m0)
+        assert np.array_equal(q, d[qk]) and np.array_equal(s, d[sk])
+    assert list(d["q_ue8m0"][2, 256:265]) == [0x38, 0x3A, 0xB8, 0xBA, 0x44, 0xC4, 0x04, 0x84, 0x7E]
+    assert d["s_ue8m0"][2, 2] == 1.0 and d["s_ue8m0"][1, 0] == 1.0 and d["s_ue8m0"][1, 1] == 32.0
+    assert d["s_ue8m0"][0, 0] == 2.0 ** -42      # all-zero group: eps / 448 rounded up
+
+
+def test_golden_silu_fixture():
+    d = _golden("silu_mul_quant.npz")
+    for ue8m0, qk, sk in ((True, "q_ue8m0", "s_ue8m0"), (False, "q_fp32", "s_fp32")):
+        q, s = oracle.silu_mul_quant(d["x_bits"], use_ue8m0=ue8m0)
+        assert np.array_equal(q, d[qk]) and np.array_equal(s, d[sk])
+
+
+def test_golden_gemm_cfg1_fixture():
+    """BASELINE config 1 regenerated from its seed: same quantized inputs,
+    same oracle output (sha256 of the bf16 result and a 16 x 64 slice)."""
+    import hashlib
+
+    from tests._util import quantized_gemm_inputs
+    d = _golden("gemm_cfg1.npz")
+    M, N, K = int(d["M"]), int(d["N"]), int(d["K"])
+    qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=int(d["seed"]))
+    sha = lambda a: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+    assert sha(qa) + sha(sa) + sha(qw) + sha(sw) == str(d["inputs_sha256"])
+    ref = oracle.gemm_nt_sample(qa, sa, qw, sw, ue8m0=True)
+    assert sha(oracle.f32_to_bf16_bits(ref.astype(np.float32))) == str(d["out_bf16_sha256"])
+    assert np.array_equal(ref[:16, :64], d["out_slice"])
