@@ -195,6 +195,16 @@ def bench_moe(steps, warmup, dev):
     c2 = torch.empty(M_sum, H, dtype=torch.bfloat16, device=dev)
     ms2 = _events_time_ms(lambda i: _ops.m_grouped_gemm_nt_contiguous(a2q, a2s, w2, s2, c2, expert_ids, False),
                           steps, warmup)
+    # the whole experts layer (quant, permute, both GEMMs, SiLU*Mul+quant, unpermute)
+    from kb_nano_amd.fused_experts import FusedExperts
+    w13, s13 = experts(I2, H)
+    w2, s2 = experts(H, I)
+    topk_w = torch.softmax(torch.randn(T, topk, generator=g), -1).to(dev)
+    layer = FusedExperts()
+    ms_layer = _events_time_ms(lambda i: layer(hidden, w13, w2, topk_w, topk_ids, E, w13_scale=s13, w2_scale=s2,
+                                               use_fp8_w8a8=True, block_shape=[128, 128]), steps, warmup)
+    res["layer_us"] = ms_layer * 1e3
+    del w13, s13, w2, s2
     for tag, ms, N, K in (("gate_up", ms1, I2, H), ("down", ms2, H, I)):
         t = ms * 1e-3
         flop = 2.0 * valid_rows * N * K
@@ -202,7 +212,6 @@ def bench_moe(steps, warmup, dev):
         res[tag] = {"N": N, "K": K, "us": ms * 1e3, "TFLOPS": flop / t / 1e12, "GB/s": nbytes / t / 1e9,
                     "frac_hbm": nbytes / t / 1e9 / HBM_PEAK_GBS,
                     "frac_roof": max(flop / (FP8_PEAK_TFLOPS * 1e12), nbytes / (HBM_PEAK_GBS * 1e9)) / t}
-    del w2, s2
     torch.cuda.empty_cache()
     return res
 

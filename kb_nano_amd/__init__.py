@@ -7,11 +7,15 @@ Four operators, each a drop-in for its kb_nano L1 counterpart:
   * ``Fp8Linear``               128x128 block-scaled FP8 GEMM, fp32 accumulate, bf16 out
   * ``Fp8GroupedGemmContiguous``  its contiguous-layout MoE grouped variant
 
+and ``FusedExperts``, the MoE experts layer that chains them (quant, permute,
+grouped GEMM, SiLU*Mul+quant, grouped GEMM, weighted unpermute).
+
 The compute runs in hand-written gfx950 HIP kernels (``csrc/``) behind the
 C-ABI of ``libkbn_fp8.so`` (declared in ``include/kbn_fp8.h``); this package
 is the PyTorch-side host layer.
 """
 from .fp8_grouped_gemm_contiguous import Fp8GroupedGemmContiguous
+from .fused_experts import FusedExperts
 from .fp8_linear import (
     Fp8Linear,
     PerTokenGroupQuantFp8,
@@ -28,6 +32,7 @@ __all__ = [
     "PerTokenGroupQuantFp8",
     "SiluMulQuantFp8",
     "Fp8GroupedGemmContiguous",
+    "FusedExperts",
     "m_grouped_fp8_gemm_nt_contiguous",
     "postprocess_fp8_weights",
     "postprocess_fp8_weights_batched",

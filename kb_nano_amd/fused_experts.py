@@ -1,0 +1,141 @@
+"""Fused MoE experts over the FP8 contiguous-layout path.
+
+Mirrors ``FusedExperts`` of ``tasks/baseline/L2/fused_experts.py:139-283``
+(kb_nano) for FP8 W8A8 block-scaled expert weights, the path its
+``_forward_deep_gemm`` takes (:246-283):
+
+    1x128 quant (row-major scales) -> contiguous permute -> grouped GEMM1 (w13)
+    -> fused SiLU*Mul + 1x128 quant -> grouped GEMM2 (w2) -> unpermute-and-reduce
+
+Every compute step runs in this package's gfx950 kernels
+(``PerTokenGroupQuantFp8``, ``m_grouped_fp8_gemm_nt_contiguous``,
+``SiluMulQuantFp8``); the permute and the weighted reduction are the
+device-side tensor ops of ``moe_layout``.  Scratch buffers are shared by all
+layers, as in the reference (layers run one after another).
+
+The reference falls back to its Triton ``fused_moe_kernel`` for BF16 weights,
+for shapes DeepGEMM does not take and while a CUDA graph is being captured
+(:228-244); that kernel family is not part of this path, so those cases raise
+``NotImplementedError`` here instead of running something else.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+
+from .fp8_linear import PerTokenGroupQuantFp8
+from .moe_grouped_gemm import _valid_deep_gemm, m_grouped_fp8_gemm_nt_contiguous
+from .moe_layout import _compute_aligned_M, _deepgemm_permute, _deepgemm_unpermute_and_reduce
+from .silu_mul_quant_fp8 import SiluMulQuantFp8
+
+__all__ = ["FusedExperts", "_compute_aligned_M", "_deepgemm_permute", "_deepgemm_unpermute_and_reduce"]
+
+_FP8_GROUP_SIZE = 128
+
+
+class _SharedBuf:
+    """Scratch buffers shared by every FusedExperts layer (reference :139-153)."""
+    __slots__ = ("a_fp8_1", "a_scale_1", "dg_ws1", "dg_ws2")
+
+    def __init__(self):
+        self.a_fp8_1 = None
+        self.a_scale_1 = None
+        self.dg_ws1 = None
+        self.dg_ws2 = None
+
+
+_SHARED_BUF = _SharedBuf()
+
+
+class FusedExperts(nn.Module):
+    """Fused MoE experts: two grouped FP8 GEMMs with SiLU*Mul+quant between.
+
+    ``forward(hidden_states, w13, w2, topk_weights, topk_ids, num_experts,
+    w13_scale, w2_scale, w13_scale_dg, w2_scale_dg, use_fp8_w8a8,
+    block_shape)`` takes the reference's arguments: hidden_states bf16 [M, K],
+    w13 fp8 [E, 2N, K], w2 fp8 [E, K, N] with 128x128 block scales
+    [E, 2N/128, K/128] and [E, K/128, N/128], topk_ids / topk_weights [M, k].
+    Returns bf16 [M, K] = sum_j w[m, j] * expert_{ids[m, j]}(x[m]).
+    """
+
+    def __init__(self):
+        super().__init__()
+        self.per_token_group_quant_fp8 = PerTokenGroupQuantFp8()
+        self.silu_mul_quant_fp8 = SiluMulQuantFp8()
+        self._sb = _SHARED_BUF
+
+    def _get_fp8_bufs(self, M: int, K: int, device):
+        sb = self._sb
+        groups = math.ceil(K / _FP8_GROUP_SIZE)
+        if sb.a_fp8_1 is None or sb.a_fp8_1.size(0) < M or sb.a_fp8_1.size(1) < K or sb.a_fp8_1.device != device:
+            sb.a_fp8_1 = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=device)
+            sb.a_scale_1 = torch.empty(M, groups, dtype=torch.float32, device=device)
+        return sb.a_fp8_1[:M, :K], sb.a_scale_1[:M, :groups]
+
+    def _get_dg_workspace(self, buf_id: int, shape, device, dtype):
+        """A view of a shared byte buffer (grown when needed) as `shape`/`dtype`
+        (reference :175-188)."""
+        sb = self._sb
+        attr = f"dg_ws{buf_id}"
+        need = torch.tensor([], dtype=dtype).element_size() * math.prod(shape)
+        raw = getattr(sb, attr)
+        if raw is None or raw.numel() < need or raw.device != device:
+            raw = torch.empty(need, dtype=torch.uint8, device=device)
+            setattr(sb, attr, raw)
+        return raw[:need].view(dtype).view(shape)
+
+    def forward(self, hidden_states: torch.Tensor, w13: torch.Tensor, w2: torch.Tensor, topk_weights: torch.Tensor,
+                topk_ids: torch.Tensor, num_experts: int, w13_scale: torch.Tensor | None = None,
+                w2_scale: torch.Tensor | None = None, w13_scale_dg: torch.Tensor | None = None,
+                w2_scale_dg: torch.Tensor | None = None, use_fp8_w8a8: bool = False,
+                block_shape: list[int] | None = None) -> torch.Tensor:
+        M, K = hidden_states.size()
+        E, N2, _ = w13.size()
+        N = N2 // 2
+        top_k = topk_ids.size(1)
+        if not use_fp8_w8a8:
+            raise NotImplementedError("FusedExperts: only FP8 W8A8 block-scaled experts are on this path "
+                                      "(the reference runs BF16 experts through its Triton kernel)")
+        if block_shape is not None and list(block_shape) != [_FP8_GROUP_SIZE, _FP8_GROUP_SIZE]:
+            raise NotImplementedError(f"FusedExperts: block_shape {block_shape} (only 128x128 blocks)")
+        if not _valid_deep_gemm(hidden_states, w13, w2):
+            raise NotImplementedError("FusedExperts: shapes outside the contiguous grouped-GEMM gate "
+                                      "(the reference falls back to its Triton kernel)")
+        if torch.cuda.is_current_stream_capturing():
+            raise NotImplementedError("FusedExperts: the reference leaves this path during graph capture "
+                                      "(fused_experts.py:230)")
+        s13 = w13_scale_dg if w13_scale_dg is not None else w13_scale
+        s2 = w2_scale_dg if w2_scale_dg is not None else w2_scale
+        if s13 is None or s2 is None:
+            raise ValueError("FusedExperts: FP8 experts need w13_scale and w2_scale")
+        return self._forward_deep_gemm(hidden_states, w13, w2, topk_weights, topk_ids, num_experts, s13, s2,
+                                       block_shape, M, K, E, N, N2, top_k)
+
+    def _forward_deep_gemm(self, hidden_states, w13, w2, topk_weights, topk_ids, num_experts, w13_scale, w2_scale,
+                           block_shape, M, K, E, N, N2, top_k) -> torch.Tensor:
+        """quant -> permute -> GEMM1 -> SiLU*Mul+quant -> GEMM2 -> unpermute
+        (reference :246-283)."""
+        dev = hidden_states.device
+        alignment = _FP8_GROUP_SIZE
+        M_sum = _compute_aligned_M(M, top_k, num_experts, alignment)
+
+        a_fp8, a_scale = self._get_fp8_bufs(M, K, dev)
+        self.per_token_group_quant_fp8(hidden_states, a_fp8, a_scale)
+
+        a1_perm, a1_scale_perm, expert_ids, inv_perm = _deepgemm_permute(a_fp8, a_scale, topk_ids, num_experts,
+                                                                        alignment)
+
+        mm1_out = self._get_dg_workspace(1, (M_sum, N2), dev, hidden_states.dtype)
+        m_grouped_fp8_gemm_nt_contiguous((a1_perm, a1_scale_perm), (w13, w13_scale), mm1_out, expert_ids)
+
+        quant_out = self._get_dg_workspace(2, (M_sum, N), dev, torch.float8_e4m3fn)
+        a2_fp8, a2_scale = self.silu_mul_quant_fp8(mm1_out, output=quant_out)
+
+        mm2_out = self._get_dg_workspace(1, (M_sum, K), dev, hidden_states.dtype)
+        m_grouped_fp8_gemm_nt_contiguous((a2_fp8, a2_scale), (w2, w2_scale), mm2_out, expert_ids)
+
+        output = torch.empty(M, K, dtype=hidden_states.dtype, device=dev)
+        _deepgemm_unpermute_and_reduce(mm2_out, topk_ids, topk_weights, inv_perm, output)
+        return output

@@ -191,3 +191,14 @@ def test_moe_layout_on_cpu_matches_oracle():
     assert a_perm.shape == (M_sum, K)
     assert np.array_equal(ids.numpy(), ids_o)
     assert np.array_equal(inv.numpy().reshape(-1), dest_o)
+
+
+def test_fused_experts_surface():
+    """FusedExperts keeps the reference forward's argument names and order
+    (tasks/baseline/L2/fused_experts.py:190-205)."""
+    import inspect
+
+    from kb_nano_amd import FusedExperts
+    names = list(inspect.signature(FusedExperts.forward).parameters)
+    assert names == ["self", "hidden_states", "w13", "w2", "topk_weights", "topk_ids", "num_experts", "w13_scale",
+                     "w2_scale", "w13_scale_dg", "w2_scale_dg", "use_fp8_w8a8", "block_shape"]
