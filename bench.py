@@ -183,6 +183,33 @@ def bench_moe(steps, warmup, dev):
         return w, s
 
     res = {"M_sum": M_sum, "rows_in_segments": rows_in_segments, "valid_rows": valid_rows}
+
+    # the layout kernels (fused_experts.py:42-136) on preallocated outputs:
+    # permute with the reference's zero padding and as the layer runs it
+    # (padding rows unwritten), then the weighted unpermute of [M_sum, H] rows
+    n_pairs, cols = T * topk, H // 128
+    s_row = s_tok.contiguous()
+    xp = torch.empty(M_sum, H, dtype=torch.float8_e4m3fn, device=dev)
+    sp = torch.empty(M_sum, cols, device=dev)
+    eid = torch.empty(M_sum, dtype=torch.int32, device=dev)
+    inv = torch.empty(T, topk, dtype=torch.int32, device=dev)
+    small_io = T * cols * 4 + n_pairs * 8 + M_sum * 4 + n_pairs * 4      # scales in, ids, expert ids, inv_perm
+    for tag, zero in (("permute", True), ("permute_layer", False)):
+        ms = _events_time_ms(lambda i: _ops.moe_permute_contiguous(a_tok, s_row, topk_ids, E, 128, M_sum, xp, sp, eid,
+                                                                   inv, zero), steps, warmup)
+        rows_out = M_sum if zero else n_pairs
+        nbytes = T * H + rows_out * (H + cols * 4) + small_io
+        res[tag] = {"us": ms * 1e3, "bytes": nbytes, "GB/s": nbytes / ms / 1e6,
+                    "frac_hbm": nbytes / ms / 1e6 / HBM_PEAK_GBS}
+    y = torch.randn(M_sum, H, generator=gen, device=dev).bfloat16()
+    topk_w = torch.softmax(torch.randn(T, topk, generator=g), -1).to(dev)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    ms = _events_time_ms(lambda i: _ops.moe_unpermute_reduce(y, inv, topk_w, out), steps, warmup)
+    nbytes = n_pairs * H * 2 + T * H * 2 + n_pairs * 8
+    res["unpermute"] = {"us": ms * 1e3, "bytes": nbytes, "GB/s": nbytes / ms / 1e6,
+                        "frac_hbm": nbytes / ms / 1e6 / HBM_PEAK_GBS}
+    del xp, sp, eid, y, out
+
     w13, s13 = experts(I2, H)
     c1 = torch.empty(M_sum, I2, dtype=torch.bfloat16, device=dev)
     ms1 = _events_time_ms(lambda i: _ops.m_grouped_gemm_nt_contiguous(a_perm, s_perm, w13, s13, c1, expert_ids, False),
@@ -199,7 +226,6 @@ def bench_moe(steps, warmup, dev):
     from kb_nano_amd.fused_experts import FusedExperts
     w13, s13 = experts(I2, H)
     w2, s2 = experts(H, I)
-    topk_w = torch.softmax(torch.randn(T, topk, generator=g), -1).to(dev)
     layer = FusedExperts()
     ms_layer = _events_time_ms(lambda i: layer(hidden, w13, w2, topk_w, topk_ids, E, w13_scale=s13, w2_scale=s2,
                                                use_fp8_w8a8=True, block_shape=[128, 128]), steps, warmup)

@@ -124,6 +124,61 @@ int kbn_fp8_grouped_gemm_nt_contiguous(const void* A, int64_t lda, const float* 
                                        int64_t E, int scale_ue8m0, void* stream);
 
 /*
+ * Workspace bytes of kbn_moe_permute_contiguous for num_pairs = M * top_k
+ * routed pairs and num_experts experts; -1 if num_experts is outside
+ * [1, 1024] or num_pairs outside [0, 2^31).  (The reference's torch ops
+ * allocate their temporaries themselves; this ABI takes them from the caller.)
+ */
+int64_t kbn_moe_permute_workspace_bytes(int64_t num_pairs, int64_t num_experts);
+
+/*
+ * Contiguous-layout MoE permute.
+ * Replaces _deepgemm_permute (tasks/baseline/L2/fused_experts.py:42-116).
+ *   topk_ids    int32 (ids_bytes 4) or int64 (8) [M, top_k], contiguous
+ *   x           [M, row_bytes] rows (any element type, e.g. fp8 [M, K]),
+ *               row stride ld_x_bytes; 16-byte aligned, row_bytes % 16 == 0
+ *   x_scale     fp32 [M, scale_cols] at x_scale[m*s_stride_m + c*s_stride_c]
+ *   M_sum       must equal roundup(M*top_k + E*(alignment-1), alignment)
+ *               (_compute_aligned_M, fused_experts.py:32-39)
+ *   x_perm      [M_sum, row_bytes] contiguous; scale_perm fp32 [M_sum, scale_cols]
+ *   expert_ids  int32 [M_sum];  inv_perm int32 [M, top_k]
+ *   Expert e owns rows [off[e], off[e] + roundup(count[e], alignment)), with
+ *   off the exclusive prefix sum of the rounded counts.  Its first count[e]
+ *   rows hold its (token, slot) pairs in (token, slot) order and carry id e;
+ *   the rest are padding with id -1, as are rows past the last segment.
+ *   inv_perm[m, j] is the row of pair (m, j).  A pair whose id is outside
+ *   [0, E) is dropped (inv_perm -1); the reference fails on it in scatter_add.
+ *   zero_padding = 1 zeroes the padding rows of x_perm and scale_perm (the
+ *   reference's torch.zeros); 0 leaves them unwritten, which is enough for
+ *   kbn_fp8_grouped_gemm_nt_contiguous (it never writes padding rows of C).
+ *   workspace   >= kbn_moe_permute_workspace_bytes(M*top_k, E), 16-byte aligned
+ */
+int kbn_moe_permute_contiguous(const void* topk_ids, int ids_bytes, int64_t M, int64_t top_k,
+                               int64_t num_experts, int64_t alignment,
+                               const void* x, int64_t ld_x_bytes, int64_t row_bytes,
+                               const float* x_scale, int64_t s_stride_m, int64_t s_stride_c,
+                               int64_t scale_cols, int64_t M_sum, void* x_perm, float* scale_perm,
+                               int32_t* expert_ids, int32_t* inv_perm, int zero_padding,
+                               void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Unpermute and top-k weighted reduction.
+ * Replaces _deepgemm_unpermute_and_reduce (tasks/baseline/L2/fused_experts.py:119-136).
+ *   y         bf16 [M_sum, H] (the second grouped GEMM's output), row stride ld_y
+ *   inv_perm  int32 [M, top_k];  topk_weights [M, top_k] fp32 (weights_bf16 0)
+ *             or bf16 (1), contiguous
+ *   out       bf16 [M, H], row stride ld_out;  H % 8 == 0, 16-byte aligned rows
+ *   out[m, h] = bf16_rne(sum over j = 0..top_k-1, in slot order, in fp32, of
+ *   y[inv_perm[m, j], h] * w[m, j]); each product rounds to fp32 (fp32
+ *   weights) or to bf16 (bf16 weights), as torch's product does.  Slots whose
+ *   inv_perm is outside [0, M_sum) contribute nothing.
+ */
+int kbn_moe_unpermute_reduce(const void* y_bf16, int64_t M_sum, int64_t H, int64_t ld_y,
+                             const int32_t* inv_perm, int64_t M, int64_t top_k,
+                             const void* topk_weights, int weights_bf16,
+                             void* out_bf16, int64_t ld_out, void* stream);
+
+/*
  * Test hook (no counterpart in the reference): the kernels' bf16 SiLU
  * applied elementwise to n bf16 bit patterns, for exhaustive checking.
  */

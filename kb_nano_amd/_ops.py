@@ -1,9 +1,11 @@
 """Tensor-level wrappers over the C-ABI and the opaque ``torch.library`` ops.
 
 Every wrapper validates dtype, device, shape and strides on the host, then
-launches on the caller's current HIP stream; nothing here allocates device
-memory, synchronises, or computes on the CPU, so the ops are safe inside
-HIP-graph capture and stay opaque to ``torch.compile``.
+launches on the caller's current HIP stream.  Nothing here synchronises or
+computes on the CPU; the only device memory taken is kernel workspace from
+torch's caching allocator (stream-ordered, and served from the graph's pool
+under capture), so the ops are safe inside HIP-graph capture and stay opaque
+to ``torch.compile``.
 
 Op schemas follow the reference (tasks/baseline/L1/fp8_linear.py:89-178 and
 tasks/baseline/L1/fp8_grouped_gemm_contiguous.py:100-133).  The reference
@@ -196,6 +198,81 @@ def m_grouped_gemm_nt_contiguous(a_fp8: torch.Tensor, a_scale: torch.Tensor, b_f
         a_fp8.data_ptr(), a_fp8.stride(0), a_scale.data_ptr(), a_scale.stride(0), a_scale.stride(1),
         b_fp8.data_ptr(), b_scale.data_ptr(), c_bf16.data_ptr(), c_bf16.stride(0), expert_ids.data_ptr(),
         M_sum, N, K, E, int(not disable_ue8m0_cast), _stream(c_bf16)), what)
+
+
+def moe_permute_contiguous(x: torch.Tensor, x_scale: torch.Tensor, topk_ids: torch.Tensor, num_experts: int,
+                           alignment: int, M_sum: int, x_perm: torch.Tensor, scale_perm: torch.Tensor,
+                           expert_ids: torch.Tensor, inv_perm: torch.Tensor, zero_padding: bool = True) -> None:
+    """Scatter the rows of ``x [M, K]`` and ``x_scale [M, K/128]`` into the
+    expert-contiguous layout ``x_perm [M_sum, K]`` / ``scale_perm``, writing
+    ``expert_ids [M_sum]`` and ``inv_perm [M, top_k]`` (int32)."""
+    what = "moe_permute_contiguous"
+    _dev_check(what, x, x_scale, topk_ids, x_perm, scale_perm, expert_ids, inv_perm)
+    _dtype_check(what, x_scale, torch.float32, "x_scale")
+    _dtype_check(what, scale_perm, torch.float32, "scale_perm")
+    _dtype_check(what, expert_ids, torch.int32, "expert_ids")
+    _dtype_check(what, inv_perm, torch.int32, "inv_perm")
+    if x_perm.dtype != x.dtype:
+        raise TypeError(f"{what}: x_perm must be {x.dtype}, got {x_perm.dtype}")
+    if topk_ids.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"{what}: topk_ids must be int32 or int64, got {topk_ids.dtype}")
+    if x.dim() != 2 or topk_ids.dim() != 2 or topk_ids.shape[0] != x.shape[0]:
+        raise ValueError(f"{what}: x [M, K] and topk_ids [M, top_k] expected, got {tuple(x.shape)} and "
+                         f"{tuple(topk_ids.shape)}")
+    M, K = x.shape
+    top_k = topk_ids.shape[1]
+    cols = K // GROUP
+    if tuple(x_scale.shape) != (M, cols):
+        raise ValueError(f"{what}: x_scale must be {(M, cols)}, got {tuple(x_scale.shape)}")
+    if tuple(x_perm.shape) != (M_sum, K) or tuple(scale_perm.shape) != (M_sum, cols):
+        raise ValueError(f"{what}: outputs must be {(M_sum, K)} and {(M_sum, cols)}")
+    if tuple(expert_ids.shape) != (M_sum,) or tuple(inv_perm.shape) != (M, top_k):
+        raise ValueError(f"{what}: expert_ids must be {(M_sum,)} and inv_perm {(M, top_k)}")
+    for t, name in ((topk_ids, "topk_ids"), (x_perm, "x_perm"), (scale_perm, "scale_perm"),
+                    (expert_ids, "expert_ids"), (inv_perm, "inv_perm")):
+        if not t.is_contiguous():
+            raise ValueError(f"{what}: {name} must be contiguous")
+    esz = x.element_size()
+    if x.stride(1) != 1 and M > 1:
+        raise ValueError(f"{what}: rows of x must be contiguous")
+    L = lib()
+    ws_bytes = int(L.kbn_moe_permute_workspace_bytes(M * top_k, num_experts))
+    if ws_bytes < 0:
+        raise ValueError(f"{what}: num_experts={num_experts} outside [1, 1024] or too many pairs")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    check(L.kbn_moe_permute_contiguous(
+        topk_ids.data_ptr(), topk_ids.element_size(), M, top_k, num_experts, alignment,
+        x.data_ptr() if M else None, x.stride(0) * esz, K * esz, x_scale.data_ptr() if M else None,
+        x_scale.stride(0), x_scale.stride(1), cols, M_sum, x_perm.data_ptr(), scale_perm.data_ptr(),
+        expert_ids.data_ptr(), inv_perm.data_ptr(), int(zero_padding), ws.data_ptr(), ws_bytes,
+        _stream(x_perm)), what)
+
+
+def moe_unpermute_reduce(y: torch.Tensor, inv_perm: torch.Tensor, topk_weights: torch.Tensor,
+                         out: torch.Tensor) -> None:
+    """``out[m] = sum_j topk_weights[m, j] * y[inv_perm[m, j]]`` (bf16 rows,
+    fp32 sum in slot order)."""
+    what = "moe_unpermute_reduce"
+    _dev_check(what, y, inv_perm, topk_weights, out)
+    _dtype_check(what, y, torch.bfloat16, "mm2_out")
+    _dtype_check(what, out, torch.bfloat16, "output")
+    _dtype_check(what, inv_perm, torch.int32, "inv_perm")
+    if topk_weights.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"{what}: topk_weights must be float32 or bfloat16, got {topk_weights.dtype}")
+    M, H = out.shape
+    if tuple(inv_perm.shape) != tuple(topk_weights.shape) or inv_perm.dim() != 2 or inv_perm.shape[0] != M:
+        raise ValueError(f"{what}: inv_perm and topk_weights must both be [{M}, top_k], got "
+                         f"{tuple(inv_perm.shape)} and {tuple(topk_weights.shape)}")
+    if y.dim() != 2 or y.shape[1] != H:
+        raise ValueError(f"{what}: mm2_out must be [M_sum, {H}], got {tuple(y.shape)}")
+    if not (inv_perm.is_contiguous() and topk_weights.is_contiguous()):
+        raise ValueError(f"{what}: inv_perm and topk_weights must be contiguous")
+    if (y.stride(1) != 1 and y.shape[0] > 1) or (out.stride(1) != 1 and M > 1):
+        raise ValueError(f"{what}: rows of mm2_out and output must be contiguous")
+    check(lib().kbn_moe_unpermute_reduce(
+        y.data_ptr(), y.shape[0], H, y.stride(0), inv_perm.data_ptr(), M, inv_perm.shape[1],
+        topk_weights.data_ptr(), int(topk_weights.dtype == torch.bfloat16), out.data_ptr(), out.stride(0),
+        _stream(out)), what)
 
 
 def debug_silu_bf16(g_bits: torch.Tensor, out_bits: torch.Tensor) -> None:

@@ -7,16 +7,18 @@ Mirrors ``FusedExperts`` of ``tasks/baseline/L2/fused_experts.py:139-283``
     1x128 quant (row-major scales) -> contiguous permute -> grouped GEMM1 (w13)
     -> fused SiLU*Mul + 1x128 quant -> grouped GEMM2 (w2) -> unpermute-and-reduce
 
-Every compute step runs in this package's gfx950 kernels
-(``PerTokenGroupQuantFp8``, ``m_grouped_fp8_gemm_nt_contiguous``,
-``SiluMulQuantFp8``); the permute and the weighted reduction are the
-device-side tensor ops of ``moe_layout``.  Scratch buffers are shared by all
-layers, as in the reference (layers run one after another).
+Every step runs in this package's gfx950 kernels: ``PerTokenGroupQuantFp8``,
+the permute and unpermute-and-reduce of ``moe_layout``,
+``m_grouped_fp8_gemm_nt_contiguous`` and ``SiluMulQuantFp8``.  Scratch
+buffers are shared by all layers, as in the reference (layers run one after
+another).
 
 The reference falls back to its Triton ``fused_moe_kernel`` for BF16 weights,
 for shapes DeepGEMM does not take and while a CUDA graph is being captured
-(:228-244); that kernel family is not part of this path, so those cases raise
-``NotImplementedError`` here instead of running something else.
+(:228-244).  Here nothing on the path synchronises with the host, so the
+layer is captured as it runs eagerly.  The Triton kernel family is not part
+of this path: BF16 experts and off-gate shapes raise ``NotImplementedError``
+instead of running something else.
 """
 from __future__ import annotations
 
@@ -36,14 +38,24 @@ _FP8_GROUP_SIZE = 128
 
 
 class _SharedBuf:
-    """Scratch buffers shared by every FusedExperts layer (reference :139-153)."""
-    __slots__ = ("a_fp8_1", "a_scale_1", "dg_ws1", "dg_ws2")
+    """Scratch buffers shared by every FusedExperts layer (reference :139-153).
+
+    ``captured`` keeps every buffer a HIP graph was captured with alive for
+    the life of the process: a later, larger call replaces the buffer here,
+    but the graph's kernels still address the old one."""
+    __slots__ = ("a_fp8_1", "a_scale_1", "dg_ws1", "dg_ws2", "captured")
 
     def __init__(self):
         self.a_fp8_1 = None
         self.a_scale_1 = None
         self.dg_ws1 = None
         self.dg_ws2 = None
+        self.captured = {}
+
+    def hold_for_graph(self):
+        for t in (self.a_fp8_1, self.a_scale_1, self.dg_ws1, self.dg_ws2):
+            if t is not None:
+                self.captured.setdefault(id(t), t)
 
 
 _SHARED_BUF = _SharedBuf()
@@ -103,9 +115,6 @@ class FusedExperts(nn.Module):
         if not _valid_deep_gemm(hidden_states, w13, w2):
             raise NotImplementedError("FusedExperts: shapes outside the contiguous grouped-GEMM gate "
                                       "(the reference falls back to its Triton kernel)")
-        if torch.cuda.is_current_stream_capturing():
-            raise NotImplementedError("FusedExperts: the reference leaves this path during graph capture "
-                                      "(fused_experts.py:230)")
         s13 = w13_scale_dg if w13_scale_dg is not None else w13_scale
         s2 = w2_scale_dg if w2_scale_dg is not None else w2_scale
         if s13 is None or s2 is None:
@@ -124,8 +133,10 @@ class FusedExperts(nn.Module):
         a_fp8, a_scale = self._get_fp8_bufs(M, K, dev)
         self.per_token_group_quant_fp8(hidden_states, a_fp8, a_scale)
 
+        # padding rows stay unwritten: the grouped GEMM skips them and never
+        # writes their output rows, so nothing downstream reads them
         a1_perm, a1_scale_perm, expert_ids, inv_perm = _deepgemm_permute(a_fp8, a_scale, topk_ids, num_experts,
-                                                                        alignment)
+                                                                        alignment, zero_padding=False)
 
         mm1_out = self._get_dg_workspace(1, (M_sum, N2), dev, hidden_states.dtype)
         m_grouped_fp8_gemm_nt_contiguous((a1_perm, a1_scale_perm), (w13, w13_scale), mm1_out, expert_ids)
@@ -138,4 +149,6 @@ class FusedExperts(nn.Module):
 
         output = torch.empty(M, K, dtype=hidden_states.dtype, device=dev)
         _deepgemm_unpermute_and_reduce(mm2_out, topk_ids, topk_weights, inv_perm, output)
+        if torch.cuda.is_current_stream_capturing():
+            self._sb.hold_for_graph()
         return output

@@ -21,6 +21,11 @@ Parity pins (see ``tests/test_oracle.py``):
   * GEMM: float64 brute force on tiny shapes, torch fp32 dequant-matmul on
     small shapes, and closed-form special cases (single non-zero K block,
     identity-like weights, all-equal scales).
+  * MoE layout: brute-force placement on small routings (each expert's rows
+    counted by a direct loop), the structural invariants of the layout
+    (segments start on alignment boundaries, (token, slot) order inside a
+    segment, injective destinations), and the reference's torch formula for
+    the unpermute-and-reduce (fp32 and bf16 weights) within one bf16 ulp.
 """
 from __future__ import annotations
 
@@ -298,12 +303,15 @@ def permute_contiguous(topk_ids: np.ndarray, num_experts: int, alignment: int):
 
     Expert e owns rows [off[e], off[e] + roundup(count[e], align)); the first
     count[e] of them hold its tokens in (token, slot) order (stable sort) and
-    carry id e, the rest are padding with id -1."""
+    carry id e, the rest are padding with id -1.  A pair whose id lies outside
+    [0, num_experts) is dropped (dest -1); the reference's scatter_add fails
+    on such ids instead."""
     ids = np.asarray(topk_ids, dtype=np.int64)
     M, k = ids.shape
     flat = ids.reshape(-1)
     M_sum = compute_aligned_M(M, k, num_experts, alignment)
-    counts = np.bincount(flat, minlength=num_experts).astype(np.int64)
+    valid = (flat >= 0) & (flat < num_experts)
+    counts = np.bincount(flat[valid], minlength=num_experts).astype(np.int64)
     aligned = (counts + alignment - 1) // alignment * alignment
     off = np.zeros(num_experts + 1, dtype=np.int64)
     off[1:] = np.cumsum(aligned)
@@ -311,17 +319,38 @@ def permute_contiguous(topk_ids: np.ndarray, num_experts: int, alignment: int):
     for e in range(num_experts):
         expert_ids[off[e]:off[e] + counts[e]] = e
     order = np.argsort(flat, kind="stable")
-    within = np.empty_like(flat)
+    within = np.zeros_like(flat)
     seen = np.zeros(num_experts, dtype=np.int64)
     for pos in order:
         e = flat[pos]
-        within[pos] = seen[e]
-        seen[e] += 1
-    dest = off[flat] + within
+        if 0 <= e < num_experts:
+            within[pos] = seen[e]
+            seen[e] += 1
+    dest = np.where(valid, off[np.where(valid, flat, 0)] + within, -1)
     return expert_ids, dest, M_sum
 
 
-def unpermute_and_reduce(mm2_out_f32: np.ndarray, inv_perm: np.ndarray, topk_weights: np.ndarray) -> np.ndarray:
-    """fused_experts.py:119-136: out[m] = sum_j w[m,j] * mm2_out[inv_perm[m,j]]."""
-    g = mm2_out_f32[np.asarray(inv_perm, dtype=np.int64)]
-    return (g * np.asarray(topk_weights, dtype=np.float32)[..., None]).sum(axis=1)
+def unpermute_and_reduce(mm2_out_f32: np.ndarray, inv_perm: np.ndarray, topk_weights: np.ndarray,
+                         bf16_products: bool = False) -> np.ndarray:
+    """fused_experts.py:119-136: out[m] = sum_j w[m,j] * mm2_out[inv_perm[m,j]]
+    (float32 result; the reference then rounds it into the bf16 output).
+
+    The reference multiplies the bf16 rows by the weights in torch, so each
+    product is rounded to float32 (float32 weights) or to bf16 (bf16 weights,
+    ``bf16_products``), and sums the top_k products in float32.  The sum is
+    taken here in slot order j = 0, 1, ..., one rounding per addition,
+    starting from +0.  Slots whose inv_perm is outside [0, rows) contribute
+    nothing."""
+    y = np.asarray(mm2_out_f32, dtype=np.float32)
+    inv = np.asarray(inv_perm, dtype=np.int64)
+    w = np.asarray(topk_weights, dtype=np.float32)
+    M, k = inv.shape
+    out = np.zeros((M, y.shape[1]), dtype=np.float32)
+    for j in range(k):
+        r = inv[:, j]
+        ok = (r >= 0) & (r < y.shape[0])
+        p = (y[np.where(ok, r, 0)] * w[:, j:j + 1]).astype(np.float32)
+        if bf16_products:
+            p = bf16_bits_to_f32(f32_to_bf16_bits(p))
+        out = np.where(ok[:, None], (out + p).astype(np.float32), out)
+    return out

@@ -177,20 +177,58 @@ def test_compute_aligned_m():
         assert _compute_aligned_M(*args) == oracle.compute_aligned_M(*args)
 
 
-def test_moe_layout_on_cpu_matches_oracle():
-    """The permute glue is device-agnostic torch; check it on CPU tensors."""
-    import numpy as np
-    import oracle
-    from kb_nano_amd.moe_layout import _deepgemm_permute
-    rng = np.random.default_rng(1)
-    M, k, E, K = 60, 4, 16, 256
-    topk = np.stack([rng.choice(E, k, replace=False) for _ in range(M)])
-    ids_o, dest_o, M_sum = oracle.permute_contiguous(topk, E, 128)
-    hid = torch.randn(M, K)
-    a_perm, s_perm, ids, inv = _deepgemm_permute(hid, torch.rand(M, 2), torch.from_numpy(topk), E, 128)
-    assert a_perm.shape == (M_sum, K)
-    assert np.array_equal(ids.numpy(), ids_o)
-    assert np.array_equal(inv.numpy().reshape(-1), dest_o)
+def test_moe_layout_has_no_cpu_path():
+    """The permute and the unpermute run only in the HIP kernels."""
+    from kb_nano_amd.moe_layout import _deepgemm_permute, _deepgemm_unpermute_and_reduce
+    topk = torch.zeros(4, 2, dtype=torch.int64)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        _deepgemm_permute(torch.zeros(4, 256, dtype=torch.float8_e4m3fn), torch.ones(4, 2), topk, 8, 128)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        _deepgemm_unpermute_and_reduce(torch.zeros(1024, 256, dtype=torch.bfloat16), topk, torch.ones(4, 2),
+                                       torch.zeros(4, 2, dtype=torch.int32), torch.empty(4, 256, dtype=torch.bfloat16))
+
+
+def test_moe_permute_workspace_query():
+    from kb_nano_amd._lib import lib
+    L = lib()
+    assert L.kbn_moe_permute_workspace_bytes(32768, 0) == -1
+    assert L.kbn_moe_permute_workspace_bytes(32768, 1025) == -1
+    assert L.kbn_moe_permute_workspace_bytes(-1, 8) == -1
+    # no pairs: counts and offsets only
+    assert L.kbn_moe_permute_workspace_bytes(0, 256) == 1024 + 1040
+    # cfg4: 32 chunks x 256 experts of histograms, a rank per pair, counts, offsets
+    assert L.kbn_moe_permute_workspace_bytes(32768, 256) == 32 * 256 * 4 + 32768 * 4 + 1024 + 1040
+    # chunks grow past 256 x 1024 pairs so the scan stays short
+    n = 1 << 20
+    assert L.kbn_moe_permute_workspace_bytes(n, 64) == 256 * 64 * 4 + n * 4 + 256 + 272
+
+
+def test_moe_permute_rejects_bad_arguments():
+    from kb_nano_amd._lib import lib
+    L = lib()
+    p = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+
+    def call(ids_bytes=8, M=4, k=2, E=8, align=128, ld=256, row=256, M_sum=None, ws=1 << 20):
+        M_sum = (M * k + E * (align - 1) + align - 1) // align * align if M_sum is None else M_sum
+        return L.kbn_moe_permute_contiguous(p, ids_bytes, M, k, E, align, p, ld, row, p, 2, 1, 2, M_sum,
+                                            p, p, p, p, 1, p, ws, None)
+    assert call(ids_bytes=2) == 1 and "ids_bytes" in _err()
+    assert call(E=2000) == 1 and "num_experts" in _err()
+    assert call(M_sum=1152) == 1 and "M_sum" in _err()   # the right value is 1024
+    assert call(row=100, ld=100) == 1 and "multiple of 16" in _err()
+    assert call(ld=128) == 1 and "row stride" in _err()
+    assert call(ws=16) == 1 and "workspace" in _err()
+
+
+def test_moe_unpermute_rejects_bad_arguments():
+    from kb_nano_amd._lib import lib
+    L = lib()
+    p = ctypes.c_void_p(4096)
+    assert L.kbn_moe_unpermute_reduce(p, 1024, 100, 100, p, 4, 2, p, 0, p, 100, None) == 1
+    assert "multiple of 8" in _err()
+    assert L.kbn_moe_unpermute_reduce(p, 1024, 256, 256, p, 4, 2, p, 0, ctypes.c_void_p(4100), 256, None) == 1
+    assert "aligned" in _err()
+    assert L.kbn_moe_unpermute_reduce(None, 1024, 256, 256, None, 0, 2, None, 0, None, 256, None) == 0  # M = 0
 
 
 def test_fused_experts_surface():

@@ -279,25 +279,3 @@ def test_grouped_gemm_free_function_colmajor_scales(gpu_device):
     ref = oracle.grouped_gemm_nt_sample(qa, sa, qb, sb, ids)
     valid = ids >= 0
     assert_gemm_close(C[torch.from_numpy(valid).to(dev)], ref[valid], "grouped free fn")
-
-
-def test_moe_layout_matches_oracle(gpu_device):
-    from kb_nano_amd.moe_layout import _deepgemm_permute, _deepgemm_unpermute_and_reduce
-    rng = np.random.default_rng(0)
-    M, k, E, K = 200, 8, 32, 256
-    topk = np.stack([rng.choice(E, k, replace=False) for _ in range(M)])
-    ids_o, dest_o, M_sum = oracle.permute_contiguous(topk, E, 128)
-    dev = gpu_device
-    hid = torch.randn(M, K, device=dev).bfloat16()
-    sc = torch.rand(M, K // 128, device=dev)
-    a_perm, s_perm, ids, inv = _deepgemm_permute(hid, sc, torch.from_numpy(topk).to(dev), E, 128)
-    assert np.array_equal(ids.cpu().numpy(), ids_o)
-    assert np.array_equal(inv.cpu().numpy().reshape(-1), dest_o)
-    assert torch.equal(a_perm[torch.from_numpy(dest_o).to(dev)], hid.repeat_interleave(k, 0))
-    assert torch.all(a_perm[ids < 0] == 0)
-    w = torch.rand(M, k, device=dev)
-    out = torch.empty(M, K, device=dev)
-    mm2 = torch.randn(M_sum, K, device=dev)
-    _deepgemm_unpermute_and_reduce(mm2, torch.from_numpy(topk).to(dev), w, inv, out)
-    ref = oracle.unpermute_and_reduce(mm2.cpu().numpy(), inv.cpu().numpy(), w.cpu().numpy())
-    assert np.allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-5)

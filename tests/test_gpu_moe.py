@@ -81,3 +81,223 @@ def test_fused_experts_rejects_paths_it_does_not_take(gpu_device):
         FusedExperts()(h, torch.zeros(4, 512, 256, dtype=torch.float8_e4m3fn, device=dev), small, w, ids, 4,
                        w13_scale=torch.ones(4, 4, 2, device=dev), w2_scale=torch.ones(4, 2, 2, device=dev),
                        use_fp8_w8a8=True)
+
+
+# ------------------------------------------------------------------ layout
+# The permute and the unpermute-and-reduce kernels (fused_experts.py:42-136)
+# against the oracle: the layout is index-exact, the copied rows byte-exact,
+# and the reduction bit-exact (same products, fp32 sum in slot order).
+
+def _routing(M, k, E, seed):
+    rng = np.random.default_rng(seed)
+    if M == 0:
+        return np.zeros((0, k), dtype=np.int64)
+    return np.argsort(rng.random((M, E)), axis=1)[:, :k].astype(np.int64)   # k distinct experts per token
+
+
+def _rand_bytes(shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, 256, shape, dtype=torch.uint8, generator=g)
+
+
+@pytest.mark.parametrize("M,k,E,align,K,ids_dtype,colmajor", [
+    (200, 8, 32, 128, 256, torch.int64, False),
+    (1, 1, 1, 128, 128, torch.int32, False),
+    (0, 4, 8, 128, 128, torch.int64, False),
+    (300, 6, 256, 128, 7168, torch.int32, True),
+    (5000, 8, 1024, 1, 128, torch.int32, False),      # most experts, no padding
+    (70000, 4, 64, 16, 128, torch.int64, False),      # > 256 x 1024 pairs: 2048-pair chunks
+])
+def test_permute_matches_oracle(gpu_device, M, k, E, align, K, ids_dtype, colmajor):
+    from kb_nano_amd.moe_layout import _deepgemm_permute
+    dev = gpu_device
+    print(f"permute M={M} k={k} E={E} align={align} K={K}", flush=True)
+    topk = _routing(M, k, E, seed=M + E)
+    ids_o, dest_o, M_sum = oracle.permute_contiguous(topk, E, align)
+    x = _rand_bytes((M, K), seed=1)
+    xs = torch.rand(K // 128, M).t() if colmajor else torch.rand(M, K // 128)
+    a_perm, s_perm, ids, inv = _deepgemm_permute(x.to(dev).view(torch.float8_e4m3fn), xs.to(dev),
+                                                 torch.from_numpy(topk).to(ids_dtype).to(dev), E, align)
+    torch.cuda.synchronize()
+    assert a_perm.shape == (M_sum, K) and s_perm.shape == (M_sum, K // 128)
+    assert ids.dtype == torch.int32 and inv.dtype == torch.int32 and inv.shape == (M, k)
+    assert np.array_equal(ids.cpu().numpy(), ids_o)
+    assert np.array_equal(inv.cpu().numpy().reshape(-1), dest_o)
+    xp = a_perm.view(torch.uint8).cpu().numpy()
+    sp = s_perm.cpu().numpy()
+    src = np.repeat(np.arange(M), k)
+    assert np.array_equal(xp[dest_o], x.numpy()[src])
+    assert np.array_equal(sp[dest_o], xs.contiguous().numpy()[src])
+    pad = ids_o < 0
+    assert not xp[pad].any() and not sp[pad].any()       # torch.zeros padding, as in the reference
+
+
+def test_permute_without_zero_padding_leaves_padding_rows(gpu_device):
+    from kb_nano_amd import _ops
+    dev = gpu_device
+    M, k, E, K = 130, 4, 16, 256
+    topk = _routing(M, k, E, seed=5)
+    ids_o, dest_o, M_sum = oracle.permute_contiguous(topk, E, 128)
+    x = _rand_bytes((M, K), seed=2).to(dev)
+    xs = torch.rand(M, 2, device=dev)
+    xp = torch.full((M_sum, K), 0xAB, dtype=torch.uint8, device=dev)
+    sp = torch.full((M_sum, 2), -3.0, device=dev)
+    ids = torch.full((M_sum,), 77, dtype=torch.int32, device=dev)
+    inv = torch.empty(M, k, dtype=torch.int32, device=dev)
+    _ops.moe_permute_contiguous(x, xs, torch.from_numpy(topk).to(dev), E, 128, M_sum, xp, sp, ids, inv,
+                                zero_padding=False)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy(), ids_o)
+    pad = torch.from_numpy(ids_o < 0).to(dev)
+    assert torch.all(xp[pad] == 0xAB) and torch.all(sp[pad] == -3.0)
+    d = torch.from_numpy(dest_o).to(dev)
+    assert torch.equal(xp[d], x.repeat_interleave(k, 0)) and torch.equal(sp[d], xs.repeat_interleave(k, 0))
+
+
+def test_permute_drops_out_of_range_ids(gpu_device):
+    from kb_nano_amd.moe_layout import _deepgemm_permute
+    dev = gpu_device
+    M, k, E, K = 64, 4, 8, 128
+    topk = _routing(M, k, E, seed=9)
+    topk[3, 1] = -1
+    topk[10, 0] = E
+    topk[11, 3] = 1 << 40                                 # would wrap to a valid id in 32 bits
+    ids_o, dest_o, M_sum = oracle.permute_contiguous(topk, E, 128)
+    assert (dest_o < 0).sum() == 3
+    x = _rand_bytes((M, K), seed=3)
+    a_perm, s_perm, ids, inv = _deepgemm_permute(x.to(dev), torch.rand(M, 1, device=dev),
+                                                 torch.from_numpy(topk).to(dev), E, 128)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy(), ids_o)
+    assert np.array_equal(inv.cpu().numpy().reshape(-1), dest_o)
+    ok = dest_o >= 0
+    assert np.array_equal(a_perm.cpu().numpy()[dest_o[ok]], x.numpy()[np.repeat(np.arange(M), k)[ok]])
+
+
+def _unpermute_inputs(M, k, H, rows, wdtype, seed, holes):
+    g = torch.Generator().manual_seed(seed)
+    y = (torch.randn(rows, H, generator=g) * 3).bfloat16()
+    inv = torch.stack([torch.randperm(rows, generator=g)[:k] for _ in range(M)]).to(torch.int32)
+    if holes:   # slots outside [0, rows) contribute nothing
+        inv[0, 0] = -1
+        inv[M // 2, k - 1] = rows + 5
+    w = torch.softmax(torch.randn(M, k, generator=g), -1).to(wdtype)
+    return y, inv, w
+
+
+@pytest.mark.parametrize("M,k,H,rows,wdtype", [
+    (300, 8, 7168, 3000, torch.float32),
+    (77, 6, 200, 500, torch.bfloat16),
+    (1, 1, 8, 1, torch.float32),
+    (64, 9, 1032, 900, torch.float32),       # top_k not a multiple of 4, H not of 1024
+])
+def test_unpermute_matches_oracle(gpu_device, M, k, H, rows, wdtype):
+    from kb_nano_amd.moe_layout import _deepgemm_unpermute_and_reduce
+    dev = gpu_device
+    print(f"unpermute M={M} k={k} H={H} w={wdtype}", flush=True)
+    y, inv, w = _unpermute_inputs(M, k, H, rows, wdtype, seed=M, holes=rows > k)
+    out = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
+    _deepgemm_unpermute_and_reduce(y.to(dev), torch.zeros(M, k, dtype=torch.int64, device=dev), w.to(dev),
+                                   inv.to(dev), out)
+    torch.cuda.synchronize()
+    ref = oracle.unpermute_and_reduce(oracle.bf16_bits_to_f32(bf16_bits(y)), inv.numpy(), w.float().numpy(),
+                                      bf16_products=wdtype == torch.bfloat16)
+    assert np.array_equal(bf16_bits(out), oracle.f32_to_bf16_bits(ref))
+
+
+@pytest.mark.parametrize("wdtype", [torch.float32, torch.bfloat16])
+def test_unpermute_matches_reference_torch_formula(gpu_device, wdtype):
+    """The reference's own torch ops (fused_experts.py:130-136) run on the GPU.
+    The products are the same; torch may add them in another order, which
+    moves the fp32 sum by at most top_k * 2^-24 * sum|p_j|, so the bf16
+    results differ by at most one bf16 ulp plus that."""
+    from kb_nano_amd.moe_layout import _deepgemm_unpermute_and_reduce
+    dev = gpu_device
+    M, k, H, rows = 256, 8, 2048, 4096
+    y, inv, w = _unpermute_inputs(M, k, H, rows, wdtype, seed=11, holes=False)
+    y, inv, w = y.to(dev), inv.to(dev), w.to(dev)
+    out = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
+    _deepgemm_unpermute_and_reduce(y, None, w, inv, out)
+    ref = torch.empty_like(out)
+    prods = y[inv.to(torch.int64).view(-1)].view(M, k, H).to(ref.dtype) * w.unsqueeze(-1)
+    ref.copy_(prods.sum(dim=1))
+    mass = prods.float().abs().sum(dim=1)
+    torch.cuda.synchronize()
+    got, want = out.float(), ref.float()
+    ulp = torch.maximum(got.abs(), want.abs()) * 2.0 ** -7
+    bound = ulp + k * 2.0 ** -24 * mass
+    assert torch.all((got - want).abs() <= bound)
+    assert np.mean(bf16_bits(out) == bf16_bits(ref)) > 0.99
+
+
+def test_layout_cfg4_full_size(gpu_device):
+    """Config 4's routing (4096 tokens, top-8 of 256 experts from seeded
+    softmax logits, hidden 7168): permute index- and byte-exact, unpermute
+    bit-exact, at full size."""
+    from kb_nano_amd.moe_layout import _deepgemm_permute, _deepgemm_unpermute_and_reduce
+    dev = gpu_device
+    T, H, E, k = 4096, 7168, 256, 8
+    g = torch.Generator().manual_seed(0)
+    topk = torch.topk(torch.softmax(torch.randn(T, E, generator=g), -1), k, dim=-1).indices
+    ids_o, dest_o, M_sum = oracle.permute_contiguous(topk.numpy(), E, 128)
+    assert M_sum == 65280
+    x = _rand_bytes((T, H), seed=4)
+    xs = torch.rand(T, H // 128, generator=g)
+    a_perm, s_perm, ids, inv = _deepgemm_permute(x.to(dev).view(torch.float8_e4m3fn), xs.to(dev), topk.to(dev),
+                                                 E, 128)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy(), ids_o)
+    assert np.array_equal(inv.cpu().numpy().reshape(-1), dest_o)
+    d = torch.from_numpy(dest_o).to(dev)
+    assert torch.equal(a_perm.view(torch.uint8)[d], x.to(dev).repeat_interleave(k, 0))
+    assert torch.equal(s_perm[d], xs.to(dev).repeat_interleave(k, 0))
+    assert not torch.any(a_perm.view(torch.uint8)[torch.from_numpy(ids_o < 0).to(dev)])
+    del a_perm, s_perm
+    w = torch.softmax(torch.randn(T, k, generator=g), -1)
+    y = (torch.randn(M_sum, H, generator=g)).bfloat16()
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    _deepgemm_unpermute_and_reduce(y.to(dev), topk.to(dev), w.to(dev), inv, out)
+    torch.cuda.synchronize()
+    ref = oracle.unpermute_and_reduce(oracle.bf16_bits_to_f32(bf16_bits(y)), dest_o.reshape(T, k), w.numpy())
+    assert np.array_equal(bf16_bits(out), oracle.f32_to_bf16_bits(ref))
+
+
+def test_fused_experts_graph_capture(gpu_device):
+    """The layer captured into a HIP graph: every replay, with eager calls on
+    other data in between, reproduces the eager output bit for bit."""
+    from kb_nano_amd.fused_experts import FusedExperts
+    dev = gpu_device
+    M, K, I, E, k = 160, 512, 640, 8, 2
+    rng = np.random.default_rng(3)
+    w13, s13 = _experts(E, 2 * I, K, seed=1)
+    w2, s2 = _experts(E, K, I, seed=2)
+    w13, w2 = to_fp8(w13, dev), to_fp8(w2, dev)
+    s13, s2 = torch.from_numpy(s13).to(dev), torch.from_numpy(s2).to(dev)
+
+    def inputs(seed):
+        h = from_bits(bf16_bits(seeded_bf16((M, K), seed=seed)), dev)
+        ids = torch.from_numpy(_routing(M, k, E, seed)).to(dev)
+        wt = torch.softmax(torch.randn(M, k, device=dev), -1)
+        return h, ids, wt
+
+    layer = FusedExperts()
+    run = lambda h, ids, wt: layer(h, w13, w2, wt, ids, E, w13_scale=s13, w2_scale=s2, use_fp8_w8a8=True,
+                                   block_shape=[128, 128])
+    h, ids, wt = inputs(21)
+    eager = run(h, ids, wt).clone()
+    h2, ids2, wt2 = inputs(22)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run(h, ids, wt)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_g = run(h, ids, wt)
+    for rep in range(3):
+        other = run(h2, ids2, wt2)                        # eager work reusing the shared buffers
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, eager), f"replay {rep}"
+        assert not torch.equal(other, eager)

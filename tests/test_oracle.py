@@ -343,6 +343,80 @@ def test_compute_aligned_M_cfg4():
     assert oracle.compute_aligned_M(4096, 8, 256, 128) == 65280
 
 
+def _brute_force_layout(topk, E, align):
+    """Placement by direct counting, independent of the oracle's sort: walk
+    the experts in order, give each its pairs in (token, slot) order, then
+    round its row count up to the alignment."""
+    M, k = topk.shape
+    M_sum = oracle.compute_aligned_M(M, k, E, align)
+    dest = np.full(M * k, -1, dtype=np.int64)
+    ids = np.full(M_sum, -1, dtype=np.int32)
+    row = 0
+    for e in range(E):
+        n_e = 0
+        for m in range(M):
+            for j in range(k):
+                if topk[m, j] == e:
+                    dest[m * k + j] = row + n_e
+                    ids[row + n_e] = e
+                    n_e += 1
+        row += -(-n_e // align) * align
+    return ids, dest, M_sum
+
+
+@pytest.mark.parametrize("M,k,E,align,seed", [(50, 4, 8, 16, 0), (9, 3, 5, 4, 1), (1, 1, 1, 128, 2),
+                                              (0, 2, 3, 8, 3), (40, 6, 7, 1, 4)])
+def test_permute_contiguous_brute_force(M, k, E, align, seed):
+    rng = np.random.default_rng(seed)
+    topk = rng.integers(0, E, size=(M, k))
+    ids, dest, M_sum = oracle.permute_contiguous(topk, E, align)
+    ids_b, dest_b, M_sum_b = _brute_force_layout(topk, E, align)
+    assert M_sum == M_sum_b
+    assert np.array_equal(ids, ids_b)
+    assert np.array_equal(dest, dest_b)
+
+
+def test_permute_contiguous_drops_out_of_range_ids():
+    topk = np.array([[0, 3], [-1, 1], [5, 0], [1, 1]])
+    ids, dest, M_sum = oracle.permute_contiguous(topk, 4, 2)
+    # valid pairs only: e0 <- (0,0), (2,1); e1 <- (1,1), (3,0), (3,1); e3 <- (0,1)
+    # rounded counts 2, 4, 0, 2 -> offsets 0, 2, 6, 6
+    assert dest.tolist() == [0, 6, -1, 2, -1, 1, 3, 4]
+    assert ids.tolist() == [0, 0, 1, 1, 1, -1, 3, -1, -1, -1, -1, -1]
+    assert M_sum == oracle.compute_aligned_M(4, 2, 4, 2)
+
+
+@pytest.mark.parametrize("wdtype", [torch.float32, torch.bfloat16])
+def test_unpermute_matches_reference_formula(wdtype):
+    """The reference's torch formula (fused_experts.py:130-136) on CPU:
+    gather, ``.to(bf16) * weights``, ``.sum(dim=1)``, copy into bf16."""
+    g = torch.Generator().manual_seed(7)
+    M, k, H, rows = 64, 8, 256, 700
+    y = torch.randn(rows, H, generator=g).bfloat16()
+    inv = torch.stack([torch.randperm(rows, generator=g)[:k] for _ in range(M)]).to(torch.int32)
+    w = torch.softmax(torch.randn(M, k, generator=g), -1).to(wdtype)
+    out = torch.empty(M, H, dtype=torch.bfloat16)
+    gathered = y[inv.to(torch.int64).view(-1)].view(M, k, H)
+    out.copy_((gathered.to(out.dtype) * w.unsqueeze(-1)).sum(dim=1))
+    got = oracle.unpermute_and_reduce(oracle.bf16_bits_to_f32(y.view(torch.int16).numpy().view(np.uint16)),
+                                      inv.numpy(), w.float().numpy(), bf16_products=wdtype == torch.bfloat16)
+    got_bits = oracle.f32_to_bf16_bits(got).astype(np.int32)
+    ref_bits = out.view(torch.int16).numpy().view(np.uint16).astype(np.int32)
+    # same products; the fp32 sum may differ in order, so allow one bf16 ulp
+    assert np.max(np.abs(got_bits - ref_bits)) <= 1
+    assert np.mean(got_bits == ref_bits) > 0.99
+
+
+def test_unpermute_slot_order_and_skips():
+    y = np.array([[1.0, 2.0], [3.0, 4.0], [1e8, -1e8]], dtype=np.float32)
+    inv = np.array([[2, 0, 2], [1, -1, 5]])
+    w = np.array([[1.0, 1.0, -1.0], [0.5, 9.0, 9.0]], dtype=np.float32)
+    out = oracle.unpermute_and_reduce(y, inv, w)
+    # slot order: (1e8 + 1) - 1e8 = 0 in fp32 (1 is lost), not 1
+    assert out[0].tolist() == [0.0, 0.0]
+    assert out[1].tolist() == [1.5, 2.0]    # rows -1 and 5 are outside [0, 3)
+
+
 # ----------------------------------------------------------- golden fixtures
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
