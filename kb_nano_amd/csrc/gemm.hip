@@ -12,9 +12,13 @@
 //    a power of two and applied inside the block-scaled MFMA
 //    (v_mfma_scale_f32_32x32x64_f8f6f4) as an E8M0 operand, so one fp32
 //    accumulator set runs across all of K with no promotion epilogue.
-//  * FP32 (disable_ue8m0_cast): scales are used as given; each 128-K stage
-//    accumulates a fresh partial with plain fp8 MFMA and is promoted into the
-//    running sum with one FMA per element and stage.
+//  * FP32 (disable_ue8m0_cast): scales are used as given.  Each scale splits
+//    exactly into a power of two, applied by the MFMA as above, and a
+//    significand in [1, 2).  The accumulators hold the running sum in units
+//    of the current block's significand product (per row) and are rescaled
+//    by the ratio of consecutive products when a block starts; the last
+//    product multiplies the sum before the store.  Power-of-two scales give
+//    ratios of 1 and skip the rescale, so such scales cost what UE8M0 does.
 //
 // Dataflow per workgroup (256 lanes = 4 wavefronts, one per SIMD):
 //   HBM --buffer_load_dwordx4 ... lds (direct DMA)--> LDS (kStages x (BM+BN) x 128 B)
@@ -36,6 +40,16 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit dword format (gfx9 family)
+
+// FP32 scale contract: s = 2^(byte - 127) * mant with byte the biased
+// exponent field (the block-scaled MFMA's E8M0 operand, exact) and mant the
+// significand in [1, 2).  Zero and subnormal scales get byte 0 (2^-127), so
+// their block adds at most 2^-127 of the value it would have at scale 1;
+// inf/NaN scales get 255, the E8M0 NaN.
+__device__ __forceinline__ int scale_exp_byte(float s) { return (int)((__float_as_uint(s) >> 23) & 0xFFu); }
+__device__ __forceinline__ float scale_mant(float s) {
+    return __uint_as_float((__float_as_uint(s) & 0x007FFFFFu) | 0x3F800000u);
+}
 
 struct GemmArgs {
     const uint8_t* A;
@@ -286,20 +300,77 @@ gemm_bs_kernel(const GemmArgs a) {
     };
     v8i fa0[FM], fb0[FN], fa1[FM], fb1[FN];
     float sa[FM], sw = 0.f, nsa[FM], nsw = 0.f;
-    v16f part[kUe8m0 ? 1 : FM][kUe8m0 ? 1 : FN];
     int ea[FM], eb = 0, nea[FM], neb = 0;
+    // FP32 contract: mantissa product mu = mant(sA) mant(sW) in [1, 4) of the
+    // current block per fragment row, and the rescale ratio mu_prev / mu for
+    // the block about to start (the exponents go to the MFMA).
+    float mu[kUe8m0 ? 1 : FM], ratio[kUe8m0 ? 1 : FM];
+    bool rescale = false;
+    // Grouped FP32 contract: rows of another expert (padding) are never
+    // stored, so their scales, whatever the buffer holds, must not trigger
+    // rescales; they keep a mantissa product of 1.
+    bool row_live[kGrouped && !kUe8m0 ? FM : 1];
+    if constexpr (kGrouped && !kUe8m0) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) row_live[i] = a.expert_ids[m0 + wm * TM + i * 32 + (lane & 31)] == expert;
+    }
+    // E8M0 bytes of raw scales; FP32 contract: the first block's mantissa
+    // products (step < 0), or the ratios to the next block's products, which
+    // then become current (their block follows)
+    auto convert = [&](const float (&s)[FM], float w, int (&e)[FM], int& f, int step) {
+        if constexpr (kUe8m0) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) e[i] = ue8m0_ceil_byte(s[i]);
+            f = ue8m0_ceil_byte(w);
+        } else {
+            const float mw = scale_mant(w);
+            float m[FM];
+            bool diff = false;
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                e[i] = scale_exp_byte(s[i]);
+                m[i] = scale_mant(s[i]) * mw;
+                if constexpr (kGrouped) m[i] = row_live[i] ? m[i] : 1.f;
+                diff |= m[i] != mu[i];
+            }
+            f = scale_exp_byte(w);
+            if (step >= 0) {
+                // the quotient of two different values in [1, 4) is never 1,
+                // so the divisions are needed exactly when a product changed
+                rescale = __any(diff);
+                if (rescale) {
+#pragma unroll
+                    for (int i = 0; i < FM; ++i) ratio[i] = mu[i] == m[i] ? 1.f : mu[i] / m[i];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i) mu[i] = m[i];
+        }
+    };
     // MFMA t (0 <= t < FM FN) of a sub-step.  The product is formed as
     // D^T = W A^T (W fragment as the MFMA's A operand), so accumulator
     // register r of lane l holds output row (l % 32) of fragment i and column
     // 8 (r / 4) + 4 (l / 32) + r % 4 of fragment j: every lane owns runs of
-    // four consecutive columns of one row, ready for packed stores.
-    auto mfma_at = [&](int t, const v8i (&fa)[FM], const v8i (&fb)[FN], bool first) {
+    // four consecutive columns of one row, ready for packed stores.  The
+    // block's scales enter as E8M0 operands: eb for the W rows, ea[i] per A row.
+    auto mfma_at = [&](int t, const v8i (&fa)[FM], const v8i (&fb)[FN]) {
         const int i = t / FN, j = t % FN;
-        if constexpr (kUe8m0)
-            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], acc[i][j], 0, 0, 0, eb, 0, ea[i]);
-        else
-            part[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], first ? v16f{} : part[i][j], 0,
-                                                                         0, 0, 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], acc[i][j], 0, 0, 0, eb, 0, ea[i]);
+    };
+    // FP32 contract: bring the running sum to the new block's mantissa base
+    // before the block's first MFMA.  One uniform branch around all of it,
+    // so the accumulators only leave the MFMA registers when a ratio is not 1.
+    auto rescale_all = [&]() {
+        if constexpr (!kUe8m0) {
+            if (rescale) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] * ratio[i];
+            }
+        }
     };
 
     // Each sub-step is laid out as FM*FN issue slots: one MFMA, then this
@@ -321,18 +392,15 @@ gemm_bs_kernel(const GemmArgs a) {
 #pragma unroll
     for (int q = 0; q < kR; ++q) read_half(stage_ptr(0), 0, q, fa0, fb0);
 
-    if constexpr (kUe8m0) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i) ea[i] = ue8m0_ceil_byte(sa[i]);
-        eb = ue8m0_ceil_byte(sw);
-    }
+    convert(sa, sw, ea, eb, -1);
 
     for (int kb = 0; kb < KB; ++kb) {
         const uint8_t* cur = stage_ptr(kb);
+        rescale_all();
         // ---- sub-step 0: K half 0 of block kb; read K half 1
 #pragma unroll
         for (int t = 0; t < kT; ++t) {
-            mfma_at(t, fa0, fb0, true);
+            mfma_at(t, fa0, fb0);
 #pragma unroll
             for (int q = t * kR / kT; q < (t + 1) * kR / kT; ++q) read_half(cur, 1, q, fa1, fb1);
             __builtin_amdgcn_sched_barrier(0);
@@ -351,15 +419,14 @@ gemm_bs_kernel(const GemmArgs a) {
         const bool live = snext < KB;
 #pragma unroll
         for (int t = 0; t < kT; ++t) {
-            mfma_at(t, fa1, fb1, false);
+            mfma_at(t, fa1, fb1);
             if (t == 0) read_scales(nxt, nsa, nsw);
-            if constexpr (kUe8m0) {
-                // E8M0 bytes of block kb+1, half a sub-step after their reads
-                if (t == kT / 2) {
-#pragma unroll
-                    for (int i = 0; i < FM; ++i) nea[i] = ue8m0_ceil_byte(nsa[i]);
-                    neb = ue8m0_ceil_byte(nsw);
-                }
+            // converted scales of block kb+1, half a sub-step after their
+            // reads (FP32 contract: none past the last block, whose mantissa
+            // products the store needs)
+            if (t == kT / 2) {
+                if constexpr (kUe8m0) convert(nsa, nsw, nea, neb, kb);
+                else if (kb + 1 < KB) convert(nsa, nsw, nea, neb, kb);
             }
 #pragma unroll
             for (int q = t * kR / kT; q < (t + 1) * kR / kT; ++q) read_half(nxt, 0, q, fa0, fb0);
@@ -367,26 +434,30 @@ gemm_bs_kernel(const GemmArgs a) {
             for (int d = t * kDma / kT; d < (t + 1) * kDma / kT; ++d) issue_one(snext, live, d);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if constexpr (!kUe8m0) {
-            // promotion of the block: acc += part * sA[row] * sW[block]
+        // FP32 contract: the running sum is kept in units of the current
+        // block's mantissa product, S_kb = S_{kb-1} mu_{kb-1} / mu_kb + 2^e P_kb
+        // (rescale_at applies the ratio as block kb+1 starts), so the true
+        // sum after the last block is S mu_last.  Ratios of 1 (power-of-two
+        // scales, or equal mantissas) skip the multiplies.
 #pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                const float f = sa[i] * sw;
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(part[i][j][r], f, acc[i][j][r]);
-                sa[i] = nsa[i];
-            }
-            sw = nsw;
-        } else {
-#pragma unroll
-            for (int i = 0; i < FM; ++i) ea[i] = nea[i];
-            eb = neb;
-        }
+        for (int i = 0; i < FM; ++i) ea[i] = nea[i];
+        eb = neb;
     }
     // the trailing (out-of-range) loads still target this workgroup's LDS
     wait_dma();
+    if constexpr (!kUe8m0) {
+        bool any = false;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) any |= mu[i] != 1.f;
+        if (__any(any)) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] * mu[i];
+        }
+    }
 
     // Epilogue of a tile: fp32 -> bf16 (RNE), written with raw buffer stores
     // whose range ends at the last row of D, so rows past M (and any offset
@@ -661,14 +732,15 @@ static int check_scale_ranges(const char* what, int64_t M, int64_t K, int64_t sm
     return 0;
 }
 
-// Dense tile configuration: 256x256 (2 LDS stages) when M > 128, 128x128 (4
-// stages) for 64 < M <= 128, 64x128 (3 stages, two workgroups per CU) for
-// M <= 64, where the weights dominate the traffic; 128x128 for the FP32
-// scale contract.
+// Dense tile configuration: 256x256 (2 LDS stages) when M > 128 (128x256,
+// 3 stages, under the FP32 contract, whose per-row mantissa state does not
+// fit next to a 256x256 tile's accumulators), 128x128 (4 stages) for
+// 64 < M <= 128, 64x128 (3 stages, two workgroups per CU) for M <= 64,
+// where the weights dominate the traffic.
 static Schedule dense_schedule(int64_t M, int64_t N, int64_t K, int ue8m0, bool allow_split) {
     Schedule s;
-    if (!ue8m0) {
-        s.bm = 128; s.bn = 128; s.stages = 4;
+    if (M > 128 && !ue8m0) {
+        s.bm = 128; s.bn = 256; s.stages = 3;
     } else if (M > 128) {
         s.bm = 256; s.bn = 256; s.stages = 2;
     } else if (M > 64) {
@@ -681,6 +753,24 @@ static Schedule dense_schedule(int64_t M, int64_t N, int64_t K, int ue8m0, bool 
     s.kb_per_split = (int)(K / kGroup);
     if (allow_split) plan_tail(s, M, (int)(K / kGroup));
     return s;
+}
+
+template <bool kUe8m0>
+static int dispatch_dense(const GemmArgs& a, const Schedule& sc, int64_t K, hipStream_t st, const char* what) {
+    if constexpr (kUe8m0) {
+        if (sc.bm == 256 && sc.bn == 256) {
+            // short K (few K blocks per tile): two wavefronts per SIMD hide
+            // the per-tile pipeline fill and epilogue better
+            if (K <= 2048) return launch_gemm<256, 256, 2, true, false, 8>(a, sc, st, what);
+            return launch_gemm<256, 256, 2, true, false>(a, sc, st, what);
+        }
+    } else {
+        if (sc.bm == 128 && sc.bn == 256) return launch_gemm<128, 256, 3, false, false>(a, sc, st, what);
+    }
+    if (sc.bm == 128 && sc.bn == 128) return launch_gemm<128, 128, 4, kUe8m0, false>(a, sc, st, what);
+    if (sc.bm == 64 && sc.bn == 128) return launch_gemm<64, 128, 3, kUe8m0, false>(a, sc, st, what);
+    set_error("%s: no kernel for %dx%d tiles", what, sc.bm, sc.bn);
+    return 1;
 }
 
 static int gemm_nt_impl(const char* what, const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
@@ -715,17 +805,7 @@ static int gemm_nt_impl(const char* what, const void* A, int64_t lda, const floa
         }
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (!scale_ue8m0) return launch_gemm<128, 128, 4, false, false>(a, sc, st, what);
-    if (sc.bm == 256 && sc.bn == 256) {
-        // short K (few K blocks per tile): two wavefronts per SIMD hide the
-        // per-tile pipeline fill and epilogue better
-        if (K <= 2048) return launch_gemm<256, 256, 2, true, false, 8>(a, sc, st, what);
-        return launch_gemm<256, 256, 2, true, false>(a, sc, st, what);
-    }
-    if (sc.bm == 128 && sc.bn == 128) return launch_gemm<128, 128, 4, true, false>(a, sc, st, what);
-    if (sc.bm == 64 && sc.bn == 128) return launch_gemm<64, 128, 3, true, false>(a, sc, st, what);
-    set_error("%s: no kernel for %dx%d tiles", what, sc.bm, sc.bn);
-    return 1;
+    return scale_ue8m0 ? dispatch_dense<true>(a, sc, K, st, what) : dispatch_dense<false>(a, sc, K, st, what);
 }
 
 extern "C" int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
@@ -776,5 +856,5 @@ extern "C" int kbn_fp8_grouped_gemm_nt_contiguous(const void* A, int64_t lda, co
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     Schedule sc;   // grouped: data-parallel, one workgroup per 128-row block x N tile
     if (scale_ue8m0) return launch_gemm<128, 256, 3, true, true>(a, sc, st, what);
-    return launch_gemm<128, 128, 4, false, true>(a, sc, st, what);
+    return launch_gemm<128, 256, 3, false, true>(a, sc, st, what);
 }

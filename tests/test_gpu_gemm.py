@@ -279,3 +279,97 @@ def test_grouped_gemm_free_function_colmajor_scales(gpu_device):
     ref = oracle.grouped_gemm_nt_sample(qa, sa, qb, sb, ids)
     valid = ids >= 0
     assert_gemm_close(C[torch.from_numpy(valid).to(dev)], ref[valid], "grouped free fn")
+
+
+# ------------------------------------------------- FP32 scale contract
+# disable_ue8m0_cast: the scales' exponents go to the MFMA, their
+# significands are carried per row and the running sum is rescaled when they
+# change between K blocks.  These cases vary the significand in every block.
+
+def _scale_factors(shape, rng, lo=-3, hi=3):
+    """Factors 2^e * m with a random e in [lo, hi] and m in [1, 2): applied to
+    real quant scales they keep realistic magnitudes but make consecutive K
+    blocks differ in both exponent and significand."""
+    return (rng.uniform(1.0, 2.0, size=shape) * np.exp2(rng.integers(lo, hi + 1, size=shape))).astype(np.float32)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 256, 2048), (100, 384, 4096), (300, 512, 3072), (1000, 640, 1024),
+                                   (77, 203, 65536), (8, 8192, 8192)])
+def test_gemm_fp32_scales_vary_per_block(gpu_device, M, N, K):
+    rng = np.random.default_rng(M + K)
+    qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=M + N)
+    sa = (sa * _scale_factors(sa.shape, rng)).astype(np.float32)
+    sw = (sw * _scale_factors(sw.shape, rng)).astype(np.float32)
+    cols = np.arange(0, N, max(1, N // 512)) if N > 1024 else None
+    ref = oracle.gemm_nt_sample(qa, sa, qw, sw, ue8m0=False, cols=cols)
+    D = _gemm_gpu(qa, sa, qw, sw, gpu_device, ue8m0=False)
+    got = D if cols is None else D[:, torch.from_numpy(cols).to(gpu_device)]
+    assert_gemm_close(got, ref, f"fp32 scales {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 512, 768), (96, 1024, 512), (1, 256, 896), (40, 384, 640)])
+def test_gemm_fp32_contract_equals_ue8m0_on_power_of_two_scales(gpu_device, M, N, K):
+    """Power-of-two scales: both contracts add the same MFMA products in the
+    same order (no rescale, no split at fewer than 8 K blocks), so the outputs
+    are identical bit for bit."""
+    qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=5)
+    D1 = _gemm_gpu(qa, sa, qw, sw, gpu_device, ue8m0=True)
+    D0 = _gemm_gpu(qa, sa, qw, sw, gpu_device, ue8m0=False)
+    assert torch.equal(D0, D1)
+
+
+def test_gemm_fp32_zero_scale_blocks(gpu_device):
+    """A zero scale takes the E8M0 operand's floor, 2^-127, so its block adds
+    at most 2^-127 of what it would add at scale 1 (the quant kernels never
+    produce zero scales: their amax is clamped to eps)."""
+    M, N, K = 200, 384, 1536
+    rng = np.random.default_rng(8)
+    qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=8)
+    sa = (sa * _scale_factors(sa.shape, rng)).astype(np.float32)
+    sw = (sw * _scale_factors(sw.shape, rng)).astype(np.float32)
+    sa[::7, 3] = 0.0
+    sa[5, :] = 0.0
+    sw[1, 5] = 0.0
+    ref = oracle.gemm_nt_sample(qa, sa, qw, sw, ue8m0=False)
+    D = _gemm_gpu(qa, sa, qw, sw, gpu_device, ue8m0=False)
+    assert_gemm_close(D, ref, "fp32 zero-scale blocks")
+    assert torch.all(D[5].float().abs() < 1e-30)       # every block of row 5 has scale 0
+
+
+@pytest.mark.parametrize("col_major_a", [False, True])
+def test_grouped_gemm_fp32_scales_vary_per_block(gpu_device, col_major_a):
+    from kb_nano_amd import _ops
+    dev = gpu_device
+    E, N, K = 5, 640, 2048
+    rng = np.random.default_rng(12)
+    ids, qa, sa, qb, sb, M_sum = _grouped_case(E, N, K, M_tok=150, topk=3, seed=12, dev=dev)
+    sa = (sa * _scale_factors(sa.shape, rng)).astype(np.float32)
+    sb = (sb * _scale_factors(sb.shape, rng)).astype(np.float32)
+    C = torch.full((M_sum, N), 7.0, dtype=torch.bfloat16, device=dev)
+    sA = torch.from_numpy(sa).to(dev)
+    if col_major_a:
+        sA = sA.t().contiguous().t()
+    _ops.m_grouped_gemm_nt_contiguous(to_fp8(qa, dev), sA, to_fp8(qb, dev), torch.from_numpy(sb).to(dev), C,
+                                      torch.from_numpy(ids).to(dev), disable_ue8m0_cast=True)
+    torch.cuda.synchronize()
+    ref = oracle.grouped_gemm_nt_sample(qa, sa, qb, sb, ids, ue8m0=False)
+    valid = ids >= 0
+    assert_gemm_close(C[torch.from_numpy(valid).to(dev)], ref[valid], "grouped fp32 scales")
+    assert torch.all(C[torch.from_numpy(~valid).to(dev)] == 7.0)
+
+
+def test_grouped_gemm_fp32_contract_equals_ue8m0_on_power_of_two_scales(gpu_device):
+    from kb_nano_amd import _ops
+    dev = gpu_device
+    E, N, K = 4, 512, 1024
+    ids, qa, sa, qb, sb, M_sum = _grouped_case(E, N, K, M_tok=130, topk=2, seed=4, dev=dev)
+    for s_ in (sa[ids >= 0], sb):   # the oracle's quant gives power-of-two (UE8M0) scales
+        assert np.all(np.frexp(s_)[0] == 0.5)
+    args = (to_fp8(qa, dev), torch.from_numpy(sa).to(dev), to_fp8(qb, dev), torch.from_numpy(sb).to(dev))
+    idt = torch.from_numpy(ids).to(dev)
+    C1 = torch.zeros(M_sum, N, dtype=torch.bfloat16, device=dev)
+    C0 = torch.zeros(M_sum, N, dtype=torch.bfloat16, device=dev)
+    _ops.m_grouped_gemm_nt_contiguous(*args, C1, idt, disable_ue8m0_cast=False)
+    _ops.m_grouped_gemm_nt_contiguous(*args, C0, idt, disable_ue8m0_cast=True)
+    torch.cuda.synchronize()
+    assert torch.equal(C0, C1)
