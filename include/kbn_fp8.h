@@ -141,6 +141,9 @@ int64_t kbn_moe_permute_workspace_bytes(int64_t num_pairs, int64_t num_experts);
  *   M_sum       must equal roundup(M*top_k + E*(alignment-1), alignment)
  *               (_compute_aligned_M, fused_experts.py:32-39)
  *   x_perm      [M_sum, row_bytes] contiguous; scale_perm fp32 [M_sum, scale_cols]
+ *               at scale_perm[r*sp_stride_m + c*sp_stride_c], row-major (the
+ *               reference's) or column-major (coalesced per-K-block loads in
+ *               the grouped GEMM)
  *   expert_ids  int32 [M_sum];  inv_perm int32 [M, top_k]
  *   Expert e owns rows [off[e], off[e] + roundup(count[e], alignment)), with
  *   off the exclusive prefix sum of the rounded counts.  Its first count[e]
@@ -158,6 +161,7 @@ int kbn_moe_permute_contiguous(const void* topk_ids, int ids_bytes, int64_t M, i
                                const void* x, int64_t ld_x_bytes, int64_t row_bytes,
                                const float* x_scale, int64_t s_stride_m, int64_t s_stride_c,
                                int64_t scale_cols, int64_t M_sum, void* x_perm, float* scale_perm,
+                               int64_t sp_stride_m, int64_t sp_stride_c,
                                int32_t* expert_ids, int32_t* inv_perm, int zero_padding,
                                void* workspace, int64_t workspace_bytes, void* stream);
 

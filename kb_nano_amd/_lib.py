@@ -31,8 +31,8 @@ SIGNATURES = {
         [_P, _I64, _P, _I64, _I64, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _P], _I),
     "kbn_moe_permute_workspace_bytes": ([_I64, _I64], _I64),
     "kbn_moe_permute_contiguous": (
-        [_P, _I, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I, _P, _I64,
-         _P], _I),
+        [_P, _I, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _P, _I,
+         _P, _I64, _P], _I),
     "kbn_moe_unpermute_reduce": ([_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I, _P, _I64, _P], _I),
     "kbn_debug_silu_bf16": ([_P, _P, _I64, _P], _I),
 }

@@ -204,8 +204,9 @@ def moe_permute_contiguous(x: torch.Tensor, x_scale: torch.Tensor, topk_ids: tor
                            alignment: int, M_sum: int, x_perm: torch.Tensor, scale_perm: torch.Tensor,
                            expert_ids: torch.Tensor, inv_perm: torch.Tensor, zero_padding: bool = True) -> None:
     """Scatter the rows of ``x [M, K]`` and ``x_scale [M, K/128]`` into the
-    expert-contiguous layout ``x_perm [M_sum, K]`` / ``scale_perm``, writing
-    ``expert_ids [M_sum]`` and ``inv_perm [M, top_k]`` (int32)."""
+    expert-contiguous layout ``x_perm [M_sum, K]`` / ``scale_perm`` (row- or
+    column-major), writing ``expert_ids [M_sum]`` and ``inv_perm [M, top_k]``
+    (int32)."""
     what = "moe_permute_contiguous"
     _dev_check(what, x, x_scale, topk_ids, x_perm, scale_perm, expert_ids, inv_perm)
     _dtype_check(what, x_scale, torch.float32, "x_scale")
@@ -228,8 +229,7 @@ def moe_permute_contiguous(x: torch.Tensor, x_scale: torch.Tensor, topk_ids: tor
         raise ValueError(f"{what}: outputs must be {(M_sum, K)} and {(M_sum, cols)}")
     if tuple(expert_ids.shape) != (M_sum,) or tuple(inv_perm.shape) != (M, top_k):
         raise ValueError(f"{what}: expert_ids must be {(M_sum,)} and inv_perm {(M, top_k)}")
-    for t, name in ((topk_ids, "topk_ids"), (x_perm, "x_perm"), (scale_perm, "scale_perm"),
-                    (expert_ids, "expert_ids"), (inv_perm, "inv_perm")):
+    for t, name in ((topk_ids, "topk_ids"), (x_perm, "x_perm"), (expert_ids, "expert_ids"), (inv_perm, "inv_perm")):
         if not t.is_contiguous():
             raise ValueError(f"{what}: {name} must be contiguous")
     esz = x.element_size()
@@ -244,7 +244,8 @@ def moe_permute_contiguous(x: torch.Tensor, x_scale: torch.Tensor, topk_ids: tor
         topk_ids.data_ptr(), topk_ids.element_size(), M, top_k, num_experts, alignment,
         x.data_ptr() if M else None, x.stride(0) * esz, K * esz, x_scale.data_ptr() if M else None,
         x_scale.stride(0), x_scale.stride(1), cols, M_sum, x_perm.data_ptr(), scale_perm.data_ptr(),
-        expert_ids.data_ptr(), inv_perm.data_ptr(), int(zero_padding), ws.data_ptr(), ws_bytes,
+        scale_perm.stride(0), scale_perm.stride(1), expert_ids.data_ptr(), inv_perm.data_ptr(), int(zero_padding),
+        ws.data_ptr(), ws_bytes,
         _stream(x_perm)), what)
 
 

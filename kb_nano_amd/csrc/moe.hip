@@ -52,7 +52,8 @@ struct PermuteArgs {
     int64_t xs_m, xs_c;
     int scale_cols;
     uint8_t* xp;            // [M_sum, row_bytes]
-    float* sp;              // [M_sum, scale_cols]
+    float* sp;              // scale (r, c) at sp[r * sp_m + c * sp_c]
+    int64_t sp_m, sp_c;
     int32_t* expert_ids;    // [M_sum]
     int32_t* inv_perm;      // [n]
     int M_sum;
@@ -196,7 +197,7 @@ __global__ __launch_bounds__(64 * kPlaceWaves) void moe_place_kernel(const Permu
         const int t = i / a.top_k;
         wave_row(a.x + (int64_t)t * a.ld_x, a.xp + (int64_t)dest * a.row_bytes, a.row_bytes, lane);
         for (int g = lane; g < a.scale_cols; g += 64)
-            a.sp[(int64_t)dest * a.scale_cols + g] = a.xs[(int64_t)t * a.xs_m + (int64_t)g * a.xs_c];
+            a.sp[(int64_t)dest * a.sp_m + (int64_t)g * a.sp_c] = a.xs[(int64_t)t * a.xs_m + (int64_t)g * a.xs_c];
         return;
     }
 
@@ -221,7 +222,7 @@ __global__ __launch_bounds__(64 * kPlaceWaves) void moe_place_kernel(const Permu
         if (lane == 0) a.expert_ids[r] = valid ? lo : -1;
         if (!valid && a.zero_padding) {
             wave_row(nullptr, a.xp + (int64_t)r * a.row_bytes, a.row_bytes, lane);
-            for (int g = lane; g < a.scale_cols; g += 64) a.sp[(int64_t)r * a.scale_cols + g] = 0.f;
+            for (int g = lane; g < a.scale_cols; g += 64) a.sp[(int64_t)r * a.sp_m + (int64_t)g * a.sp_c] = 0.f;
         }
     }
 }
@@ -347,7 +348,8 @@ extern "C" int kbn_moe_permute_contiguous(const void* topk_ids, int ids_bytes, i
                                           int64_t num_experts, int64_t alignment, const void* x, int64_t ld_x_bytes,
                                           int64_t row_bytes, const float* x_scale, int64_t s_stride_m,
                                           int64_t s_stride_c, int64_t scale_cols, int64_t M_sum, void* x_perm,
-                                          float* scale_perm, int32_t* expert_ids, int32_t* inv_perm,
+                                          float* scale_perm, int64_t sp_stride_m, int64_t sp_stride_c,
+                                          int32_t* expert_ids, int32_t* inv_perm,
                                           int zero_padding, void* workspace, int64_t workspace_bytes, void* stream) {
     const char* what = "moe_permute_contiguous";
     KBN_CHECK_ARG(ids_bytes == 4 || ids_bytes == 8, "%s: ids_bytes must be 4 or 8, got %d", what, ids_bytes);
@@ -374,7 +376,16 @@ extern "C" int kbn_moe_permute_contiguous(const void* topk_ids, int ids_bytes, i
         if (scale_cols > 0) KBN_CHECK_ARG(x_scale, "%s: null x_scale", what);
     }
     if (row_bytes > 0) KBN_CHECK_ARG(x_perm && aligned16(x_perm), "%s: x_perm must be 16-byte aligned", what);
-    if (scale_cols > 0) KBN_CHECK_ARG(scale_perm, "%s: null scale_perm", what);
+    if (scale_cols > 0) {
+        KBN_CHECK_ARG(scale_perm, "%s: null scale_perm", what);
+        // the rows x columns of scale_perm must not overlap: row-major, column-major or any
+        // other layout whose strides separate them
+        const bool rowmaj = sp_stride_c == 1 && sp_stride_m >= scale_cols;
+        const bool colmaj = sp_stride_m == 1 && sp_stride_c >= M_sum;
+        KBN_CHECK_ARG(rowmaj || colmaj, "%s: scale_perm strides (%lld, %lld) must be row-major (s_m >= %lld, 1) "
+                      "or column-major (1, s_c >= %lld)", what, (long long)sp_stride_m, (long long)sp_stride_c,
+                      (long long)scale_cols, (long long)M_sum);
+    }
     const PermutePlan plan = permute_plan(n, num_experts);
     KBN_CHECK_ARG(workspace && aligned16(workspace) && workspace_bytes >= plan.bytes,
                   "%s: workspace of %lld bytes (16-byte aligned) needed, got %lld", what, (long long)plan.bytes,
@@ -406,6 +417,8 @@ extern "C" int kbn_moe_permute_contiguous(const void* topk_ids, int ids_bytes, i
     a.scale_cols = (int)scale_cols;
     a.xp = static_cast<uint8_t*>(x_perm);
     a.sp = scale_perm;
+    a.sp_m = sp_stride_m;
+    a.sp_c = sp_stride_c;
     a.expert_ids = expert_ids;
     a.inv_perm = inv_perm;
     a.M_sum = (int)M_sum;

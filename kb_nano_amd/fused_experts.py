@@ -134,9 +134,12 @@ class FusedExperts(nn.Module):
         self.per_token_group_quant_fp8(hidden_states, a_fp8, a_scale)
 
         # padding rows stay unwritten: the grouped GEMM skips them and never
-        # writes their output rows, so nothing downstream reads them
+        # writes their output rows, so nothing downstream reads them.  The
+        # scales come out column-major, so GEMM1 reads each K block's row
+        # scales contiguously (GEMM2's come column-major from SiLU*Mul+quant).
         a1_perm, a1_scale_perm, expert_ids, inv_perm = _deepgemm_permute(a_fp8, a_scale, topk_ids, num_experts,
-                                                                        alignment, zero_padding=False)
+                                                                        alignment, zero_padding=False,
+                                                                        scale_colmajor=True)
 
         mm1_out = self._get_dg_workspace(1, (M_sum, N2), dev, hidden_states.dtype)
         m_grouped_fp8_gemm_nt_contiguous((a1_perm, a1_scale_perm), (w13, w13_scale), mm1_out, expert_ids)

@@ -29,19 +29,27 @@ def _compute_aligned_M(M: int, num_topk: int, local_num_experts: int, alignment:
 
 
 def _deepgemm_permute(hidden_states: torch.Tensor, a_scale: torch.Tensor, topk_ids: torch.Tensor,
-                      local_num_experts: int, alignment: int, zero_padding: bool = True):
+                      local_num_experts: int, alignment: int, zero_padding: bool = True,
+                      scale_colmajor: bool = False):
     """Scatter (token, slot) rows into the expert-contiguous layout
     (reference :42-116).  Returns (a_perm, a_scale_perm, expert_ids, inv_perm).
 
     ``zero_padding=False`` leaves the padding rows of ``a_perm`` and
     ``a_scale_perm`` unwritten: the grouped GEMM never writes a padding row of
-    its output, so the experts layer does not need them zeroed."""
+    its output, so the experts layer does not need them zeroed.
+    ``scale_colmajor=True`` returns ``a_scale_perm`` as a column-major view
+    (strides ``(1, M_sum)``, same values): the grouped GEMM then reads each K
+    block's row scales as one contiguous run instead of one cache line per
+    row."""
     M, K = hidden_states.shape
     k = topk_ids.size(1)
     dev = hidden_states.device
     M_sum = _compute_aligned_M(M, k, local_num_experts, alignment)
     a_perm = torch.empty(M_sum, K, dtype=hidden_states.dtype, device=dev)
-    a_scale_perm = torch.empty(M_sum, K // _GROUP, dtype=torch.float32, device=dev)
+    if scale_colmajor:
+        a_scale_perm = torch.empty(K // _GROUP, M_sum, dtype=torch.float32, device=dev).t()
+    else:
+        a_scale_perm = torch.empty(M_sum, K // _GROUP, dtype=torch.float32, device=dev)
     expert_ids = torch.empty(M_sum, dtype=torch.int32, device=dev)
     inv_perm = torch.empty(M, k, dtype=torch.int32, device=dev)
     _ops.moe_permute_contiguous(hidden_states, a_scale, topk_ids.contiguous(), local_num_experts, alignment, M_sum,

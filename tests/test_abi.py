@@ -208,16 +208,18 @@ def test_moe_permute_rejects_bad_arguments():
     L = lib()
     p = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
 
-    def call(ids_bytes=8, M=4, k=2, E=8, align=128, ld=256, row=256, M_sum=None, ws=1 << 20):
+    def call(ids_bytes=8, M=4, k=2, E=8, align=128, ld=256, row=256, M_sum=None, ws=1 << 20, sp=(2, 1)):
         M_sum = (M * k + E * (align - 1) + align - 1) // align * align if M_sum is None else M_sum
         return L.kbn_moe_permute_contiguous(p, ids_bytes, M, k, E, align, p, ld, row, p, 2, 1, 2, M_sum,
-                                            p, p, p, p, 1, p, ws, None)
+                                            p, p, sp[0], sp[1], p, p, 1, p, ws, None)
     assert call(ids_bytes=2) == 1 and "ids_bytes" in _err()
     assert call(E=2000) == 1 and "num_experts" in _err()
     assert call(M_sum=1152) == 1 and "M_sum" in _err()   # the right value is 1024
     assert call(row=100, ld=100) == 1 and "multiple of 16" in _err()
     assert call(ld=128) == 1 and "row stride" in _err()
     assert call(ws=16) == 1 and "workspace" in _err()
+    assert call(sp=(1, 100)) == 1 and "column-major" in _err()    # columns would overlap rows (M_sum 1024)
+    assert call(sp=(1, 1)) == 1 and "strides" in _err()
 
 
 def test_moe_unpermute_rejects_bad_arguments():

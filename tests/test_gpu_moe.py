@@ -132,6 +132,28 @@ def test_permute_matches_oracle(gpu_device, M, k, E, align, K, ids_dtype, colmaj
     assert not xp[pad].any() and not sp[pad].any()       # torch.zeros padding, as in the reference
 
 
+@pytest.mark.parametrize("zero_padding", [True, False])
+def test_permute_column_major_scales(gpu_device, zero_padding):
+    """scale_colmajor: the same values in a (1, M_sum)-strided view."""
+    from kb_nano_amd.moe_layout import _deepgemm_permute
+    dev = gpu_device
+    M, k, E, K = 300, 8, 64, 1024
+    topk = _routing(M, k, E, seed=31)
+    ids_o, dest_o, M_sum = oracle.permute_contiguous(topk, E, 128)
+    x = _rand_bytes((M, K), seed=5).to(dev).view(torch.float8_e4m3fn)
+    xs = torch.rand(M, K // 128, device=dev)
+    t = torch.from_numpy(topk).to(dev)
+    ref = _deepgemm_permute(x, xs, t, E, 128)
+    got = _deepgemm_permute(x, xs, t, E, 128, zero_padding=zero_padding, scale_colmajor=True)
+    torch.cuda.synchronize()
+    assert got[1].stride() == (1, M_sum)
+    d = torch.from_numpy(dest_o).to(dev)
+    assert torch.equal(got[1][d], ref[1][d]) and torch.equal(got[1][d], xs.repeat_interleave(k, 0))
+    assert torch.equal(got[2], ref[2]) and torch.equal(got[3], ref[3])
+    if zero_padding:
+        assert torch.equal(got[1], ref[1]) and torch.equal(got[0].view(torch.uint8), ref[0].view(torch.uint8))
+
+
 def test_permute_without_zero_padding_leaves_padding_rows(gpu_device):
     from kb_nano_amd import _ops
     dev = gpu_device
