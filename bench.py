@@ -108,6 +108,35 @@ def bench_quant(steps, warmup, dev, M=4096, K=18432):
     return {"M": M, "K": K, "us": ms * 1e3, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS, "rotated_copies": n}
 
 
+def bench_norm(steps, warmup, dev, H=7168):
+    """Fused RMSNorm (+ residual add) + 1x128 quant at DeepSeek-V3's hidden
+    size: algorithmic bytes = the bf16 row(s) read and written, the fp8 codes
+    and the scales (the weight vector stays in L2)."""
+    import torch
+    from kb_nano_amd import _ops
+    out = []
+    gen = torch.Generator(device=dev).manual_seed(11)
+    w = torch.randn(H, generator=gen, device=dev).bfloat16()
+    G = -(-H // 128)
+    for M in (4096, 128):
+        for add in (False, True):
+            per_row = H * (2 + 1) + 4 * G + (3 * 2 * H if add else 0)   # fused: reads r, writes r and x
+            nbytes = M * per_row
+            n = _copies_for(nbytes, 2)
+            xs = [torch.randn(M, H, generator=gen, device=dev).bfloat16() for _ in range(n)]
+            rs = [torch.randn(M, H, generator=gen, device=dev).bfloat16() for _ in range(n)] if add else None
+            qs = [torch.empty(M, H, dtype=torch.float8_e4m3fn, device=dev) for _ in range(n)]
+            ss = [torch.empty(G, M, device=dev).t() for _ in range(n)]
+            fn = (lambda i: _ops.rmsnorm_fp8_quant(qs[i % n], ss[i % n], xs[i % n], w, 1e-6, residual=rs[i % n])) \
+                if add else (lambda i: _ops.rmsnorm_fp8_quant(qs[i % n], ss[i % n], xs[i % n], w, 1e-6))
+            ms = _events_time_ms(fn, steps, warmup)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            out.append({"M": M, "H": H, "residual_add": add, "us": ms * 1e3, "GB/s": gbs,
+                        "frac_hbm": gbs / HBM_PEAK_GBS, "rotated_copies": n})
+            del xs, rs, qs, ss
+    return out
+
+
 def _gemm_case(name, M, N, K, steps, warmup, dev, seed):
     import torch
     from kb_nano_amd import _ops
@@ -303,7 +332,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default="all",
-                    help="comma list of extra sections: quant,dsv3,moe,decode (default all; 'none' = headline only)")
+                    help="comma list of extra sections: quant,norm,dsv3,moe,decode (default all; 'none' = headline only)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three 1 GiB device copies (reference for rocprofv3 byte counters)")
@@ -325,7 +354,7 @@ def main():
     from kb_nano_amd._lib import require_gfx950
     require_gfx950(0)
 
-    sections = {"quant", "dsv3", "moe", "decode"} if args.only == "all" else \
+    sections = {"quant", "norm", "dsv3", "moe", "decode"} if args.only == "all" else \
         set() if args.only == "none" else set(args.only.split(","))
 
     torch.cuda.synchronize()
@@ -337,6 +366,11 @@ def main():
     if "quant" in sections:
         extra["quant_cfg_4096x18432"] = bench_quant(**small)
         print(f"[bench] quant: {extra['quant_cfg_4096x18432']}", file=sys.stderr, flush=True)
+    if "norm" in sections:
+        extra["rmsnorm_quant_dsv3"] = bench_norm(**small)
+        for r in extra["rmsnorm_quant_dsv3"]:
+            print(f"[bench] rmsnorm_quant M={r['M']} add={r['residual_add']}: {r['us']:.1f} us {r['GB/s']:.0f} GB/s",
+                  file=sys.stderr, flush=True)
     if "dsv3" in sections:
         extra["gemm_dsv3_cfg3"] = bench_dsv3(**small)
         for r in extra["gemm_dsv3_cfg3"]:

@@ -183,6 +183,28 @@ int kbn_moe_unpermute_reduce(const void* y_bf16, int64_t M_sum, int64_t H, int64
                              void* out_bf16, int64_t ld_out, void* stream);
 
 /*
+ * Fused RMSNorm (+ residual add) + per-token-group (1x128) FP8 quantization.
+ * Replaces ops kb_nano_norm::rmsnorm_fp8_quant and
+ * kb_nano_norm::fused_add_rmsnorm_fp8_quant (tasks/baseline/L1/rmsnorm_quant.py:27-55;
+ * kernels tasks/baseline/L1/csrc/rmsnorm_quant.cu:21-93, :124-201).
+ *   x         bf16 [M, H], row stride ld_x; w bf16 [H]; 16-byte aligned, H % 8 == 0
+ *   residual  NULL: plain RMSNorm of x (H <= 16384).  Otherwise bf16 [M, H],
+ *             row stride ld_r (H <= 8192): residual <- bf16(residual + x), the
+ *             norm is taken of the fp32 sums, and x <- bf16(normalized row).
+ *   q         fp8 [M, H], row stride ld_q (multiple of 8)
+ *   scale     fp32 (m, g) at scale[m*s_stride_m + g*s_stride_g], g < ceil(H/128)
+ *             (the reference's column-major buffer: (1, M))
+ *   inv = 1/sqrt(mean(a^2) + eps) over the row; v = (a_bf16 * inv) * w in fp32;
+ *   each 1x128 group (the last one partial when H % 128 != 0) gets the UE8M0
+ *   scale ceil_pow2(max(max|v|, 1e-10) / 448) and codes e4m3_rne(v / scale).
+ *   The sum of squares is fp32 in a fixed order, inv uses the correctly
+ *   rounded sqrt and divide (the reference: its thread layout's order, rsqrtf).
+ */
+int kbn_rmsnorm_fp8_quant(void* x_bf16, int64_t M, int64_t H, int64_t ld_x, const void* w_bf16,
+                          void* residual_bf16, int64_t ld_r, void* q_fp8, int64_t ld_q, float* scale,
+                          int64_t s_stride_m, int64_t s_stride_g, float eps, void* stream);
+
+/*
  * Test hook (no counterpart in the reference): the kernels' bf16 SiLU
  * applied elementwise to n bf16 bit patterns, for exhaustive checking.
  */

@@ -8,7 +8,9 @@ Four operators, each a drop-in for its kb_nano L1 counterpart:
   * ``Fp8GroupedGemmContiguous``  its contiguous-layout MoE grouped variant
 
 and ``FusedExperts``, the MoE experts layer that chains them (quant, permute,
-grouped GEMM, SiLU*Mul+quant, grouped GEMM, weighted unpermute).
+grouped GEMM, SiLU*Mul+quant, grouped GEMM, weighted unpermute), plus the
+fused ``RMSNormFP8Quant`` / ``FusedAddRMSNormFP8Quant`` that produce the
+quantized activations of a decoder layer's first linear.
 
 The compute runs in hand-written gfx950 HIP kernels (``csrc/``) behind the
 C-ABI of ``libkbn_fp8.so`` (declared in ``include/kbn_fp8.h``); this package
@@ -25,6 +27,7 @@ from .fp8_linear import (
     postprocess_fp8_weights_batched,
 )
 from .moe_grouped_gemm import m_grouped_fp8_gemm_nt_contiguous
+from .rmsnorm_quant import FusedAddRMSNormFP8Quant, RMSNormFP8Quant
 from .silu_mul_quant_fp8 import SiluMulQuantFp8
 
 __all__ = [
@@ -33,6 +36,8 @@ __all__ = [
     "SiluMulQuantFp8",
     "Fp8GroupedGemmContiguous",
     "FusedExperts",
+    "RMSNormFP8Quant",
+    "FusedAddRMSNormFP8Quant",
     "m_grouped_fp8_gemm_nt_contiguous",
     "postprocess_fp8_weights",
     "postprocess_fp8_weights_batched",

@@ -276,6 +276,39 @@ def moe_unpermute_reduce(y: torch.Tensor, inv_perm: torch.Tensor, topk_weights: 
         _stream(out)), what)
 
 
+def rmsnorm_fp8_quant(output_fp8: torch.Tensor, output_scales: torch.Tensor, input: torch.Tensor,
+                      weight: torch.Tensor, eps: float, residual: torch.Tensor | None = None) -> None:
+    """RMSNorm of ``input [..., H]`` (of ``residual + input`` when ``residual``
+    is given, updating both in place as the reference does) quantized 1x128
+    into ``output_fp8 [T, H]`` and ``output_scales [T, ceil(H/128)]`` (any
+    strides; the reference allocates them column-major)."""
+    what = "fused_add_rmsnorm_fp8_quant" if residual is not None else "rmsnorm_fp8_quant"
+    tensors = (output_fp8, output_scales, input, weight) + ((residual,) if residual is not None else ())
+    _dev_check(what, *tensors)
+    _dtype_check(what, output_fp8, FP8, "output_fp8")
+    _dtype_check(what, output_scales, torch.float32, "output_scales")
+    for t, name in ((input, "input"), (weight, "weight")) + (((residual, "residual"),) if residual is not None else ()):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{what}: {name} must be bfloat16 on this path, got {t.dtype}")
+    H = input.size(-1)
+    T = input.numel() // H if H else 0
+    G = -(-H // GROUP)
+    if not input.is_contiguous() or (residual is not None and not residual.is_contiguous()):
+        raise ValueError(f"{what}: input and residual must be contiguous")
+    if residual is not None and residual.shape != input.shape:
+        raise ValueError(f"{what}: residual must match input {tuple(input.shape)}, got {tuple(residual.shape)}")
+    if tuple(weight.shape) != (H,) or not weight.is_contiguous():
+        raise ValueError(f"{what}: weight must be a contiguous [{H}] vector, got {tuple(weight.shape)}")
+    if tuple(output_fp8.shape) != (T, H) or output_fp8.stride(1) != 1:
+        raise ValueError(f"{what}: output_fp8 must be [{T}, {H}] with contiguous rows")
+    if tuple(output_scales.shape) != (T, G):
+        raise ValueError(f"{what}: output_scales must be [{T}, {G}], got {tuple(output_scales.shape)}")
+    check(lib().kbn_rmsnorm_fp8_quant(
+        input.data_ptr(), T, H, H, weight.data_ptr(), residual.data_ptr() if residual is not None else None, H,
+        output_fp8.data_ptr(), output_fp8.stride(0), output_scales.data_ptr(), output_scales.stride(0),
+        output_scales.stride(1), float(eps), _stream(input)), what)
+
+
 def debug_silu_bf16(g_bits: torch.Tensor, out_bits: torch.Tensor) -> None:
     """Test hook: the kernels' silu (bf16 in, bf16 out) on int16 bit patterns."""
     _dev_check("debug_silu_bf16", g_bits, out_bits)
@@ -291,6 +324,7 @@ def debug_silu_bf16(g_bits: torch.Tensor, out_bits: torch.Tensor) -> None:
 
 _fp8_lib = torch.library.Library("kb_nano_fp8", "FRAGMENT")
 _moe_lib = torch.library.Library("kb_nano_fp8_moe", "FRAGMENT")
+_norm_lib = torch.library.Library("kb_nano_norm", "FRAGMENT")
 
 
 def _has_op(ns: str, name: str) -> bool:
@@ -332,6 +366,18 @@ def _register():
                         "bool disable_ue8m0_cast) -> ()")
         _moe_lib.impl("m_grouped_gemm_nt_contiguous", m_grouped_gemm_nt_contiguous, "CUDA")
         _moe_lib.impl("m_grouped_gemm_nt_contiguous", _meta_noop, "Meta")
+    # schemas of tasks/baseline/L1/rmsnorm_quant.py:27-55
+    if not _has_op("kb_nano_norm", "rmsnorm_fp8_quant"):
+        _norm_lib.define("rmsnorm_fp8_quant(Tensor! output_fp8, Tensor! output_scales, "
+                         "Tensor input, Tensor weight, float eps) -> ()")
+        _norm_lib.impl("rmsnorm_fp8_quant", lambda q, s, x, w, eps: rmsnorm_fp8_quant(q, s, x, w, eps), "CUDA")
+        _norm_lib.impl("rmsnorm_fp8_quant", _meta_noop, "Meta")
+    if not _has_op("kb_nano_norm", "fused_add_rmsnorm_fp8_quant"):
+        _norm_lib.define("fused_add_rmsnorm_fp8_quant(Tensor! output_fp8, Tensor! output_scales, "
+                         "Tensor(a!) input, Tensor(b!) residual, Tensor weight, float eps) -> ()")
+        _norm_lib.impl("fused_add_rmsnorm_fp8_quant",
+                       lambda q, s, x, r, w, eps: rmsnorm_fp8_quant(q, s, x, w, eps, residual=r), "CUDA")
+        _norm_lib.impl("fused_add_rmsnorm_fp8_quant", _meta_noop, "Meta")
 
 
 _register()

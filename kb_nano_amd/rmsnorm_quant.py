@@ -1,0 +1,57 @@
+"""Fused RMSNorm (+ residual add) + per-token-group FP8 quantization.
+
+Drop-in for ``tasks/baseline/L1/rmsnorm_quant.py`` (kb_nano): the same two
+modules with the same ``forward`` signatures and column-major scale output,
+and the ops ``kb_nano_norm::rmsnorm_fp8_quant`` /
+``kb_nano_norm::fused_add_rmsnorm_fp8_quant`` with the reference schemas
+(registered by ``_ops``).  One gfx950 launch (``csrc/norm.hip``) per call,
+one wavefront per token.
+
+Numerics (reference ``csrc/rmsnorm_quant.cu:21-201``): the normalized value
+``(x * inv_rms) * w`` stays fp32 until the UE8M0 1x128 quantization; the
+fused variant adds the residual first (fp32), stores it back as bf16, and
+overwrites ``input`` with the bf16 normalized row.  bf16 activations only
+(the reference also dispatches fp16/fp32); hidden sizes up to 16384 (8192
+with the residual add), any multiple of 8.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import _ops  # noqa: F401  (registers torch.ops.kb_nano_norm.*)
+from ._ops import FP8, GROUP
+
+_FP8_GROUP_SIZE = GROUP
+
+
+def _outputs(input: torch.Tensor):
+    hidden_size = input.size(-1)
+    num_tokens = input.numel() // hidden_size
+    num_groups = (hidden_size + _FP8_GROUP_SIZE - 1) // _FP8_GROUP_SIZE
+    output_fp8 = torch.empty(num_tokens, hidden_size, dtype=FP8, device=input.device)
+    output_scales = torch.empty(num_groups, num_tokens, dtype=torch.float32, device=input.device).transpose(0, 1)
+    return output_fp8, output_scales
+
+
+class RMSNormFP8Quant(nn.Module):
+    """``forward(input, weight, eps=1e-6) -> (output_fp8, output_scales)``:
+    output_fp8 [num_tokens, hidden] float8_e4m3fn, output_scales [num_tokens,
+    num_groups] float32 column-major (reference :65-98)."""
+
+    def forward(self, input: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> tuple[torch.Tensor, torch.Tensor]:
+        output_fp8, output_scales = _outputs(input)
+        torch.ops.kb_nano_norm.rmsnorm_fp8_quant(output_fp8, output_scales, input, weight, eps)
+        return output_fp8, output_scales
+
+
+class FusedAddRMSNormFP8Quant(nn.Module):
+    """``forward(input, residual, weight, eps=1e-6) -> (output_fp8,
+    output_scales, residual)``; modifies ``input`` (normalized bf16 row) and
+    ``residual`` (residual + input) in place (reference :101-134)."""
+
+    def forward(self, input: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                eps: float = 1e-6) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        output_fp8, output_scales = _outputs(input)
+        torch.ops.kb_nano_norm.fused_add_rmsnorm_fp8_quant(output_fp8, output_scales, input, residual, weight, eps)
+        return output_fp8, output_scales, residual

@@ -92,6 +92,9 @@ def lib():
             L.orc_grouped_gemm_nt_sample.argtypes = [_P, _P, _I64, _I64, _P, _P, _P,
                                                      _I64, _I64, _I64, _I64,
                                                      _P, _I64, _P, _I64, _P, ctypes.c_int]
+            L.orc_rmsnorm_quant.restype = ctypes.c_int
+            L.orc_rmsnorm_quant.argtypes = [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _I64,
+                                            ctypes.c_float]
             _LIB = L
     return _LIB
 
@@ -354,3 +357,30 @@ def unpermute_and_reduce(mm2_out_f32: np.ndarray, inv_perm: np.ndarray, topk_wei
             p = bf16_bits_to_f32(f32_to_bf16_bits(p))
         out = np.where(ok[:, None], (out + p).astype(np.float32), out)
     return out
+
+
+# ---------------------------------------------------------------------------
+# Fused RMSNorm + 1x128 quant (tasks/baseline/L1/csrc/rmsnorm_quant.cu:21-201)
+# ---------------------------------------------------------------------------
+
+def rmsnorm_quant(x_bits: np.ndarray, w_bits: np.ndarray, eps: float = 1e-6, residual_bits=None):
+    """RMSNorm of bf16 ``x [M, H]`` (of ``residual + x`` when ``residual_bits``
+    is given) with bf16 weight ``w [H]``, quantized 1x128 to e4m3 with UE8M0
+    scales.  Returns ``(codes uint8 [M, H], scales fp32 [M, ceil(H/128)])``,
+    plus, for the residual variant, ``(residual_out, x_out)`` bf16 bits: the
+    bf16 sum and the bf16 normalized row (the reference overwrites its inputs
+    with them).  Sum of squares in the fixed fp32 order of ``orc_rmsnorm_quant``."""
+    x = np.array(x_bits, dtype=np.uint16, copy=True, order="C")
+    w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    M, H = x.shape
+    if w.shape != (H,):
+        raise ValueError("weight must be [H]")
+    G = -(-H // 128)
+    q = np.empty((M, H), dtype=np.uint8)
+    s = np.empty((M, G), dtype=np.float32)
+    r = None if residual_bits is None else np.array(residual_bits, dtype=np.uint16, copy=True, order="C")
+    rc = lib().orc_rmsnorm_quant(_ptr(x), M, H, H, _ptr(w), None if r is None else _ptr(r), H, _ptr(q), H,
+                                 _ptr(s), G, 1, float(eps))
+    if rc:
+        raise ValueError(f"orc_rmsnorm_quant failed ({rc})")
+    return (q, s) if r is None else (q, s, r, x)

@@ -31,11 +31,15 @@
  *                          the contiguous grouped contract of
  *                          tasks/baseline/L1/fp8_grouped_gemm_contiguous.py:136-170:
  *                          row r uses expert expert_ids[r]; rows with -1 are skipped.
+ *   orc_rmsnorm_quant      tasks/baseline/L1/csrc/rmsnorm_quant.cu:21-93 and :124-201
+ *                          (RMSNorm, optional residual add, UE8M0 1x128 quant of the
+ *                          fp32 normalized values), in a fixed fp32 reduction order.
  *
  * Everything is plain scalar C99 on the host; no GPU code.
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
@@ -291,4 +295,84 @@ int orc_grouped_gemm_nt_sample(const uint8_t* A, const float* sA, int64_t sA_sm,
         if (rc) return rc;
     }
     return 0;
+}
+
+/* Fused RMSNorm + 1x128 FP8 quantization, plain and with residual add
+ * (tasks/baseline/L1/csrc/rmsnorm_quant.cu:21-93 and :124-201, module
+ * tasks/baseline/L1/rmsnorm_quant.py:27-55):
+ *   plain:  a = x;  base = x
+ *   fused:  a = fp32(r) + fp32(x) (unrounded);  r <- bf16(a);  base = fp32(bf16(a))
+ *   inv  = 1 / sqrt(sum(a^2) / H + eps)
+ *   v    = (base * inv) * w            (two fp32 products, not rounded to bf16)
+ *   per 128-group: amax = max(max|v|, 1e-10); s = ceil_pow2(amax / 448);
+ *   q = e4m3_rne(fminf(fmaxf(v / s, -448), 448)); fused: x <- bf16(v)
+ * The reference sums in whatever order its thread layout gives and takes
+ * rsqrtf; this restatement fixes the order the gfx950 kernel uses, so the
+ * kernel can be checked bit for bit: 64 lanes, lane l owns the 8-element
+ * chunks starting at c*512 + 8l (c = 0, 1, ...), accumulates a*a with fmaf in
+ * chunk then element order, and the 64 partials are combined by the xor
+ * butterfly p[l] + p[l ^ d] for d = 32, 16, ..., 1.  inv uses the correctly
+ * rounded sqrt and divide.  r == NULL selects the plain variant.
+ * H % 8 == 0; scale (m, g) at s[m*s_m + g*s_g] for g < ceil(H/128). */
+int orc_rmsnorm_quant(uint16_t* x, int64_t M, int64_t H, int64_t ld_x, const uint16_t* w, uint16_t* r,
+                      int64_t ld_r, uint8_t* q, int64_t ld_q, float* s, int64_t s_m, int64_t s_g, float eps) {
+    if (H <= 0 || H % 8) return 1;
+    const int64_t G = (H + 127) / 128, C = (H + 511) / 512;
+    int bad = 0;
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m) {
+        float* base = (float*)malloc((size_t)H * sizeof(float));
+        if (!base) { bad = 1; continue; }
+        uint16_t* xr = x + m * ld_x;
+        uint16_t* rr = r ? r + m * ld_r : NULL;
+        float part[64];
+        for (int l = 0; l < 64; ++l) {
+            float p = 0.0f;
+            for (int64_t c = 0; c < C; ++c) {
+                const int64_t e0 = c * 512 + 8 * l;
+                if (e0 >= H) continue;
+                for (int j = 0; j < 8; ++j) {
+                    const int64_t e = e0 + j;
+                    const float xv = orc_bf16_to_float(xr[e]);
+                    float a = xv;
+                    if (rr) {
+                        a = orc_bf16_to_float(rr[e]) + xv;
+                        rr[e] = orc_float_to_bf16(a);
+                        base[e] = orc_bf16_to_float(rr[e]);
+                    } else {
+                        base[e] = xv;
+                    }
+                    p = fmaf(a, a, p);
+                }
+            }
+            part[l] = p;
+        }
+        for (int d = 32; d >= 1; d >>= 1) {
+            float t[64];
+            for (int l = 0; l < 64; ++l) t[l] = part[l] + part[l ^ d];
+            memcpy(part, t, sizeof(t));
+        }
+        const float mean = part[0] / (float)H;
+        const float inv = 1.0f / sqrtf(mean + eps);
+        for (int64_t g = 0; g < G; ++g) {
+            const int64_t e1 = (g + 1) * 128 < H ? (g + 1) * 128 : H;
+            float amax = 0.0f;
+            for (int64_t e = g * 128; e < e1; ++e) {
+                const float v = (base[e] * inv) * orc_bf16_to_float(w[e]);
+                const float av = fabsf(v);
+                if (av > amax) amax = av;
+            }
+            const float sc = group_scale(amax, 1e-10f, 1);
+            for (int64_t e = g * 128; e < e1; ++e) {
+                const float v = (base[e] * inv) * orc_bf16_to_float(w[e]);
+                /* the reference clamps with fminf(fmaxf(.)) (rmsnorm_quant.cu:82):
+                 * a NaN quotient becomes -448 */
+                q[m * ld_q + e] = orc_e4m3_encode(fminf(fmaxf(v / sc, -448.0f), 448.0f));
+                if (rr) xr[e] = orc_float_to_bf16(v);
+            }
+            s[m * s_m + g * s_g] = sc;
+        }
+        free(base);
+    }
+    return bad ? 2 : 0;
 }

@@ -242,3 +242,34 @@ def test_fused_experts_surface():
     names = list(inspect.signature(FusedExperts.forward).parameters)
     assert names == ["self", "hidden_states", "w13", "w2", "topk_weights", "topk_ids", "num_experts", "w13_scale",
                      "w2_scale", "w13_scale_dg", "w2_scale_dg", "use_fp8_w8a8", "block_shape"]
+
+
+def test_rmsnorm_quant_rejects_bad_hidden_sizes():
+    from kb_nano_amd._lib import lib
+    L = lib()
+    p = ctypes.c_void_p(4096)   # never dereferenced: validation fails first
+    assert L.kbn_rmsnorm_fp8_quant(p, 4, 100, 100, p, None, 0, p, 104, p, 1, 4, 1e-6, None) == 1
+    assert "multiple of 8" in _err()
+    assert L.kbn_rmsnorm_fp8_quant(p, 4, 16392, 16392, p, None, 0, p, 16392, p, 1, 4, 1e-6, None) == 1
+    assert "at most 16384" in _err()
+    assert L.kbn_rmsnorm_fp8_quant(p, 4, 8200, 8200, p, p, 8200, p, 8200, p, 1, 4, 1e-6, None) == 1
+    assert "at most 8192" in _err()
+    assert L.kbn_rmsnorm_fp8_quant(None, 0, 1024, 1024, None, None, 0, None, 1024, None, 1, 0, 1e-6, None) == 0
+
+
+def test_rmsnorm_quant_surface_matches_reference():
+    """Module names, forward arguments and op schemas of
+    tasks/baseline/L1/rmsnorm_quant.py:27-134."""
+    import inspect
+    from kb_nano_amd import FusedAddRMSNormFP8Quant, RMSNormFP8Quant
+    assert list(inspect.signature(RMSNormFP8Quant.forward).parameters) == ["self", "input", "weight", "eps"]
+    assert list(inspect.signature(FusedAddRMSNormFP8Quant.forward).parameters) == [
+        "self", "input", "residual", "weight", "eps"]
+    def args(op):
+        sch = op.default._schema
+        return [(a.name, bool(a.alias_info and a.alias_info.is_write)) for a in sch.arguments]
+    assert args(torch.ops.kb_nano_norm.rmsnorm_fp8_quant) == [
+        ("output_fp8", True), ("output_scales", True), ("input", False), ("weight", False), ("eps", False)]
+    assert args(torch.ops.kb_nano_norm.fused_add_rmsnorm_fp8_quant) == [
+        ("output_fp8", True), ("output_scales", True), ("input", True), ("residual", True), ("weight", False),
+        ("eps", False)]

@@ -461,3 +461,98 @@ def test_golden_gemm_cfg1_fixture():
     ref = oracle.gemm_nt_sample(qa, sa, qw, sw, ue8m0=True)
     assert sha(oracle.f32_to_bf16_bits(ref.astype(np.float32))) == str(d["out_bf16_sha256"])
     assert np.array_equal(ref[:16, :64], d["out_slice"])
+
+
+# ------------------------------------------------------ RMSNorm + 1x128 quant
+# oracle.rmsnorm_quant restates tasks/baseline/L1/csrc/rmsnorm_quant.cu:21-201
+# in the kernel's fixed fp32 order; these pin it independently of that order.
+
+def _bf16(a):
+    return oracle.f32_to_bf16_bits(np.asarray(a, dtype=np.float32))
+
+
+def test_rmsnorm_quant_unit_rows_reduce_to_plain_quant():
+    """x = +-1 and eps = 0: sum(x^2) = H exactly, inv = 1, so v = x * w is a
+    bf16 value and the codes and scales are the plain 1x128 quant of it."""
+    rng = np.random.default_rng(3)
+    M, H = 6, 1024
+    x = np.where(rng.random((M, H)) < 0.5, -1.0, 1.0).astype(np.float32)
+    w = rng.standard_normal(H).astype(np.float32) * np.exp2(rng.integers(-6, 6, H))
+    wb = _bf16(w)
+    q, s = oracle.rmsnorm_quant(_bf16(x), wb, eps=0.0)
+    xw = _bf16(x * oracle.bf16_bits_to_f32(wb)[None, :])
+    q2, s2 = oracle.quant_group128(xw, use_ue8m0=True)
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
+
+
+def test_rmsnorm_quant_scale_invariance():
+    """Scaling a row by 2^k scales every square by 4^k exactly, so with eps=0
+    the normalized values, codes and scales do not change."""
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((5, 2048)).astype(np.float32)
+    w = _bf16(rng.standard_normal(2048))
+    q0, s0 = oracle.rmsnorm_quant(_bf16(x), w, eps=0.0)
+    for k in (-20, 7):
+        qk, sk = oracle.rmsnorm_quant(_bf16(x * np.float32(2.0 ** k)), w, eps=0.0)
+        assert np.array_equal(q0, qk) and np.array_equal(s0, sk)
+
+
+def test_rmsnorm_quant_matches_float64():
+    """Against the same math in float64: codes and scales agree except where
+    v / s lies within fp32 rounding of an e4m3 tie (adjacent codes only)."""
+    rng = np.random.default_rng(5)
+    M, H, eps = 64, 7168, 1e-6
+    xb = _bf16(rng.standard_normal((M, H)))
+    wb = _bf16(rng.standard_normal(H))
+    q, s = oracle.rmsnorm_quant(xb, wb, eps=eps)
+    x = oracle.bf16_bits_to_f32(xb).astype(np.float64)
+    w = oracle.bf16_bits_to_f32(wb).astype(np.float64)
+    v = x / np.sqrt((x * x).mean(axis=1, keepdims=True) + eps) * w[None, :]
+    amax = np.maximum(np.abs(v).reshape(M, H // 128, 128).max(axis=2), 1e-10)
+    s64 = np.exp2(np.ceil(np.log2(amax / 448.0)))
+    assert np.mean(s == s64) > 0.999
+    codes64 = oracle.e4m3_encode(np.clip(v / np.repeat(s, 128, axis=1), -448, 448).astype(np.float32))
+    dq = oracle.e4m3_decode(q).astype(np.float64)
+    d64 = oracle.e4m3_decode(codes64).astype(np.float64)
+    same = q == codes64
+    assert same.mean() > 0.999
+    # where they differ, they are neighbours on the e4m3 grid
+    step = np.abs(d64) * 2.0 ** -3 + 2.0 ** -9
+    assert np.all(np.abs(dq - d64)[~same] <= step[~same] + 1e-12)
+
+
+def test_rmsnorm_quant_meets_reference_two_kernel_bar():
+    """The reference's own acceptance test (tests/debug/test_fused_norm_quant.py:
+    43-76): against RMSNorm to bf16 followed by the 1x128 quant, fewer than 7%
+    of codes differ and the scales agree within 0.016."""
+    rng = np.random.default_rng(6)
+    for H in (3584, 4096, 8192):
+        wb = _bf16(rng.standard_normal(H))
+        for bs in (1, 8, 32, 128):
+            xb = _bf16(rng.standard_normal((bs, H)))
+            q, s = oracle.rmsnorm_quant(xb, wb, eps=1e-6)
+            x = oracle.bf16_bits_to_f32(xb)
+            inv = (1.0 / np.sqrt((x.astype(np.float64) ** 2).mean(axis=1, keepdims=True) + 1e-6)).astype(np.float32)
+            norm = _bf16(oracle.bf16_bits_to_f32(_bf16(x * inv)) * oracle.bf16_bits_to_f32(wb)[None, :])
+            q2, s2 = oracle.quant_group128(norm, use_ue8m0=True)
+            assert np.mean(q != q2) < 0.07
+            assert np.max(np.abs(s - s2)) <= 0.016
+
+
+def test_rmsnorm_quant_residual_variant():
+    """Fused add: residual <- bf16(residual + x) exactly; the normalized bf16
+    row written back into x re-quantizes to the same codes where it is not a
+    tie; and the codes are those of the plain variant on the new residual
+    except where the unrounded sum of squares moves a value across a tie."""
+    rng = np.random.default_rng(7)
+    M, H = 16, 4096
+    xb = _bf16(rng.standard_normal((M, H)))
+    rb = _bf16(rng.standard_normal((M, H)) * 4)
+    wb = _bf16(rng.standard_normal(H))
+    q, s, r_out, x_out = oracle.rmsnorm_quant(xb, wb, eps=1e-6, residual_bits=rb)
+    assert np.array_equal(r_out, _bf16(oracle.bf16_bits_to_f32(rb) + oracle.bf16_bits_to_f32(xb)))
+    q_plain, s_plain = oracle.rmsnorm_quant(r_out, wb, eps=1e-6)
+    assert np.mean(q == q_plain) > 0.99 and np.mean(s == s_plain) > 0.99
+    xo = oracle.bf16_bits_to_f32(x_out)
+    dq = oracle.e4m3_decode(q) * np.repeat(s, 128, axis=1)
+    assert np.all(np.abs(xo - dq) <= np.abs(xo) * 2.0 ** -3 + np.repeat(s, 128, axis=1) * 2.0 ** -9 + 1e-30)
