@@ -105,17 +105,12 @@ __device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
     return v;
 }
 
-// Pack four already-clamped floats into four e4m3fn codes (RNE, hardware).
+// Pack four floats into four e4m3fn codes with the hardware conversion:
+// round to nearest even, |x| in (448, 464] -> 448, larger or NaN -> NaN code.
 __device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {
     int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
     w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
     return (uint32_t)w;
-}
-
-// clamp(v, -448, 448) that keeps NaN (comparisons with NaN are false).
-__device__ __forceinline__ float clamp_fp8(float v) {
-    v = v > kFp8Max ? kFp8Max : v;
-    return v < -kFp8Max ? -kFp8Max : v;
 }
 
 }  // namespace kbn

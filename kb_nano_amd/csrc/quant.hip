@@ -105,15 +105,22 @@ __device__ __forceinline__ float quant8_store(const float (&v)[8], float eps, in
     amax = __uint_as_float(row16_max_u32(__float_as_uint(amax)));
     amax = fmaxf(amax, eps);
     float sc = amax / kFp8Max;
+    // The reference clamps v / sc to [-448, 448] before the cast.  Here that
+    // clamp can never act on a finite value: sc >= fl(amax / 448), so
+    // |v / sc| <= 448 (1 + 2^-23)^2 < 464, and the hardware conversion rounds
+    // to nearest even, which maps (448, 464] to 448 (it only goes to NaN above
+    // 464).  NaN stays NaN, as under the reference's torch.clamp.  Dropping the
+    // two compares and two selects per element is worth 4% (SiLU) to 14%
+    // (quant) of kernel time.
     uint32_t lo, hi;
     if (kUe8m0) {
         sc = ue8m0_ceil(sc);
         const float inv = pow2_recip(sc);
-        lo = pack4_e4m3(clamp_fp8(v[0] * inv), clamp_fp8(v[1] * inv), clamp_fp8(v[2] * inv), clamp_fp8(v[3] * inv));
-        hi = pack4_e4m3(clamp_fp8(v[4] * inv), clamp_fp8(v[5] * inv), clamp_fp8(v[6] * inv), clamp_fp8(v[7] * inv));
+        lo = pack4_e4m3(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+        hi = pack4_e4m3(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
     } else {
-        lo = pack4_e4m3(clamp_fp8(v[0] / sc), clamp_fp8(v[1] / sc), clamp_fp8(v[2] / sc), clamp_fp8(v[3] / sc));
-        hi = pack4_e4m3(clamp_fp8(v[4] / sc), clamp_fp8(v[5] / sc), clamp_fp8(v[6] / sc), clamp_fp8(v[7] / sc));
+        lo = pack4_e4m3(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
+        hi = pack4_e4m3(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);
     }
     __builtin_nontemporal_store(u32x2{lo, hi}, reinterpret_cast<u32x2*>(qptr + sub * 8));
     return sc;
