@@ -137,6 +137,25 @@ def bench_norm(steps, warmup, dev, H=7168):
     return out
 
 
+def bench_requant(steps, warmup, dev, E=32, N=4096, K=7168):
+    """Load-time in-place requant of MoE expert weights (DeepSeek-V3's
+    gate_up shape, E experts in one launch): algorithmic bytes = the fp8
+    codes read and written plus the block scales read and written."""
+    import torch
+    from kb_nano_amd import postprocess_fp8_weights_batched
+    gen = torch.Generator(device=dev).manual_seed(13)
+    W = torch.empty(E, N, K, dtype=torch.float8_e4m3fn, device=dev)
+    sW = torch.empty(E, N // 128, K // 128, device=dev)
+    for e in range(E):
+        W[e], sW[e] = _rand_weight(N, K, gen, dev, torch)
+    nbytes = 2 * E * N * K + 8 * E * (N // 128) * (K // 128)
+    ms = _events_time_ms(lambda i: postprocess_fp8_weights_batched(W, sW), steps, warmup)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    del W, sW
+    torch.cuda.empty_cache()
+    return {"E": E, "N": N, "K": K, "us": ms * 1e3, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
+
+
 def _gemm_case(name, M, N, K, steps, warmup, dev, seed):
     import torch
     from kb_nano_amd import _ops
@@ -332,7 +351,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default="all",
-                    help="comma list of extra sections: quant,norm,dsv3,moe,decode (default all; 'none' = headline only)")
+                    help="comma list of extra sections: quant,norm,requant,dsv3,moe,decode (default all; 'none' = headline only)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three 1 GiB device copies (reference for rocprofv3 byte counters)")
@@ -354,7 +373,7 @@ def main():
     from kb_nano_amd._lib import require_gfx950
     require_gfx950(0)
 
-    sections = {"quant", "norm", "dsv3", "moe", "decode"} if args.only == "all" else \
+    sections = {"quant", "norm", "requant", "dsv3", "moe", "decode"} if args.only == "all" else \
         set() if args.only == "none" else set(args.only.split(","))
 
     torch.cuda.synchronize()
@@ -371,6 +390,9 @@ def main():
         for r in extra["rmsnorm_quant_dsv3"]:
             print(f"[bench] rmsnorm_quant M={r['M']} add={r['residual_add']}: {r['us']:.1f} us {r['GB/s']:.0f} GB/s",
                   file=sys.stderr, flush=True)
+    if "requant" in sections:
+        extra["weight_requant_dsv3_experts"] = bench_requant(**small)
+        print(f"[bench] weight requant: {extra['weight_requant_dsv3_experts']}", file=sys.stderr, flush=True)
     if "dsv3" in sections:
         extra["gemm_dsv3_cfg3"] = bench_dsv3(**small)
         for r in extra["gemm_dsv3_cfg3"]:

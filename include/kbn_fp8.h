@@ -205,6 +205,22 @@ int kbn_rmsnorm_fp8_quant(void* x_bf16, int64_t M, int64_t H, int64_t ld_x, cons
                           int64_t s_stride_m, int64_t s_stride_g, float eps, void* stream);
 
 /*
+ * 128x128 block (re)quantization of weights, one launch over [E, N, K].
+ * Replaces postprocess_fp8_weights[_batched] (tasks/baseline/L1/fp8_linear.py:453-554)
+ * and the DeepGEMM per_block_cast_to_fp8 it calls (:497-499, :543-545).
+ *   w_in    [E, N, K] contiguous: fp8 codes (in_f32 = 0), dequantized with the
+ *           block scale s_in[e*s_in_e + nb*s_in_ld + kb], or fp32 values (1)
+ *   w_out   fp8 [E, N, K] contiguous, s_out[e*s_out_e + nb*s_out_ld + kb];
+ *           both may alias the inputs (in-place requant).  K % 16 == 0,
+ *           16-byte aligned weights.
+ *   Per block: sf = max(max|x|, eps) / 448, rounded up to a power of two when
+ *   use_ue8m0; codes = e4m3_rne(x * (1/sf)); ragged blocks pad with zeros.
+ */
+int kbn_fp8_block_requant(const void* w_in, int in_f32, const float* s_in, int64_t s_in_e, int64_t s_in_ld,
+                          int64_t E, int64_t N, int64_t K, void* w_out, float* s_out,
+                          int64_t s_out_e, int64_t s_out_ld, int use_ue8m0, float eps, void* stream);
+
+/*
  * Test hook (no counterpart in the reference): the kernels' bf16 SiLU
  * applied elementwise to n bf16 bit patterns, for exhaustive checking.
  */

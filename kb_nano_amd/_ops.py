@@ -309,6 +309,42 @@ def rmsnorm_fp8_quant(output_fp8: torch.Tensor, output_scales: torch.Tensor, inp
         output_scales.stride(1), float(eps), _stream(input)), what)
 
 
+def fp8_block_requant(w_in: torch.Tensor, s_in: torch.Tensor | None, w_out: torch.Tensor, s_out: torch.Tensor,
+                      use_ue8m0: bool, eps: float) -> None:
+    """128x128 block quantization of ``w_in`` ([N, K] or [E, N, K]; fp8 codes
+    dequantized with the block scales ``s_in``, or fp32) into ``w_out`` (fp8,
+    same shape) and ``s_out`` ([(E,) ceil(N/128), >= ceil(K/128)]); outputs may
+    alias the inputs."""
+    what = "fp8_block_requant"
+    _dev_check(what, *[t for t in (w_in, s_in, w_out, s_out) if t is not None])
+    in_f32 = w_in.dtype == torch.float32
+    if not in_f32:
+        _dtype_check(what, w_in, FP8, "w_in")
+        if s_in is None:
+            raise ValueError(f"{what}: fp8 input needs its block scales")
+        _dtype_check(what, s_in, torch.float32, "s_in")
+    _dtype_check(what, w_out, FP8, "w_out")
+    _dtype_check(what, s_out, torch.float32, "s_out")
+    if w_in.shape != w_out.shape or w_in.dim() not in (2, 3):
+        raise ValueError(f"{what}: w_in and w_out must both be [N, K] or [E, N, K]")
+    if not (w_in.is_contiguous() and w_out.is_contiguous()):
+        raise ValueError(f"{what}: weights must be contiguous")
+    E = w_in.shape[0] if w_in.dim() == 3 else 1
+    N, K = w_in.shape[-2:]
+    NB, KB = -(-N // GROUP), -(-K // GROUP)
+
+    def strides(s, name):
+        if s.dim() != w_in.dim() or s.shape[-2] < NB or s.shape[-1] < KB or s.stride(-1) != 1:
+            raise ValueError(f"{what}: {name} must be [..., >= {NB}, >= {KB}] with unit column stride")
+        return (s.stride(0) if s.dim() == 3 else NB * s.stride(-2)), s.stride(-2)
+
+    so_e, so_ld = strides(s_out, "s_out")
+    si_e, si_ld = strides(s_in, "s_in") if not in_f32 else (0, 0)
+    check(lib().kbn_fp8_block_requant(
+        w_in.data_ptr(), int(in_f32), s_in.data_ptr() if not in_f32 else None, si_e, si_ld, E, N, K,
+        w_out.data_ptr(), s_out.data_ptr(), so_e, so_ld, int(bool(use_ue8m0)), float(eps), _stream(w_out)), what)
+
+
 def debug_silu_bf16(g_bits: torch.Tensor, out_bits: torch.Tensor) -> None:
     """Test hook: the kernels' silu (bf16 in, bf16 out) on int16 bit patterns."""
     _dev_check("debug_silu_bf16", g_bits, out_bits)

@@ -139,45 +139,43 @@ class Fp8Linear(nn.Module):
 # ---------------------------------------------------------------------------
 
 def _block_requant(w_f32: torch.Tensor, use_ue8m0: bool, eps: float = 1e-4):
-    """128x128 block quantization of a float32 [N,K] matrix on its device.
+    """128x128 block quantization of a float32 [N,K] (or [E,N,K]) weight on
+    its device, in one gfx950 launch (``kbn_fp8_block_requant``).
 
-    Follows DeepGEMM v2.1.1.post3's ``per_block_cast_to_fp8`` (pyproject.toml:21;
-    called at fp8_linear.py:497-499): pad to whole blocks, amax per block
-    clamped to 1e-4, sf = amax/448 rounded up to a power of two under UE8M0,
-    codes = fp8(x * (1/sf)).  Returns (fp8 [N,K], fp32 [ceil(N/128), ceil(K/128)])."""
-    N, K = w_f32.shape
+    DeepGEMM v2.1.1.post3's ``per_block_cast_to_fp8`` (pyproject.toml:21;
+    called at fp8_linear.py:497-499): ragged blocks pad with zeros, amax per
+    block clamped to ``eps``, sf = amax/448 rounded up to a power of two under
+    UE8M0, codes = fp8(x * (1/sf)).  Returns (fp8, fp32 [(E,) ceil(N/128),
+    ceil(K/128)])."""
+    N, K = w_f32.shape[-2:]
     NB, KB = math.ceil(N / GROUP), math.ceil(K / GROUP)
-    pad = torch.zeros(NB * GROUP, KB * GROUP, dtype=torch.float32, device=w_f32.device)
-    pad[:N, :K] = w_f32
-    blocks = pad.view(NB, GROUP, KB, GROUP)
-    sf = blocks.abs().amax(dim=(1, 3), keepdim=True).clamp_min(eps) / _FP8_INFO.max
-    if use_ue8m0:
-        sf = torch.pow(2.0, torch.ceil(torch.log2(sf)))
-    q = (blocks * (1.0 / sf)).to(FP8).view(NB * GROUP, KB * GROUP)[:N, :K].contiguous()
-    return q, sf.view(NB, KB)
+    w = w_f32 if w_f32.is_contiguous() else w_f32.contiguous()
+    q = torch.empty(w.shape, dtype=FP8, device=w.device)
+    s = torch.empty(w.shape[:-2] + (NB, KB), dtype=torch.float32, device=w.device)
+    _ops.fp8_block_requant(w, None, q, s, use_ue8m0, eps)
+    return q, s
 
 
 def postprocess_fp8_weights(weight_fp8: torch.Tensor, scale_inv: torch.Tensor):
     """Re-quantize a checkpoint's fp8 weight to the scale format the GEMM
-    consumes (reference :453-512).  Under the UE8M0 contract the weight is
-    dequantized per 128x128 block and re-quantized with power-of-two scales;
-    the scale layout stays the canonical fp32 [ceil(N/128), ceil(K/128)]
-    (the gfx950 kernels read it directly, no layout transform is needed)."""
+    consumes (reference :453-512): each 128x128 block is dequantized with its
+    fp32 scale and re-quantized, with power-of-two scales under the UE8M0
+    contract, in one gfx950 launch that reads and writes one byte per element.
+    The scale layout stays the canonical fp32 [ceil(N/128), ceil(K/128)] (the
+    kernels read it directly, so DeepGEMM's layout transform has no
+    counterpart).  Returns new (weight, scale) tensors."""
     N, K = weight_fp8.shape
     NB, KB = math.ceil(N / GROUP), math.ceil(K / GROUP)
-    scale = scale_inv[:NB, :KB].to(torch.float32)
-    expand = scale.repeat_interleave(GROUP, 0)[:N].repeat_interleave(GROUP, 1)[:, :K]
-    w_f32 = weight_fp8.to(torch.float32) * expand
-    return _block_requant(w_f32, use_ue8m0=is_e8m0_used())
+    w = torch.empty_like(weight_fp8)
+    s = torch.empty(NB, KB, dtype=torch.float32, device=weight_fp8.device)
+    _ops.fp8_block_requant(weight_fp8.contiguous(), scale_inv.to(torch.float32), w, s, is_e8m0_used(), 1e-4)
+    return w, s
 
 
 def postprocess_fp8_weights_batched(weight_fp8: torch.Tensor, scale_inv: torch.Tensor) -> None:
-    """In-place per-expert version for MoE weights [E,N,K] / scales
-    [E, ceil(N/128), ceil(K/128)] (reference :515-554)."""
+    """In-place version for MoE weights [E,N,K] / scales [E, >= ceil(N/128),
+    >= ceil(K/128)] (reference :515-554), all experts in one launch."""
     assert weight_fp8.ndim == 3
-    E, N, K = weight_fp8.shape
-    NB, KB = math.ceil(N / GROUP), math.ceil(K / GROUP)
-    for e in range(E):
-        w_new, s_new = postprocess_fp8_weights(weight_fp8[e], scale_inv[e])
-        weight_fp8[e].copy_(w_new)
-        scale_inv[e, :NB, :KB].copy_(s_new)
+    if scale_inv.dtype != torch.float32:
+        raise TypeError("postprocess_fp8_weights_batched: scale_inv must be float32 to be rewritten in place")
+    _ops.fp8_block_requant(weight_fp8, scale_inv, weight_fp8, scale_inv, is_e8m0_used(), 1e-4)

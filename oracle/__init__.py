@@ -21,6 +21,11 @@ Parity pins (see ``tests/test_oracle.py``):
   * GEMM: float64 brute force on tiny shapes, torch fp32 dequant-matmul on
     small shapes, and closed-form special cases (single non-zero K block,
     identity-like weights, all-equal scales).
+  * weight block requant: the reference's torch formula (DeepGEMM's
+    ``per_block_cast_to_fp8`` on the dequantized weight) executed by torch on
+    the CPU, ``quant_block128``'s division form under UE8M0 (equal there,
+    since 1/sf is exact), and the identity on power-of-two-scaled blocks
+    whose largest code is 448.
   * MoE layout: brute-force placement on small routings (each expert's rows
     counted by a direct loop), the structural invariants of the layout
     (segments start on alignment boundaries, (token, slot) order inside a
@@ -217,6 +222,47 @@ def quant_block128(w_f32: np.ndarray, eps: float = EPS, use_ue8m0: bool = True):
     v = np.clip(w / sx, -FP8_MAX, FP8_MAX).astype(np.float32)
     q = _encode_fast(v)
     return q, s.astype(np.float32)
+
+
+def block_requant(w: np.ndarray, s_in=None, use_ue8m0: bool = True, eps: float = 1e-4):
+    """Load-time 128x128 block requantization of a weight [N, K] or [E, N, K]
+    (tasks/baseline/L1/fp8_linear.py:453-554).
+
+    ``w`` is either uint8 e4m3 codes, dequantized as fp32(code) * s_in[block]
+    (:486, :533-535), or float32 values (s_in None).  Each block then goes
+    through DeepGEMM v2.1.1.post3's ``per_block_cast_to_fp8`` (called at
+    :497-499 and :543-545; DeepGEMM is not vendored in the reference):
+    zero-padded to whole blocks, amax = max|x| clamped below at eps (1e-4
+    there), sf = amax / 448, rounded up to a power of two under UE8M0, codes =
+    e4m3(x * (1 / sf)) with the reciprocal taken in float32.  Every |x * (1/sf)|
+    is at most 448 (1 + 2^-23)^2, which the cast rounds to 448, so clipping to
+    +-448 before the nearest-code encoder changes nothing.  Returns (uint8
+    codes of w's shape, float32 scales [(E,) ceil(N/128), ceil(K/128)])."""
+    w = np.asarray(w)
+    squeeze = w.ndim == 2
+    if squeeze:
+        w = w[None]
+        if s_in is not None:
+            s_in = np.asarray(s_in)[None]
+    E, N, K = w.shape
+    NB, KB = -(-N // GROUP), -(-K // GROUP)
+    if w.dtype == np.uint8:
+        s = np.asarray(s_in, dtype=np.float32)[:, :NB, :KB]
+        sx = np.repeat(np.repeat(s, GROUP, 1), GROUP, 2)[:, :N, :K]
+        x = (e4m3_decode(w) * sx).astype(np.float32)
+    else:
+        x = np.asarray(w, dtype=np.float32)
+    pad = np.zeros((E, NB * GROUP, KB * GROUP), dtype=np.float32)
+    pad[:, :N, :K] = x
+    amax = np.abs(pad.reshape(E, NB, GROUP, KB, GROUP)).max(axis=(2, 4))
+    sf = (np.maximum(amax, np.float32(eps)) / np.float32(FP8_MAX)).astype(np.float32)
+    if use_ue8m0:
+        sf = ue8m0_from_ratio(sf)
+    inv = (np.float32(1.0) / sf).astype(np.float32)
+    ix = np.repeat(np.repeat(inv, GROUP, 1), GROUP, 2)[:, :N, :K]
+    v = np.clip(x * ix, -FP8_MAX, FP8_MAX).astype(np.float32)
+    q = _encode_fast(v)
+    return (q[0], sf[0]) if squeeze else (q, sf)
 
 
 def _encode_fast(v: np.ndarray) -> np.ndarray:

@@ -556,3 +556,86 @@ def test_rmsnorm_quant_residual_variant():
     xo = oracle.bf16_bits_to_f32(x_out)
     dq = oracle.e4m3_decode(q) * np.repeat(s, 128, axis=1)
     assert np.all(np.abs(xo - dq) <= np.abs(xo) * 2.0 ** -3 + np.repeat(s, 128, axis=1) * 2.0 ** -9 + 1e-30)
+
+
+# ------------------------------------------------------- weight block requant
+
+def _torch_per_block_cast(x: torch.Tensor, use_ue8m0: bool):
+    """DeepGEMM's per_block_cast_to_fp8 as the reference calls it
+    (tasks/baseline/L1/fp8_linear.py:497-499), run by torch on the CPU: zero
+    padding to whole blocks, amax clamped at 1e-4, sf = amax/448 (rounded up
+    to 2^ceil(log2 sf) under UE8M0), codes = (x * (1/sf)).to(e4m3)."""
+    m, n = x.shape
+    xp = torch.zeros(-(-m // 128) * 128, -(-n // 128) * 128)
+    xp[:m, :n] = x
+    xv = xp.view(-1, 128, xp.size(1) // 128, 128)
+    amax = xv.abs().float().amax(dim=(1, 3), keepdim=True).clamp(1e-4)
+    sf = amax / 448.0
+    if use_ue8m0:
+        sf = torch.pow(2.0, torch.ceil(torch.log2(sf.abs())))
+    q = (xv * (1.0 / sf)).to(torch.float8_e4m3fn)
+    return (q.view_as(xp)[:m, :n].contiguous().view(torch.uint8).numpy(),
+            sf.view(xv.size(0), xv.size(2)).numpy())
+
+
+def _checkpoint_weight(N, K, seed):
+    """fp8 codes plus arbitrary (non power-of-two) fp32 block scales, as a
+    checkpoint stores them."""
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((N, K)) * 0.03).astype(np.float32)
+    q, s = oracle.quant_block128(w, use_ue8m0=False)
+    s = (s * rng.uniform(0.5, 3.0, s.shape)).astype(np.float32)
+    return q, s
+
+
+@pytest.mark.parametrize("N,K", [(256, 384), (200, 208), (130, 512), (128, 16)])
+@pytest.mark.parametrize("use_ue8m0", [True, False])
+def test_block_requant_vs_torch_deepgemm_formula(N, K, use_ue8m0):
+    q, s = _checkpoint_weight(N, K, seed=N + K)
+    got_q, got_s = oracle.block_requant(q, s, use_ue8m0=use_ue8m0)
+    # the reference's dequant (:486): codes to fp32 times the block scale
+    sx = torch.from_numpy(s).repeat_interleave(128, 0)[:N].repeat_interleave(128, 1)[:, :K]
+    x = torch.from_numpy(q).view(torch.float8_e4m3fn).float() * sx
+    ref_q, ref_s = _torch_per_block_cast(x, use_ue8m0)
+    assert np.array_equal(got_s, ref_s)
+    assert np.array_equal(got_q, ref_q)
+    # an fp32 master weight goes through the same cast
+    got_q2, got_s2 = oracle.block_requant(x.numpy(), None, use_ue8m0=use_ue8m0)
+    assert np.array_equal(got_q2, ref_q) and np.array_equal(got_s2, ref_s)
+
+
+def test_block_requant_batched_and_special_blocks():
+    """Experts requantize independently; an all-zero block gets sf = 1e-4/448
+    (2^-22 under UE8M0) and zero codes; a block with a huge entry keeps its
+    largest code at 448; ue8m0 with fp32 input equals quant_block128's
+    division form at eps 1e-4 (1/sf is exact for a power of two)."""
+    rng = np.random.default_rng(3)
+    E, N, K = 3, 256, 256
+    x = (rng.standard_normal((E, N, K)) * 0.05).astype(np.float32)
+    x[1, :128, 128:] = 0.0
+    x[2, 5, 7] = 3.0e4
+    q, s = oracle.block_requant(x, None, use_ue8m0=True)
+    for e in range(E):
+        qe, se = oracle.block_requant(x[e], None, use_ue8m0=True)
+        assert np.array_equal(q[e], qe) and np.array_equal(s[e], se)
+        qb, sb = oracle.quant_block128(x[e], eps=1e-4, use_ue8m0=True)
+        assert np.array_equal(qe, qb) and np.array_equal(se, sb)
+    assert s[1, 0, 1] == np.float32(2.0 ** -22) and not q[1, :128, 128:].any()
+    assert oracle.e4m3_decode(q[2, 5, 7]) == 448.0 or s[2, 0, 0] * 448 > 3.0e4
+    _, s_plain = oracle.block_requant(x[1], None, use_ue8m0=False)
+    assert s_plain[0, 1] == np.float32(np.float32(1e-4) / np.float32(448))
+
+
+def test_block_requant_identity_on_pow2_checkpoint():
+    """Codes whose block maximum is 448 with power-of-two block scales come
+    back unchanged under UE8M0: amax = 448 * 2^k gives sf = 2^k exactly."""
+    rng = np.random.default_rng(8)
+    N, K = 384, 256
+    q = oracle._encode_fast(np.clip(rng.standard_normal((N, K)) * 60, -447, 447).astype(np.float32))
+    q[::128, ::128] = 0x7E                     # 448 in every block
+    s = (2.0 ** rng.integers(-14, -6, (3, 2))).astype(np.float32)
+    q2, s2 = oracle.block_requant(q, s, use_ue8m0=True)
+    assert np.array_equal(q2, q) and np.array_equal(s2, s)
+    # a non power-of-two scale moves the codes: x * (1/sf) is then inexact
+    q3, s3 = oracle.block_requant(q, s * np.float32(1.3), use_ue8m0=True)
+    assert not np.array_equal(q3, q) and np.array_equal(s3, s * 2)
