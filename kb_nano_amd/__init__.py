@@ -29,6 +29,7 @@ from .fp8_linear import (
 from .moe_grouped_gemm import m_grouped_fp8_gemm_nt_contiguous
 from .rmsnorm_quant import FusedAddRMSNormFP8Quant, RMSNormFP8Quant
 from .silu_mul_quant_fp8 import SiluMulQuantFp8
+from .weight_path import postprocess_model_fp8_weights, warmup_fp8_linear
 
 __all__ = [
     "Fp8Linear",
@@ -38,6 +39,8 @@ __all__ = [
     "FusedExperts",
     "RMSNormFP8Quant",
     "FusedAddRMSNormFP8Quant",
+    "postprocess_model_fp8_weights",
+    "warmup_fp8_linear",
     "m_grouped_fp8_gemm_nt_contiguous",
     "postprocess_fp8_weights",
     "postprocess_fp8_weights_batched",

@@ -98,6 +98,15 @@ class FusedExperts(nn.Module):
             setattr(sb, attr, raw)
         return raw[:need].view(dtype).view(shape)
 
+    def _reserve(self, max_tokens: int, K: int, N2: int, top_k: int, num_experts: int, device) -> None:
+        """Size the shared scratch buffers for up to ``max_tokens`` tokens of
+        this layer's shape, so later calls (and graph captures) reuse them
+        instead of growing them."""
+        M_sum = _compute_aligned_M(max_tokens, top_k, num_experts, _FP8_GROUP_SIZE)
+        self._get_fp8_bufs(max_tokens, K, device)
+        self._get_dg_workspace(1, (M_sum, max(N2, K)), device, torch.bfloat16)
+        self._get_dg_workspace(2, (M_sum, N2 // 2), device, torch.float8_e4m3fn)
+
     def forward(self, hidden_states: torch.Tensor, w13: torch.Tensor, w2: torch.Tensor, topk_weights: torch.Tensor,
                 topk_ids: torch.Tensor, num_experts: int, w13_scale: torch.Tensor | None = None,
                 w2_scale: torch.Tensor | None = None, w13_scale_dg: torch.Tensor | None = None,
