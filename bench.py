@@ -290,6 +290,82 @@ def bench_moe(steps, warmup, dev):
     return res
 
 
+def bench_moe_sorted(steps, warmup, dev):
+    """The sorted-token MoE path (DeepSeek-V3's FP8 experts in kb_nano,
+    VllmFusedExperts): config 4's batch (4096 tokens, hidden 7168, 256
+    experts, top-8, intermediate 2048) and two decode batches (64 tokens
+    through the align path, 4 tokens through the naive one-pair blocks).
+    Reports the align and moe_sum kernels, both sorted-token GEMMs at config 4
+    and the whole layer per batch."""
+    import torch
+    from kb_nano_amd import VllmFusedExperts, _ops
+    from kb_nano_amd.moe_align import MoeAlign
+    from kb_nano_amd.moe_grouped_gemm import get_triton_config
+    H, E, topk, I2, I = 7168, 256, 8, 4096, 2048
+    gen = torch.Generator(device=dev).manual_seed(7)
+
+    def experts(N, K):
+        w = torch.empty(E, N, K, dtype=torch.float8_e4m3fn, device=dev)
+        s = torch.empty(E, -(-N // 128), K // 128, device=dev)
+        for e in range(E):
+            w[e], s[e] = _rand_weight(N, K, gen, dev, torch)
+        return w, s
+
+    w13, s13 = experts(I2, H)
+    w2, s2 = experts(H, I)
+    wbytes13 = E * (I2 * H + 4 * (I2 // 128) * (H // 128))
+    wbytes2 = E * (H * I + 4 * (H // 128) * (I // 128))
+    layer = VllmFusedExperts()
+    res = {}
+    for T in (4096, 64, 4):
+        g = torch.Generator().manual_seed(T)
+        topk_ids = torch.topk(torch.softmax(torch.randn(T, E, generator=g), -1), topk, dim=-1).indices.to(dev)
+        topk_w = torch.softmax(torch.randn(T, topk, generator=g), -1).to(dev)
+        hidden = torch.randn(T, H, generator=gen, device=dev).bfloat16()
+        ms = _events_time_ms(lambda i: layer(hidden, w13, w2, topk_w, topk_ids, E, s13, s2, [128, 128]),
+                             steps, warmup)
+        active = int(torch.unique(topk_ids).numel())
+        res[f"layer_T{T}"] = {"us": ms * 1e3, "active_experts": active,
+                              "weight_GB/s": active * (wbytes13 + wbytes2) / E / ms / 1e6}
+        if T != 4096:
+            continue
+        block = get_triton_config(T, w13.shape, w2.shape, topk, True, [128, 128])["BLOCK_SIZE_M"]
+        al = MoeAlign()
+        ms = _events_time_ms(lambda i: al(topk_ids, block, E), steps, warmup)
+        res["align"] = {"us": ms * 1e3, "block": block}
+        sorted_ids, expert_ids, post = al(topk_ids, block, E)
+        a1, s_a1 = _quant_act(hidden, torch)
+        s_a1 = s_a1.contiguous()
+        n_pairs = T * topk
+        c1 = torch.empty(n_pairs, I2, dtype=torch.bfloat16, device=dev)
+        EM = sorted_ids.numel()
+        ms1 = _events_time_ms(lambda i: _ops.fused_moe_gemm(a1, s_a1, w13, s13, c1, sorted_ids, expert_ids, post, EM,
+                                                            block, topk), steps, warmup)
+        # GEMM2's input as the layer makes it: SiLU*Mul + quant of GEMM1's rows
+        a2q = torch.empty(n_pairs, I, dtype=torch.float8_e4m3fn, device=dev)
+        a2s = torch.empty(I // 128, n_pairs, device=dev).t()
+        _ops.silu_mul_quant_fp8(c1, a2q, a2s)
+        c2 = torch.empty(n_pairs, H, dtype=torch.bfloat16, device=dev)
+        wflat = topk_w.reshape(-1).contiguous()
+        ms2 = _events_time_ms(lambda i: _ops.fused_moe_gemm(a2q, a2s, w2, s2, c2, sorted_ids, expert_ids, post, EM,
+                                                            block, 1, topk_weights=wflat), steps, warmup)
+        total = int(post.item())
+        for tag, ms, N, K, wb in (("gemm1", ms1, I2, H, wbytes13), ("gemm2", ms2, H, I, wbytes2)):
+            t = ms * 1e-3
+            flop = 2.0 * n_pairs * N * K
+            nbytes = wb + total * (K + 4 * K // 128) + n_pairs * 2 * N
+            res[tag] = {"N": N, "K": K, "us": ms * 1e3, "TFLOPS": flop / t / 1e12, "GB/s": nbytes / t / 1e9,
+                        "frac_roof": max(flop / (FP8_PEAK_TFLOPS * 1e12), nbytes / (HBM_PEAK_GBS * 1e9)) / t}
+        out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        ms = _events_time_ms(lambda i: _ops.moe_sum(c2.view(T, topk, H), out), steps, warmup)
+        nbytes = n_pairs * H * 2 + T * H * 2
+        res["moe_sum"] = {"us": ms * 1e3, "GB/s": nbytes / ms / 1e6, "frac_hbm": nbytes / ms / 1e6 / HBM_PEAK_GBS}
+        del c1, c2, a2q, a2s, a1, out
+    del w13, s13, w2, s2
+    torch.cuda.empty_cache()
+    return res
+
+
 PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "silu_mul_quant_cfg2.md")
 
 
@@ -351,7 +427,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default="all",
-                    help="comma list of extra sections: quant,norm,requant,dsv3,moe,decode (default all; 'none' = headline only)")
+                    help="comma list of extra sections: quant,norm,requant,dsv3,moe,moe_sorted,decode (default all; 'none' = headline only)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three 1 GiB device copies (reference for rocprofv3 byte counters)")
@@ -373,7 +449,7 @@ def main():
     from kb_nano_amd._lib import require_gfx950
     require_gfx950(0)
 
-    sections = {"quant", "norm", "requant", "dsv3", "moe", "decode"} if args.only == "all" else \
+    sections = {"quant", "norm", "requant", "dsv3", "moe", "moe_sorted", "decode"} if args.only == "all" else \
         set() if args.only == "none" else set(args.only.split(","))
 
     torch.cuda.synchronize()
@@ -401,6 +477,9 @@ def main():
     if "moe" in sections:
         extra["moe_grouped_cfg4"] = bench_moe(**small)
         print(f"[bench] moe: {extra['moe_grouped_cfg4']}", file=sys.stderr, flush=True)
+    if "moe_sorted" in sections:
+        extra["moe_sorted_dsv3"] = bench_moe_sorted(**small)
+        print(f"[bench] moe sorted-token: {extra['moe_sorted_dsv3']}", file=sys.stderr, flush=True)
     if "decode" in sections:
         extra["decode_llama70b_cfg5"] = bench_decode(**small)
         for r in extra["decode_llama70b_cfg5"]:

@@ -205,6 +205,74 @@ int kbn_rmsnorm_fp8_quant(void* x_bf16, int64_t M, int64_t H, int64_t ld_x, cons
                           int64_t s_stride_m, int64_t s_stride_g, float eps, void* stream);
 
 /*
+ * Sorted-token MoE layout: moe_align_block_size.
+ * Replaces _C.moe_align_block_size (tasks/baseline/L1/csrc/moe_align.cu:28-383,
+ * bound by tasks/baseline/L1/moe_align.py:92 and
+ * tasks/baseline/L2/vllm_fused_experts.py:66-97).
+ *   topk_ids  [numel] int32 (ids_bytes 4) or int64 (8), flattened (token, slot)
+ *   Expert e's pairs fill slots [cumsum[e], cumsum[e] + count_e) in (token,
+ *   slot) order (the reference's atomic placement allows any order inside an
+ *   expert); segments are padded to block_size and every other slot of
+ *   sorted_token_ids holds numel.  expert_ids[b] is the owner of block b for
+ *   b < *num_tokens_post_pad / block_size (later entries are not written).
+ *   Pairs with ids outside [0, E) are not placed.  cumsum [E + 1] may be NULL.
+ *   sorted_len >= numel + min(numel, E) * (block_size - 1) and
+ *   expert_len * block_size >= that bound (the reference's buffer sizes).
+ *   workspace >= kbn_moe_permute_workspace_bytes(numel, E), 16-byte aligned.
+ */
+int kbn_moe_align_block_size(const void* topk_ids, int ids_bytes, int64_t numel, int64_t num_experts,
+                             int64_t block_size, int32_t* sorted_token_ids, int64_t sorted_len,
+                             int32_t* expert_ids, int64_t expert_len, int32_t* num_tokens_post_pad,
+                             int32_t* cumsum, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Sorted-token fused-MoE FP8 GEMM with 128x128 block scales.
+ * Replaces MoeGroupedGemm / _fused_moe_kernel (tasks/baseline/L1/moe_grouped_gemm.py:86-189,
+ * :298-382) on its use_fp8_w8a8 + block_shape [128, 128] path.
+ *   Row R < EM of the padded grid holds pair t = sorted_token_ids[R] (t >= num_valid:
+ *   padding), or with sorted_token_ids NULL (the reference's naive block
+ *   assignment) pair R / block_m on the first row of each block.  Block b =
+ *   R / block_m uses expert expert_ids[b]; blocks at or past
+ *   *num_tokens_post_padded are skipped.
+ *   A  fp8 [rows_A, K] (row stride lda) with fp32 scales sA (strides in
+ *      elements); pair t reads row t / top_k.
+ *   B  fp8 [E, N, K], sB fp32 [E, ceil(N/128), K/128], both contiguous.
+ *   C  bf16 [num_valid, ldc]: row t = sum_kb sA[t/top_k, kb] sB[e, n/128, kb]
+ *      (A.B^T of block kb), times topk_weights[t] (fp32) when that is not NULL.
+ *   Scales are taken as given.  K % 128 == 0, block_m a multiple of 64.
+ *   workspace: NULL, or kbn_fp8_fused_moe_gemm_workspace_bytes(EM, K) bytes,
+ *   16-byte aligned (see below).
+ */
+int kbn_fp8_fused_moe_gemm(const void* A, int64_t lda, int64_t rows_A, const float* sA, int64_t sA_stride_m,
+                           int64_t sA_stride_k, const void* B, const float* sB, void* C_bf16, int64_t ldc,
+                           const int32_t* sorted_token_ids, const int32_t* expert_ids,
+                           const int32_t* num_tokens_post_padded, int64_t EM, int64_t block_m,
+                           int64_t num_valid, int64_t top_k, const float* topk_weights, int64_t N, int64_t K,
+                           int64_t E, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Workspace of kbn_fp8_fused_moe_gemm (EM * K/128 fp32, -1 for bad sizes).
+ * With it, a first launch gathers the activation scales into sorted-row
+ * order so the GEMM reads them coalesced (about 8% faster at DeepSeek-V3
+ * sizes); with workspace NULL each row's scales are read where they lie.
+ */
+int64_t kbn_fp8_fused_moe_gemm_workspace_bytes(int64_t EM, int64_t K);
+
+/*
+ * Top-k sum of the experts' output rows.
+ * Replaces _C.moe_sum (tasks/baseline/L1/csrc/moe_sum.cu:8-63, bound by
+ * tasks/baseline/L1/moe_sum.py:43).
+ *   x    bf16, row (m, j) at x + (m * top_k + j) * ld_x, H columns
+ *   out  bf16 [M, H], row stride ld_out
+ *   top_k <= 4: x accumulates in bf16 from 0, rounding after every add (the
+ *   reference kernel's scalar_t accumulator).  top_k > 4 (and 1): the
+ *   reference's at::sum_out: four fp32 accumulators taking slots j % 4,
+ *   combined ((a0 + a1) + a2) + a3, one rounding to bf16.
+ */
+int kbn_moe_sum(const void* x_bf16, int64_t M, int64_t top_k, int64_t H, int64_t ld_x, void* out_bf16,
+                int64_t ld_out, void* stream);
+
+/*
  * 128x128 block (re)quantization of weights, one launch over [E, N, K].
  * Replaces postprocess_fp8_weights[_batched] (tasks/baseline/L1/fp8_linear.py:453-554)
  * and the DeepGEMM per_block_cast_to_fp8 it calls (:497-499, :543-545).

@@ -8,7 +8,9 @@ Four operators, each a drop-in for its kb_nano L1 counterpart:
   * ``Fp8GroupedGemmContiguous``  its contiguous-layout MoE grouped variant
 
 and ``FusedExperts``, the MoE experts layer that chains them (quant, permute,
-grouped GEMM, SiLU*Mul+quant, grouped GEMM, weighted unpermute), plus the
+grouped GEMM, SiLU*Mul+quant, grouped GEMM, weighted unpermute), its
+sorted-token counterpart ``VllmFusedExperts`` (``MoeAlign``,
+``MoeGroupedGemm``, ``MoeSum``), plus the
 fused ``RMSNormFP8Quant`` / ``FusedAddRMSNormFP8Quant`` that produce the
 quantized activations of a decoder layer's first linear.
 
@@ -26,9 +28,12 @@ from .fp8_linear import (
     postprocess_fp8_weights,
     postprocess_fp8_weights_batched,
 )
-from .moe_grouped_gemm import m_grouped_fp8_gemm_nt_contiguous
+from .moe_align import MoeAlign
+from .moe_grouped_gemm import MoeGroupedGemm, m_grouped_fp8_gemm_nt_contiguous
+from .moe_sum import MoeSum
 from .rmsnorm_quant import FusedAddRMSNormFP8Quant, RMSNormFP8Quant
 from .silu_mul_quant_fp8 import SiluMulQuantFp8
+from .vllm_fused_experts import VllmFusedExperts
 from .weight_path import postprocess_model_fp8_weights, warmup_fp8_linear
 
 __all__ = [
@@ -37,6 +42,10 @@ __all__ = [
     "SiluMulQuantFp8",
     "Fp8GroupedGemmContiguous",
     "FusedExperts",
+    "VllmFusedExperts",
+    "MoeAlign",
+    "MoeGroupedGemm",
+    "MoeSum",
     "RMSNormFP8Quant",
     "FusedAddRMSNormFP8Quant",
     "postprocess_model_fp8_weights",

@@ -35,6 +35,11 @@ SIGNATURES = {
          _P, _I64, _P], _I),
     "kbn_moe_unpermute_reduce": ([_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I, _P, _I64, _P], _I),
     "kbn_rmsnorm_fp8_quant": ([_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _F, _P], _I),
+    "kbn_moe_align_block_size": ([_P, _I, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _P], _I),
+    "kbn_fp8_fused_moe_gemm": ([_P, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                _P, _I64, _I64, _I64, _P, _I64, _P], _I),
+    "kbn_fp8_fused_moe_gemm_workspace_bytes": ([_I64, _I64], _I64),
+    "kbn_moe_sum": ([_P, _I64, _I64, _I64, _I64, _P, _I64, _P], _I),
     "kbn_fp8_block_requant": ([_P, _I, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I, _F, _P], _I),
     "kbn_debug_silu_bf16": ([_P, _P, _I64, _P], _I),
 }

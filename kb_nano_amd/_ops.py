@@ -309,6 +309,117 @@ def rmsnorm_fp8_quant(output_fp8: torch.Tensor, output_scales: torch.Tensor, inp
         output_scales.stride(1), float(eps), _stream(input)), what)
 
 
+def moe_align_block_size(topk_ids: torch.Tensor, num_experts: int, block_size: int, sorted_token_ids: torch.Tensor,
+                         expert_ids: torch.Tensor, num_tokens_post_pad: torch.Tensor,
+                         cumsum: torch.Tensor | None = None) -> None:
+    """Sorted-token layout of ``topk_ids`` (any shape, int32/int64): slots of
+    each expert padded to ``block_size``, sentinel ``numel`` elsewhere, one
+    expert id per block, the padded total in ``num_tokens_post_pad[0]``."""
+    what = "moe_align_block_size"
+    _dev_check(what, topk_ids, sorted_token_ids, expert_ids, num_tokens_post_pad,
+               *([cumsum] if cumsum is not None else []))
+    for t, name in ((sorted_token_ids, "sorted_token_ids"), (expert_ids, "expert_ids"),
+                    (num_tokens_post_pad, "num_tokens_post_pad")) + (((cumsum, "cumsum"),) if cumsum is not None else ()):
+        _dtype_check(what, t, torch.int32, name)
+        if not t.is_contiguous():
+            raise ValueError(f"{what}: {name} must be contiguous")
+    if topk_ids.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"{what}: topk_ids must be int32 or int64, got {topk_ids.dtype}")
+    if not topk_ids.is_contiguous():
+        raise ValueError(f"{what}: topk_ids must be contiguous")
+    if cumsum is not None and cumsum.numel() < num_experts + 1:
+        raise ValueError(f"{what}: cumsum needs {num_experts + 1} entries")
+    numel = topk_ids.numel()
+    L = lib()
+    ws_bytes = int(L.kbn_moe_permute_workspace_bytes(numel, num_experts))
+    if ws_bytes < 0:
+        raise ValueError(f"{what}: num_experts={num_experts} outside [1, 1024] or too many pairs")
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=topk_ids.device)
+    check(L.kbn_moe_align_block_size(
+        topk_ids.data_ptr() if numel else None, topk_ids.element_size(), numel, num_experts, block_size,
+        sorted_token_ids.data_ptr(), sorted_token_ids.numel(), expert_ids.data_ptr(), expert_ids.numel(),
+        num_tokens_post_pad.data_ptr(), cumsum.data_ptr() if cumsum is not None else None,
+        ws.data_ptr(), ws.numel(), _stream(sorted_token_ids)), what)
+
+
+def fused_moe_gemm(a: torch.Tensor, a_scale: torch.Tensor, b: torch.Tensor, b_scale: torch.Tensor, c: torch.Tensor,
+                   sorted_token_ids: torch.Tensor | None, expert_ids: torch.Tensor,
+                   num_tokens_post_padded: torch.Tensor, EM: int, block_m: int, top_k: int,
+                   topk_weights: torch.Tensor | None = None) -> None:
+    """Sorted-token FP8 GEMM: ``c[t] = (a[t // top_k] . b[e]^T)`` with 1x128
+    activation and 128x128 weight block scales, for every routed pair t
+    (``c`` is [num_valid, N], num_valid = c rows), times ``topk_weights[t]``
+    when given."""
+    what = "fused_moe_gemm"
+    tensors = [a, a_scale, b, b_scale, c, expert_ids, num_tokens_post_padded]
+    if sorted_token_ids is not None:
+        tensors.append(sorted_token_ids)
+    if topk_weights is not None:
+        tensors.append(topk_weights)
+    _dev_check(what, *tensors)
+    _dtype_check(what, a, FP8, "A")
+    _dtype_check(what, b, FP8, "B")
+    _dtype_check(what, a_scale, torch.float32, "a_scale")
+    _dtype_check(what, b_scale, torch.float32, "b_scale")
+    _dtype_check(what, c, torch.bfloat16, "C")
+    for t, name in ((expert_ids, "expert_ids"), (num_tokens_post_padded, "num_tokens_post_padded")) + \
+            (((sorted_token_ids, "sorted_token_ids"),) if sorted_token_ids is not None else ()):
+        _dtype_check(what, t, torch.int32, name)
+        if not t.is_contiguous():
+            raise ValueError(f"{what}: {name} must be contiguous")
+    if a.dim() != 2 or b.dim() != 3 or c.dim() != 2:
+        raise ValueError(f"{what}: A [rows, K], B [E, N, K] and C [pairs, N] expected")
+    E, N, K = b.shape
+    rows_A = a.shape[0]
+    if a.shape[1] != K or c.shape[1] != N:
+        raise ValueError(f"{what}: K or N mismatch: A {tuple(a.shape)}, B {tuple(b.shape)}, C {tuple(c.shape)}")
+    KB, NB = -(-K // GROUP), -(-N // GROUP)
+    if tuple(a_scale.shape) != (rows_A, KB):
+        raise ValueError(f"{what}: a_scale must be {(rows_A, KB)}, got {tuple(a_scale.shape)}")
+    if tuple(b_scale.shape) != (E, NB, KB) or not b_scale.is_contiguous() or not b.is_contiguous():
+        raise ValueError(f"{what}: B and b_scale must be contiguous [E, N, K] and [E, {NB}, {KB}]")
+    if a.stride(1) != 1 or c.stride(1) != 1:
+        raise ValueError(f"{what}: rows of A and C must be contiguous")
+    num_valid = c.shape[0]
+    if topk_weights is not None:
+        _dtype_check(what, topk_weights, torch.float32, "topk_weights")
+        if topk_weights.numel() != num_valid or not topk_weights.is_contiguous():
+            raise ValueError(f"{what}: topk_weights must hold one contiguous fp32 weight per pair ({num_valid})")
+    if sorted_token_ids is not None and sorted_token_ids.numel() < EM:
+        raise ValueError(f"{what}: sorted_token_ids holds {sorted_token_ids.numel()} rows, EM = {EM}")
+    if expert_ids.numel() * block_m < EM:
+        raise ValueError(f"{what}: expert_ids holds {expert_ids.numel()} blocks of {block_m}, EM = {EM}")
+    L = lib()
+    # the scales are gathered into sorted-row order in a workspace from the
+    # caching allocator (stream-ordered on the launch stream)
+    ws_bytes = int(L.kbn_fp8_fused_moe_gemm_workspace_bytes(EM, K))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=c.device) if ws_bytes > 0 else None
+    check(L.kbn_fp8_fused_moe_gemm(
+        a.data_ptr(), a.stride(0), rows_A, a_scale.data_ptr(), a_scale.stride(0), a_scale.stride(1),
+        b.data_ptr(), b_scale.data_ptr(), c.data_ptr(), c.stride(0),
+        sorted_token_ids.data_ptr() if sorted_token_ids is not None else None, expert_ids.data_ptr(),
+        num_tokens_post_padded.data_ptr(), EM, block_m, num_valid, top_k,
+        topk_weights.data_ptr() if topk_weights is not None else None, N, K, E,
+        ws.data_ptr() if ws is not None else None, ws_bytes if ws is not None else 0, _stream(c)), what)
+
+
+def moe_sum(x: torch.Tensor, out: torch.Tensor) -> None:
+    """``out[m] = sum_j x[m, j]`` over the top-k rows of each token: ``x``
+    bf16 [M, top_k, H] (or [M * top_k, H] viewed so), ``out`` bf16 [M, H]."""
+    what = "moe_sum"
+    _dev_check(what, x, out)
+    _dtype_check(what, x, torch.bfloat16, "input")
+    _dtype_check(what, out, torch.bfloat16, "output")
+    if x.dim() != 3 or out.dim() != 2 or x.shape[0] != out.shape[0] or x.shape[2] != out.shape[1]:
+        raise ValueError(f"{what}: input [M, top_k, H] and output [M, H] expected, got {tuple(x.shape)} and "
+                         f"{tuple(out.shape)}")
+    M, top_k, H = x.shape
+    if x.stride(2) != 1 or out.stride(1) != 1 or (M > 1 and x.stride(0) != top_k * x.stride(1)):
+        raise ValueError(f"{what}: rows of input and output must be contiguous, slots of a token adjacent")
+    check(lib().kbn_moe_sum(x.data_ptr(), M, top_k, H, x.stride(1), out.data_ptr(), out.stride(0), _stream(out)),
+          what)
+
+
 def fp8_block_requant(w_in: torch.Tensor, s_in: torch.Tensor | None, w_out: torch.Tensor, s_out: torch.Tensor,
                       use_ue8m0: bool, eps: float) -> None:
     """128x128 block quantization of ``w_in`` ([N, K] or [E, N, K]; fp8 codes

@@ -77,6 +77,18 @@ struct GemmArgs {
     float* P;
     int64_t ws_bytes;            // bytes at P
     int splits, kb_per_split;
+    // Sorted-token layout (fused MoE): row R of the tile grid holds routed pair
+    // sorted_ids[R] (or, with no list, pair R / block_m on the first row of
+    // each block and nothing elsewhere); a pair t >= num_valid is padding.
+    // A row of pair t: t / a_row_div.  Output row: t.  Expert of block b:
+    // expert_ids[b], blocks at or past *num_post_pad are skipped.
+    const int32_t* sorted_ids;
+    const int32_t* num_post_pad;
+    int block_m, num_valid, a_row_div;
+    int64_t A_bytes;             // bytes at A the gathers may read
+    int64_t D_bytes;             // bytes at D the scattered stores may write
+    const float* row_weight;     // [num_valid] fp32 factors of the output rows, or nullptr
+    int sa_sorted;               // sA already holds row R's scales at R (gathered by sorted_scale_gather_kernel)
 };
 
 // Raw buffer descriptor (base, byte range) built from uniform values so it
@@ -178,9 +190,10 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 //               of K half 0 (and the scales) of block kb+1.
 // So kStages-1 blocks are in flight while one is consumed, and no fragment
 // register set is ever copied.
-template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, bool kSplitK, int kWaves>
+template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, bool kSplitK, int kWaves, bool kSorted = false>
 __global__ __launch_bounds__(64 * kWaves, (kStages * (BM + BN) * 128 + kStages * 512 * kWaves <= 80 * 1024) ? 2 : 1) void
 gemm_bs_kernel(const GemmArgs a) {
+    static_assert(!(kSorted && (kGrouped || kSplitK)), "the sorted-token layout is its own grouped mode");
     static_assert(kWaves == 4 || kWaves == 8, "2x2 or 2x4 wavefronts");
     constexpr int WM = 2, WN = kWaves / 2;
     constexpr int TM = BM / WM, TN = BN / WN;   // wavefront tile
@@ -214,8 +227,24 @@ gemm_bs_kernel(const GemmArgs a) {
         Wbase += (int64_t)expert * a.w_estride;
         sWbase += (int64_t)expert * a.sW_estride;
     }
+    if constexpr (kSorted) {
+        // a tile lies inside one block of block_m rows (BM divides block_m)
+        if (m0 >= a.num_post_pad[0]) return;
+        expert = a.expert_ids[m0 / a.block_m];
+        if (expert < 0 || expert >= a.E) return;
+        Wbase += (int64_t)expert * a.w_estride;
+        sWbase += (int64_t)expert * a.sW_estride;
+    }
+    // routed pair of tile row r, or -1 for padding
+    auto pair_of = [&](int r) -> int {
+        const int R = m0 + r;
+        if (R >= a.M) return -1;
+        const int t = a.sorted_ids ? a.sorted_ids[R] : (R % a.block_m == 0 ? R / a.block_m : -1);
+        return (t >= 0 && t < a.num_valid) ? t : -1;
+    };
 
-    const v4i dA = make_desc(a.A + (int64_t)m0 * a.lda, (int64_t)(a.M - m0 - 1) * a.lda + a.K);
+    const v4i dA = kSorted ? make_desc(a.A, a.A_bytes)
+                           : make_desc(a.A + (int64_t)m0 * a.lda, (int64_t)(a.M - m0 - 1) * a.lda + a.K);
     const v4i dW = make_desc(Wbase + (int64_t)n0 * a.ldw, (int64_t)(a.N - n0 - 1) * a.ldw + a.K);
     const v4i dSA = make_desc(a.sA, a.sA_bytes);
     const v4i dSW = make_desc(sWbase, (int64_t)NB * a.sW_ld * 4);
@@ -232,10 +261,29 @@ gemm_bs_kernel(const GemmArgs a) {
     const int a_o = a_e - ch_e + ch_o;
     const int w_e = (int)((wave * kBInstr * 8 + drow) * a.ldw) + ch_e + kb0 * kRowB;
     const int w_o = w_e - ch_e + ch_o;
+    // sorted layout: byte offset of each DMA row of this lane's A instructions
+    // (gathered rows; padding reads zeros)
+    int a_row[kSorted ? kAInstr : 1];
+    if constexpr (kSorted) {
+#pragma unroll
+        for (int i = 0; i < kAInstr; ++i) {
+            const int t = pair_of(wave * kAInstr * 8 + i * 8 + drow);
+            a_row[i] = t >= 0 ? (t / a.a_row_div) * (int)a.lda + kb0 * kRowB : kOob;
+        }
+    }
     const int sa_row = wave * 64 + lane;
-    const bool sa_live = (sa_row < BM) & (m0 + sa_row < a.M);
+    int sa_src = -1;    // activation-scale row of this lane's tile row
+    if (sa_row < BM) {
+        if constexpr (kSorted) {
+            const int t = pair_of(sa_row);
+            sa_src = t < 0 ? -1 : a.sa_sorted ? m0 + sa_row : t / a.a_row_div;
+        } else {
+            sa_src = m0 + sa_row < a.M ? m0 + sa_row : -1;
+        }
+    }
+    const bool sa_live = sa_src >= 0;
     const int sa_kstep = sa_live ? (int)(a.sA_sk * 4) : 0;
-    const int sa_off0 = sa_live ? (int)((int64_t)(m0 + sa_row) * a.sA_sm * 4) + kb0 * sa_kstep : kOob;
+    const int sa_off0 = sa_live ? (int)((int64_t)sa_src * a.sA_sm * 4) + kb0 * sa_kstep : kOob;
     const bool sw_live = (lane < (BN + 127) / 128) & (n0 / 128 + lane < NB);
     const int sw_kstep = sw_live ? 4 : 0;
     const int sw_off0 = sw_live ? (n0 / 128 + lane) * (int)a.sW_ld * 4 + kb0 * 4 : kOob;
@@ -254,8 +302,10 @@ gemm_bs_kernel(const GemmArgs a) {
             dma_b32(dSW, base + kA + kB + kSA + wave * 256, live ? sw_off0 + s * sw_kstep : kOob);
         } else if (d < 2 + kAInstr) {
             const int i = d - 2;
-            dma_b128(dA, base + (wave * kAInstr + i) * 1024,
-                     live ? ((i & 1) ? a_o : a_e) + (int)(i * 8 * a.lda) + k0 : kOob);
+            int off;
+            if constexpr (kSorted) off = a_row[i] + ((i & 1) ? ch_o : ch_e) + k0;
+            else off = ((i & 1) ? a_o : a_e) + (int)(i * 8 * a.lda) + k0;
+            dma_b128(dA, base + (wave * kAInstr + i) * 1024, live ? off : kOob);
         } else {
             const int i = d - 2 - kAInstr;
             dma_b128(dW, base + kA + (wave * kBInstr + i) * 1024,
@@ -489,19 +539,44 @@ gemm_bs_kernel(const GemmArgs a) {
         }
     };
 
+    // sorted layout: each fragment row's output row (its pair) and factor
+    int out_row[kSorted ? FM : 1];
+    if constexpr (kSorted) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            out_row[i] = pair_of(wm * TM + i * 32 + (lane & 31));
+            if (a.row_weight) {
+                const float f = out_row[i] >= 0 ? a.row_weight[out_row[i]] : 0.f;
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] * f;
+            }
+        }
+    }
+    // row byte offset of fragment row i in D (kOob: not stored)
+    auto out_off = [&](int i) -> int {
+        const int row = wm * TM + i * 32 + (lane & 31);
+        if constexpr (kSorted) return out_row[i] >= 0 ? out_row[i] * (int)a.ldd * 2 : kOob;
+        else if constexpr (kGrouped) return a.expert_ids[m0 + row] == expert ? row * (int)a.ldd * 2 : kOob;
+        else return row * (int)a.ldd * 2;
+    };
+
     auto epilogue = [&]() {
-        const int64_t bytes = std::min<int64_t>((int64_t)(a.M - m0 - 1) * a.ldd * 2 + (int64_t)a.N * 2,
-                                                (int64_t)BM * a.ldd * 2);
-        const __amdgpu_buffer_rsrc_t dD =
-            __builtin_amdgcn_make_buffer_rsrc(a.D + (int64_t)m0 * a.ldd, (short)0, (int)bytes, (int)kRsrcWord3);
+        const int64_t bytes = kSorted ? a.D_bytes
+                                      : std::min<int64_t>((int64_t)(a.M - m0 - 1) * a.ldd * 2 + (int64_t)a.N * 2,
+                                                          (int64_t)BM * a.ldd * 2);
+        const __amdgpu_buffer_rsrc_t dD = __builtin_amdgcn_make_buffer_rsrc(
+            kSorted ? a.D : a.D + (int64_t)m0 * a.ldd, (short)0, (int)std::min<int64_t>(bytes, 0x7FFFFFFFLL),
+            (int)kRsrcWord3);
         const int h = lane >> 5;
         const int ncol = n0 + wn * TN + 8 * h;
         const bool vec = a.vec_store && (n0 + BN <= a.N || a.N % 8 == 0);
         if (vec) {
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
-                const bool ok = kGrouped ? a.expert_ids[m0 + wm * TM + i * 32 + (lane & 31)] == expert : true;
-                const int roff = (wm * TM + i * 32 + (lane & 31)) * (int)a.ldd * 2;
+                const int roff = out_off(i);
+                const bool ok = roff != kOob;
 #pragma unroll
                 for (int j = 0; j < FN; ++j) {
 #pragma unroll
@@ -525,8 +600,8 @@ gemm_bs_kernel(const GemmArgs a) {
         } else {
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
-                const bool ok = kGrouped ? a.expert_ids[m0 + wm * TM + i * 32 + (lane & 31)] == expert : true;
-                const int roff = (wm * TM + i * 32 + (lane & 31)) * (int)a.ldd * 2;
+                const int roff = out_off(i);
+                const bool ok = roff != kOob;
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
 #pragma unroll
@@ -698,6 +773,39 @@ static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const cha
     return 0;
 }
 
+// Sorted-token layout: the activation scales of every row R below the padded
+// total, gathered into column-major [KB, EM] order (row R of block kb at
+// kb * EM + R; padding rows get 0), so the GEMM's per-row scale loads are
+// contiguous across lanes instead of one cache line per lane.
+__global__ __launch_bounds__(256) void sorted_scale_gather_kernel(const GemmArgs a, float* out, int KB) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int R = (int)(i % a.M);
+    const int kb = (int)(i / a.M);
+    if (kb >= KB || R >= a.num_post_pad[0]) return;
+    const int t = a.sorted_ids ? a.sorted_ids[R] : (R % a.block_m == 0 ? R / a.block_m : -1);
+    float v = 0.f;
+    if (t >= 0 && t < a.num_valid) v = a.sA[(int64_t)(t / a.a_row_div) * a.sA_sm + (int64_t)kb * a.sA_sk];
+    out[(int64_t)kb * a.M + R] = v;
+}
+
+// Sorted-token (fused MoE) launch: one workgroup per BM x BN tile of the
+// padded row grid; tiles past the padded total exit at once.
+template <int BM, int BN, int kStages>
+static int launch_sorted(GemmArgs a, hipStream_t st, const char* what) {
+    a.tiles_m = (a.M + BM - 1) / BM;
+    a.tiles_n = (a.N + BN - 1) / BN;
+    const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
+    KBN_CHECK_ARG(tiles <= 0x7FFFFFFFLL, "%s: too many tiles", what);
+    if (tiles == 0) return 0;
+    a.tile_base = 0;
+    a.tile_count = (int)tiles;
+    a.splits = 1;
+    a.kb_per_split = a.K / kRowB;
+    gemm_bs_kernel<BM, BN, kStages, false, false, false, 4, true><<<dim3((unsigned)tiles), dim3(256), 0, st>>>(a);
+    KBN_CHECK_LAUNCH(what);
+    return 0;
+}
+
 }  // namespace kbn
 
 using namespace kbn;
@@ -857,4 +965,74 @@ extern "C" int kbn_fp8_grouped_gemm_nt_contiguous(const void* A, int64_t lda, co
     Schedule sc;   // grouped: data-parallel, one workgroup per 128-row block x N tile
     if (scale_ue8m0) return launch_gemm<128, 256, 3, true, true>(a, sc, st, what);
     return launch_gemm<128, 256, 3, false, true>(a, sc, st, what);
+}
+
+extern "C" int64_t kbn_fp8_fused_moe_gemm_workspace_bytes(int64_t EM, int64_t K) {
+    if (EM < 0 || K <= 0 || K % kGroup != 0 || EM > 0x7FFFFFFFLL) return -1;
+    return EM * (K / kGroup) * 4;
+}
+
+extern "C" int kbn_fp8_fused_moe_gemm(const void* A, int64_t lda, int64_t rows_A, const float* sA, int64_t sA_stride_m,
+                                      int64_t sA_stride_k, const void* B, const float* sB, void* C_bf16, int64_t ldc,
+                                      const int32_t* sorted_token_ids, const int32_t* expert_ids,
+                                      const int32_t* num_tokens_post_padded, int64_t EM, int64_t block_m,
+                                      int64_t num_valid, int64_t top_k, const float* topk_weights, int64_t N,
+                                      int64_t K, int64_t E, void* workspace, int64_t workspace_bytes, void* stream) {
+    const char* what = "fused_moe_gemm";
+    KBN_CHECK_ARG(rows_A >= 0 && N >= 0 && K > 0 && E > 0 && EM >= 0 && num_valid >= 0 && top_k >= 1,
+                  "%s: bad shape", what);
+    KBN_CHECK_ARG(K % kGroup == 0, "%s: K=%lld must be a multiple of 128", what, (long long)K);
+    KBN_CHECK_ARG(block_m >= 64 && block_m % 64 == 0, "%s: block_m=%lld must be a multiple of 64", what,
+                  (long long)block_m);
+    if (EM == 0 || N == 0 || num_valid == 0) return 0;
+    KBN_CHECK_ARG(A && sA && B && sB && C_bf16 && expert_ids && num_tokens_post_padded, "%s: null pointer", what);
+    KBN_CHECK_ARG((num_valid - 1) / top_k < rows_A, "%s: %lld pairs over top_k %lld need %lld A rows, got %lld", what,
+                  (long long)num_valid, (long long)top_k, (long long)((num_valid - 1) / top_k + 1), (long long)rows_A);
+    KBN_CHECK_ARG(lda >= K && lda % 16 == 0 && aligned16(A) && aligned16(B), "%s: A and B rows must be 16-byte aligned",
+                  what);
+    KBN_CHECK_ARG(ldc >= N && ((reinterpret_cast<uintptr_t>(C_bf16) & 1u) == 0), "%s: bad C", what);
+    // gathered rows and scattered stores use 32-bit byte offsets
+    KBN_CHECK_ARG(rows_A * lda < 0x7FFFFFFFLL && num_valid * ldc * 2 < 0x7FFFFFFFLL && EM <= 0x7FFFFFFFLL &&
+                      N <= 0x7FFFFFFFLL && K <= 0x7FFFFFFFLL && E <= 0x7FFFFFFFLL && num_valid <= 0x7FFFFFFFLL,
+                  "%s: operands span >= 2 GiB", what);
+    const int64_t NB = (N + kGroup - 1) / kGroup, KB = K / kGroup;
+    if (int rc = check_scale_ranges(what, rows_A, K, sA_stride_m, sA_stride_k, NB, KB)) return rc;
+    GemmArgs a{};
+    a.A = (const uint8_t*)A; a.lda = lda; a.A_bytes = rows_A * lda;
+    a.sA = sA; a.sA_sm = sA_stride_m; a.sA_sk = sA_stride_k;
+    a.sA_bytes = scale_bytes(rows_A, KB, sA_stride_m, sA_stride_k);
+    a.W = (const uint8_t*)B; a.ldw = K; a.w_estride = N * K;
+    a.sW = sB; a.sW_ld = KB; a.sW_estride = NB * KB;
+    a.D = (uint16_t*)C_bf16; a.ldd = ldc; a.D_bytes = (num_valid - 1) * ldc * 2 + N * 2;
+    a.vec_store = (reinterpret_cast<uintptr_t>(C_bf16) % 16 == 0) && (ldc % 8 == 0);
+    a.expert_ids = expert_ids;
+    a.sorted_ids = sorted_token_ids;
+    a.num_post_pad = num_tokens_post_padded;
+    a.block_m = (int)block_m;
+    a.num_valid = (int)num_valid;
+    a.a_row_div = (int)top_k;
+    a.row_weight = topk_weights;
+    a.M = (int)EM; a.N = (int)N; a.K = (int)K; a.E = (int)E;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (workspace) {
+        // gather the scales into sorted order first; the GEMM then reads them
+        // like the contiguous layout's
+        const int64_t need = EM * KB * 4;
+        KBN_CHECK_ARG(workspace_bytes >= need && aligned16(workspace) && need < 0x7FFFFFFFLL,
+                      "%s: workspace of %lld bytes (16-byte aligned) needed, got %lld", what, (long long)need,
+                      (long long)workspace_bytes);
+        const int64_t threads = EM * KB;
+        sorted_scale_gather_kernel<<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st>>>(
+            a, static_cast<float*>(workspace), (int)KB);
+        KBN_CHECK_LAUNCH(what);
+        a.sA = static_cast<const float*>(workspace);
+        a.sA_sm = 1;
+        a.sA_sk = EM;
+        a.sA_bytes = need;
+        a.sa_sorted = 1;
+    }
+    // the scales are taken as given (fp32 contract), as the reference's
+    // per-block promotion does
+    if (block_m % 128 == 0) return launch_sorted<128, 256, 3>(a, st, what);
+    return launch_sorted<64, 256, 3>(a, st, what);
 }

@@ -19,7 +19,23 @@
 //          asked, zeros for padding rows.
 // Ranks follow (token, slot) order inside each expert, as the reference's
 // stable argsort does, so the layout is index-identical to the reference.
+//
+// The same count and scan also build the sorted-token layout of
+// moe_align_block_size (tasks/baseline/L1/csrc/moe_align.cu:28-383, the
+// sgl-kernel source vLLM uses): a third launch writes each pair's index into
+// its slot, fills the rest of the buffer with the sentinel numel, and
+// writes the owner expert of every block.  The reference places pairs with
+// atomics, so its order inside an expert varies from run to run; here it is
+// the (token, slot) order, one of the orders the reference can produce.
+//
+// moe_sum (tasks/baseline/L1/csrc/moe_sum.cu:8-63) sums the top-k output rows
+// of each token: for top_k <= 4 in bf16, rounding after every add as the
+// reference kernel's bf16 accumulator does; otherwise through the reference's
+// at::sum_out, whose fp32 order on this GPU is four round-robin accumulators
+// combined left to right (measured against torch.sum), then one rounding.
 #include "kbn_common.h"
+
+#include <algorithm>
 
 namespace kbn {
 namespace {
@@ -59,6 +75,11 @@ struct PermuteArgs {
     int M_sum;
     int zero_padding;
     int place_blocks;       // blocks [0, place_blocks) copy pairs, the rest fill rows
+    // moe_align_block_size
+    int32_t* sorted_ids;    // [sorted_len]: pair index per slot, numel elsewhere
+    int sorted_len;
+    int32_t* post_pad;      // [1]: total padded slots
+    int32_t* cumsum_out;    // [E + 1] segment offsets, or nullptr
 };
 
 // Expert id of pair i, or -1 when it lies outside [0, E).
@@ -225,6 +246,131 @@ __global__ __launch_bounds__(64 * kPlaceWaves) void moe_place_kernel(const Permu
             for (int g = lane; g < a.scale_cols; g += 64) a.sp[(int64_t)r * a.sp_m + (int64_t)g * a.sp_c] = 0.f;
         }
     }
+}
+
+// moe_align_block_size placement.  Blocks [0, place_blocks): one thread per
+// pair writes its index into its slot.  The remaining blocks: one thread per
+// slot of the buffer writes the sentinel into slots no pair owns and, at the
+// first slot of each block below the total, the block's expert.
+constexpr int kAlignThreads = 256;
+
+__global__ __launch_bounds__(kAlignThreads) void moe_align_place_kernel(const PermuteArgs a) {
+    __shared__ int s_off[kMaxExperts + 1];
+    __shared__ int s_cnt[kMaxExperts];
+    if ((int)blockIdx.x < a.place_blocks) {
+        const int i = (int)blockIdx.x * kAlignThreads + (int)threadIdx.x;
+        if (i >= a.n) return;
+        const int e = load_id(a, i);
+        if (e < 0) return;
+        a.sorted_ids[a.offsets[e] + a.hist[(int64_t)(i / a.chunk) * a.E + e] + a.rank[i]] = i;
+        return;
+    }
+    for (int j = threadIdx.x; j <= a.E; j += kAlignThreads) {
+        s_off[j] = a.offsets[j];
+        if (j < a.E) s_cnt[j] = a.counts[j];
+    }
+    __syncthreads();
+    const int total = s_off[a.E];
+    const int r = ((int)blockIdx.x - a.place_blocks) * kAlignThreads + (int)threadIdx.x;
+    if (r == 0) {
+        a.post_pad[0] = total;
+        if (a.cumsum_out)
+            for (int j = 0; j <= a.E; ++j) a.cumsum_out[j] = s_off[j];
+    }
+    if (r >= a.sorted_len) return;
+    int lo = 0, hi = a.E;   // last e in [0, E] with offsets[e] <= r
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_off[mid] <= r) lo = mid;
+        else hi = mid - 1;
+    }
+    const bool valid = lo < a.E && r - s_off[lo] < s_cnt[lo];
+    if (!valid) a.sorted_ids[r] = a.n;
+    if (r < total && r % a.align == 0) a.expert_ids[r / a.align] = lo;
+}
+
+// ----------------------------------------------------------------- moe_sum ---
+
+constexpr int kSumThreads = 128;   // 8 bf16 columns per thread
+
+struct MoeSumArgs {
+    const uint16_t* x;       // row (m, j) at x + (m * top_k + j) * ld_x
+    int64_t ld_x;
+    int top_k;
+    int H;
+    uint16_t* out;           // [M, H], row stride ld_out
+    int64_t ld_out;
+    int col_blocks;
+    int vec;                 // rows allow 16-B accesses
+};
+
+__device__ __forceinline__ float bf16_round(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return __uint_as_float(((u >> 16) | 0x40u) << 16);
+    return __uint_as_float(((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16) << 16);
+}
+
+// out[m, c] for the 8 columns c0 .. c0+7 of token m, v(j, q) the bf16 value
+// of slot j, column c0 + q.
+template <typename Load>
+__device__ __forceinline__ void topk_sum8(int top_k, Load v, float (&r)[8]) {
+#pragma clang fp contract(off)
+    if (top_k <= 4) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) r[q] = 0.f;
+        for (int j = 0; j < top_k; ++j) {
+            float x[8];
+            v(j, x);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) r[q] = bf16_round(r[q] + x[q]);
+        }
+        return;
+    }
+    float acc[4][8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v(j, acc[j]);
+    for (int j = 4; j < top_k; ++j) {
+        float x[8];
+        v(j, x);
+        float (&t)[8] = acc[j & 3];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) t[q] = t[q] + x[q];
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) r[q] = bf16_round(((acc[0][q] + acc[1][q]) + acc[2][q]) + acc[3][q]);
+}
+
+__global__ __launch_bounds__(kSumThreads) void moe_sum_kernel(const MoeSumArgs a) {
+    const int m = (int)blockIdx.x / a.col_blocks;
+    const int cb = (int)blockIdx.x - m * a.col_blocks;
+    const int c0 = (cb * kSumThreads + (int)threadIdx.x) * 8;
+    if (c0 >= a.H) return;
+    const uint16_t* row0 = a.x + (int64_t)m * a.top_k * a.ld_x + c0;
+    uint16_t* o = a.out + (int64_t)m * a.ld_out + c0;
+    const int nc = min(8, a.H - c0);
+    float r[8];
+    if (a.vec && nc == 8) {
+        topk_sum8(a.top_k, [&](int j, float (&x)[8]) {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(row0 + (int64_t)j * a.ld_x);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                x[2 * q] = bf16lo(w[q]);
+                x[2 * q + 1] = bf16hi(w[q]);
+            }
+        }, r);
+        u32x4 w;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            w[q] = (__float_as_uint(r[2 * q]) >> 16) | (__float_as_uint(r[2 * q + 1]) & 0xFFFF0000u);
+        *reinterpret_cast<u32x4*>(o) = w;
+        return;
+    }
+    topk_sum8(a.top_k, [&](int j, float (&x)[8]) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            x[q] = q < nc ? __uint_as_float((uint32_t)row0[(int64_t)j * a.ld_x + q] << 16) : 0.f;
+    }, r);
+    for (int q = 0; q < nc; ++q) o[q] = (uint16_t)(__float_as_uint(r[q]) >> 16);
 }
 
 // ------------------------------------------------------------ unpermute ---
@@ -438,6 +584,91 @@ extern "C" int kbn_moe_permute_contiguous(const void* topk_ids, int ids_bytes, i
         moe_place_kernel<<<dim3((unsigned)blocks), dim3(64 * kPlaceWaves), 0, st>>>(a);
         KBN_CHECK_LAUNCH(what);
     }
+    return 0;
+}
+
+extern "C" int kbn_moe_align_block_size(const void* topk_ids, int ids_bytes, int64_t numel, int64_t num_experts,
+                                        int64_t block_size, int32_t* sorted_token_ids, int64_t sorted_len,
+                                        int32_t* expert_ids, int64_t expert_len, int32_t* num_tokens_post_pad,
+                                        int32_t* cumsum, void* workspace, int64_t workspace_bytes, void* stream) {
+    const char* what = "moe_align_block_size";
+    KBN_CHECK_ARG(ids_bytes == 4 || ids_bytes == 8, "%s: ids_bytes must be 4 or 8, got %d", what, ids_bytes);
+    KBN_CHECK_ARG(numel >= 0 && numel <= 0x3FFFFFFFLL, "%s: bad numel=%lld", what, (long long)numel);
+    KBN_CHECK_ARG(num_experts >= 1 && num_experts <= kMaxExperts, "%s: num_experts=%lld outside [1, %d]", what,
+                  (long long)num_experts, kMaxExperts);
+    KBN_CHECK_ARG(block_size >= 1 && block_size <= (1 << 16), "%s: bad block_size %lld", what, (long long)block_size);
+    // the padded total never exceeds numel + min(numel, E) * (block_size - 1)
+    const int64_t bound = numel + std::min(numel, num_experts) * (block_size - 1);
+    KBN_CHECK_ARG(sorted_len >= bound && sorted_len <= 0x7FFFFFFFLL,
+                  "%s: sorted_token_ids holds %lld slots, the layout may need %lld", what, (long long)sorted_len,
+                  (long long)bound);
+    KBN_CHECK_ARG(expert_len * block_size >= bound, "%s: expert_ids holds %lld blocks, the layout may need %lld", what,
+                  (long long)expert_len, (long long)((bound + block_size - 1) / block_size));
+    KBN_CHECK_ARG(sorted_token_ids && expert_ids && num_tokens_post_pad, "%s: null output", what);
+    if (numel > 0) KBN_CHECK_ARG(topk_ids, "%s: null topk_ids", what);
+    const PermutePlan plan = permute_plan(numel, num_experts);
+    KBN_CHECK_ARG(workspace && aligned16(workspace) && workspace_bytes >= plan.bytes,
+                  "%s: workspace of %lld bytes (16-byte aligned) needed, got %lld", what, (long long)plan.bytes,
+                  (long long)workspace_bytes);
+    PermuteArgs a{};
+    a.ids = topk_ids;
+    a.ids64 = ids_bytes == 8;
+    a.n = (int)numel;
+    a.top_k = 1;
+    a.E = (int)num_experts;
+    int bits = 0;
+    while ((1LL << bits) < num_experts) ++bits;
+    a.bits = bits;
+    a.align = (int)block_size;
+    a.chunk = plan.chunk;
+    a.nchunks = plan.nchunks;
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    a.hist = reinterpret_cast<int*>(ws + plan.hist_off);
+    a.rank = reinterpret_cast<int*>(ws + plan.rank_off);
+    a.counts = reinterpret_cast<int*>(ws + plan.counts_off);
+    a.offsets = reinterpret_cast<int*>(ws + plan.offsets_off);
+    a.expert_ids = expert_ids;
+    a.sorted_ids = sorted_token_ids;
+    a.sorted_len = (int)sorted_len;
+    a.post_pad = num_tokens_post_pad;
+    a.cumsum_out = cumsum;
+    a.place_blocks = (int)((numel + kAlignThreads - 1) / kAlignThreads);
+    const int64_t fill_blocks = (sorted_len + kAlignThreads - 1) / kAlignThreads;
+
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (a.nchunks > 0) {
+        moe_count_kernel<<<dim3(a.nchunks), dim3(64), 0, st>>>(a);
+        KBN_CHECK_LAUNCH(what);
+    }
+    moe_scan_kernel<<<dim3(1), dim3(1024), 0, st>>>(a);
+    KBN_CHECK_LAUNCH(what);
+    moe_align_place_kernel<<<dim3((unsigned)(a.place_blocks + std::max<int64_t>(fill_blocks, 1))),
+                             dim3(kAlignThreads), 0, st>>>(a);
+    KBN_CHECK_LAUNCH(what);
+    return 0;
+}
+
+extern "C" int kbn_moe_sum(const void* x_bf16, int64_t M, int64_t top_k, int64_t H, int64_t ld_x, void* out_bf16,
+                           int64_t ld_out, void* stream) {
+    const char* what = "moe_sum";
+    KBN_CHECK_ARG(M >= 0 && top_k >= 1 && M * top_k <= 0x7FFFFFFFLL, "%s: bad M=%lld top_k=%lld", what,
+                  (long long)M, (long long)top_k);
+    KBN_CHECK_ARG(H >= 0 && H <= 0x7FFFFFFFLL && ld_x >= H && ld_out >= H, "%s: bad H or row strides", what);
+    if (M == 0 || H == 0) return 0;
+    KBN_CHECK_ARG(x_bf16 && out_bf16, "%s: null pointer", what);
+    MoeSumArgs a{};
+    a.x = static_cast<const uint16_t*>(x_bf16);
+    a.ld_x = ld_x;
+    a.top_k = (int)top_k;
+    a.H = (int)H;
+    a.out = static_cast<uint16_t*>(out_bf16);
+    a.ld_out = ld_out;
+    a.vec = aligned16(x_bf16) && aligned16(out_bf16) && ld_x % 8 == 0 && ld_out % 8 == 0;
+    a.col_blocks = (int)(((H + 7) / 8 + kSumThreads - 1) / kSumThreads);
+    const int64_t blocks = M * a.col_blocks;
+    KBN_CHECK_ARG(blocks <= 0x7FFFFFFFLL, "%s: M*H too large", what);
+    moe_sum_kernel<<<dim3((unsigned)blocks), dim3(kSumThreads), 0, static_cast<hipStream_t>(stream)>>>(a);
+    KBN_CHECK_LAUNCH(what);
     return 0;
 }
 

@@ -26,6 +26,12 @@ Parity pins (see ``tests/test_oracle.py``):
     the CPU, ``quant_block128``'s division form under UE8M0 (equal there,
     since 1/sf is exact), and the identity on power-of-two-scaled blocks
     whose largest code is 448.
+  * moe_align_block_size: each expert's slots hold exactly its pairs in
+    (token, slot) order (checked against a stable argsort), the reference's
+    buffer-size bound, sentinel and searchsorted block owners; moe_sum:
+    inputs whose fp32 sums are exact, where per-add bf16 rounding, a single
+    final rounding and the accumulator order give different answers, and on
+    the GPU torch.sum itself (the reference's at::sum_out).
   * MoE layout: brute-force placement on small routings (each expert's rows
     counted by a direct loop), the structural invariants of the layout
     (segments start on alignment boundaries, (token, slot) order inside a
@@ -377,6 +383,102 @@ def permute_contiguous(topk_ids: np.ndarray, num_experts: int, alignment: int):
             seen[e] += 1
     dest = np.where(valid, off[np.where(valid, flat, 0)] + within, -1)
     return expert_ids, dest, M_sum
+
+
+# ---------------------------------------------------------------------------
+# Sorted-token MoE (tasks/baseline/L1/csrc/moe_align.cu, moe_sum.cu,
+# tasks/baseline/L1/moe_grouped_gemm.py:86-189)
+# ---------------------------------------------------------------------------
+
+def moe_align_block_size(topk_ids: np.ndarray, num_experts: int, block_size: int, sorted_len: int | None = None):
+    """moe_align.cu:56-205 restated (the counting, padded prefix sum, sentinel
+    fill and per-block expert search), with pairs placed in flattened
+    (token, slot) order inside each expert.  The reference places them with
+    atomics (:28-40), so any order inside an expert is one it can produce.
+
+    Returns (sorted_ids int32 [sorted_len], expert_ids int32 [total /
+    block_size], total, cumsum int32 [E + 1]).  ``sorted_len`` defaults to
+    the reference's buffer size (vllm_fused_experts.py:74-78).  Pairs with
+    ids outside [0, E) are not placed."""
+    flat = np.asarray(topk_ids, dtype=np.int64).reshape(-1)
+    numel = flat.size
+    if sorted_len is None:
+        sorted_len = numel * block_size if numel < num_experts else numel + num_experts * (block_size - 1)
+    valid = (flat >= 0) & (flat < num_experts)
+    counts = np.bincount(flat[valid], minlength=num_experts).astype(np.int64)
+    padded = (counts + block_size - 1) // block_size * block_size
+    cumsum = np.zeros(num_experts + 1, dtype=np.int64)
+    cumsum[1:] = np.cumsum(padded)
+    total = int(cumsum[-1])
+    sorted_ids = np.full(sorted_len, numel, dtype=np.int32)
+    fill = cumsum[:-1].copy()
+    for i in range(numel):                      # (token, slot) order
+        e = flat[i]
+        if 0 <= e < num_experts:
+            sorted_ids[fill[e]] = i
+            fill[e] += 1
+    # expert of block b: last e with cumsum[e] <= b * block_size (:185-199)
+    starts = np.arange(total // block_size, dtype=np.int64) * block_size
+    expert_ids = (np.searchsorted(cumsum, starts, side="right") - 1).astype(np.int32)
+    return sorted_ids, expert_ids, total, cumsum.astype(np.int32)
+
+
+def moe_sum(x_bits: np.ndarray) -> np.ndarray:
+    """moe_sum.cu:8-63 on bf16 bit patterns x [M, top_k, H] -> [M, H].
+
+    top_k in 2..4: the kernel's bf16 accumulator, 0 + x_0 + x_1 ..., each sum
+    rounded to bf16 (:14-19).  Otherwise at::sum_out (:58-60): fp32 sums in
+    four accumulators taking slots j % 4, combined ((a0 + a1) + a2) + a3 and
+    rounded once (torch's reduction order for this shape on the MI355X,
+    measured against torch.sum)."""
+    x = bf16_bits_to_f32(np.asarray(x_bits, dtype=np.uint16))
+    M, k, H = x.shape
+    if 2 <= k <= 4:
+        acc = np.zeros((M, H), dtype=np.float32)
+        for j in range(k):
+            acc = bf16_bits_to_f32(f32_to_bf16_bits(acc + x[:, j]))
+        return f32_to_bf16_bits(acc)
+    parts = []
+    for q in range(min(4, k)):
+        a = x[:, q].copy()
+        for j in range(q + 4, k, 4):
+            a = (a + x[:, j]).astype(np.float32)
+        parts.append(a)
+    tot = parts[0]
+    for a in parts[1:]:
+        tot = (tot + a).astype(np.float32)
+    return f32_to_bf16_bits(tot)
+
+
+def fused_moe_gemm_sample(A, sA, B, sB, sorted_ids, expert_ids, total: int, block_m: int, num_valid: int,
+                          top_k: int, topk_weights=None, cols=None, naive: bool = False) -> dict:
+    """moe_grouped_gemm.py:86-189 on its FP8 block-scaled path, in float64:
+    for every pair t placed in a block below ``total``,
+    C[t, n] = w[t] * sum_kb sA[t // top_k, kb] sB[e, n // 128, kb] (A[t // top_k] . B[e, n]) over block kb.
+    With ``naive`` (no sorted list) block b holds pair b alone.  Returns
+    {pair t: float64 [len(cols)]}."""
+    B = np.asarray(B)
+    E, N, K = B.shape
+    cols = np.arange(N, dtype=np.int64) if cols is None else np.asarray(cols, dtype=np.int64)
+    rows_of = {}                                  # expert -> pairs
+    nblocks = total // block_m
+    for b in range(nblocks):
+        e = int(expert_ids[b])
+        if naive:
+            pairs = [b] if b < num_valid else []
+        else:
+            pairs = [int(t) for t in sorted_ids[b * block_m:(b + 1) * block_m] if 0 <= t < num_valid]
+        rows_of.setdefault(e, []).extend(pairs)
+    out = {}
+    for e, pairs in rows_of.items():
+        if not pairs:
+            continue
+        arows = np.array([t // top_k for t in pairs], dtype=np.int64)
+        vals = gemm_nt_sample(np.asarray(A)[arows], np.asarray(sA)[arows], B[e], np.asarray(sB)[e], cols=cols)
+        for r, t in enumerate(pairs):
+            w = 1.0 if topk_weights is None else float(np.asarray(topk_weights, dtype=np.float32).reshape(-1)[t])
+            out[t] = vals[r] * w
+    return out
 
 
 def unpermute_and_reduce(mm2_out_f32: np.ndarray, inv_perm: np.ndarray, topk_weights: np.ndarray,

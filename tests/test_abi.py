@@ -273,3 +273,70 @@ def test_rmsnorm_quant_surface_matches_reference():
     assert args(torch.ops.kb_nano_norm.fused_add_rmsnorm_fp8_quant) == [
         ("output_fp8", True), ("output_scales", True), ("input", True), ("residual", True), ("weight", False),
         ("eps", False)]
+
+
+def test_sorted_moe_entry_points_reject_bad_arguments():
+    from kb_nano_amd._lib import lib
+    L = lib()
+    p = ctypes.c_void_p(4096)   # never dereferenced: validation fails first
+    # moe_align_block_size: 100 pairs, 16 experts, blocks of 64 need 100 + 16*63 slots
+    assert L.kbn_moe_align_block_size(p, 4, 100, 16, 64, p, 1000, p, 100, p, None, p, 1 << 20, None) == 1
+    assert "sorted_token_ids holds 1000" in _err()
+    assert L.kbn_moe_align_block_size(p, 4, 100, 16, 64, p, 1108, p, 10, p, None, p, 1 << 20, None) == 1
+    assert "expert_ids holds 10" in _err()
+    assert L.kbn_moe_align_block_size(p, 2, 100, 16, 64, p, 1108, p, 18, p, None, p, 1 << 20, None) == 1
+    assert "ids_bytes" in _err()
+    assert L.kbn_moe_align_block_size(p, 4, 100, 16, 64, p, 1108, p, 18, p, None, p, 16, None) == 1
+    assert "workspace" in _err()
+    # fused MoE GEMM
+    args = dict(lda=256, rows=8, N=512, K=256, E=4, block=64, nv=16, topk=2)
+
+    def gemm(**kw):
+        a = {**args, **kw}
+        return L.kbn_fp8_fused_moe_gemm(p, a["lda"], a["rows"], p, 2, 1, p, p, p, a["N"], p, p, p, 1024,
+                                        a["block"], a["nv"], a["topk"], None, a["N"], a["K"], a["E"],
+                                        a.get("ws"), a.get("ws_bytes", 0), None)
+    assert gemm(K=200, lda=208) == 1 and "multiple of 128" in _err()
+    assert gemm(block=32) == 1 and "multiple of 64" in _err()
+    assert gemm(rows=4) == 1 and "A rows" in _err()
+    assert gemm(lda=250) == 1 and "16-byte" in _err()
+    assert L.kbn_fp8_fused_moe_gemm_workspace_bytes(1024, 256) == 1024 * 2 * 4
+    assert gemm(ws=p, ws_bytes=100) == 1 and "workspace" in _err()
+    # moe_sum
+    assert L.kbn_moe_sum(p, 4, 0, 128, 128, p, 128, None) == 1 and "top_k" in _err()
+    assert L.kbn_moe_sum(p, 4, 2, 128, 100, p, 128, None) == 1 and "strides" in _err()
+    assert L.kbn_moe_sum(None, 0, 2, 128, 128, None, 128, None) == 0
+
+
+def test_sorted_moe_surface_matches_reference():
+    """Argument names and order of the sorted-token modules
+    (tasks/baseline/L1/moe_align.py:71-77, moe_sum.py:25-29,
+    moe_grouped_gemm.py:308-324, tasks/baseline/L2/vllm_fused_experts.py:116-127)."""
+    import importlib.util
+    import inspect
+
+    from kb_nano_amd import MoeAlign, MoeGroupedGemm, MoeSum, VllmFusedExperts
+    assert list(inspect.signature(MoeAlign.forward).parameters) == ["self", "topk_ids", "block_size",
+                                                                    "num_experts", "naive"]
+    assert list(inspect.signature(MoeSum.forward).parameters) == ["self", "input", "topk"]
+    assert list(inspect.signature(MoeGroupedGemm.forward).parameters) == [
+        "self", "A", "B", "C", "topk_weights", "sorted_token_ids", "expert_ids", "num_tokens_post_padded",
+        "mul_routed_weight", "top_k", "config", "a_scale", "b_scale", "use_fp8_w8a8", "block_shape"]
+    assert list(inspect.signature(VllmFusedExperts.forward).parameters) == [
+        "self", "hidden_states", "w13", "w2", "topk_weights", "topk_ids", "num_experts", "w13_scale", "w2_scale",
+        "block_shape"]
+    for fname, cls in [("moe_align", "MoeAlign"), ("moe_sum", "MoeSum"), ("moe_grouped_gemm", "MoeGroupedGemm")]:
+        path = os.path.join(ROOT, "kb_nano_amd", "candidate", "L1", fname + ".py")
+        spec = importlib.util.spec_from_file_location(f"_cand_{fname}", path)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        assert isinstance(getattr(mod, cls), type)
+
+
+def test_sorted_moe_config_block_sizes():
+    from kb_nano_amd.moe_grouped_gemm import MoeGroupedGemm, get_triton_config
+    assert get_triton_config(4, (256, 4096, 7168), (256, 7168, 2048), 8, True, [128, 128])["BLOCK_SIZE_M"] == 64
+    assert get_triton_config(4096, (256, 4096, 7168), (256, 7168, 2048), 8, True, [128, 128])["BLOCK_SIZE_M"] == 128
+    with pytest.raises(NotImplementedError):
+        MoeGroupedGemm()(torch.zeros(4, 256), torch.zeros(2, 256, 256), torch.zeros(8, 256), None, None,
+                         torch.zeros(8, dtype=torch.int32), torch.zeros(1, dtype=torch.int32), False, 2)

@@ -639,3 +639,96 @@ def test_block_requant_identity_on_pow2_checkpoint():
     # a non power-of-two scale moves the codes: x * (1/sf) is then inexact
     q3, s3 = oracle.block_requant(q, s * np.float32(1.3), use_ue8m0=True)
     assert not np.array_equal(q3, q) and np.array_equal(s3, s * 2)
+
+
+# ------------------------------------------------------- sorted-token MoE
+
+@pytest.mark.parametrize("M,k,E,block", [(37, 8, 16, 4), (5, 2, 64, 16), (300, 8, 256, 64), (3, 1, 8, 128),
+                                         (64, 6, 33, 32)])
+def test_moe_align_oracle_layout(M, k, E, block):
+    """Each expert's slots hold exactly its pairs (brute force over the flat
+    ids), segments are padded to the block size, the rest of the reference's
+    buffer is the sentinel numel, and block owners follow the segments."""
+    rng = np.random.default_rng(M * 7 + E)
+    ids = rng.integers(0, E, size=(M, k))
+    if M > 10:
+        ids[3, 0] = -1                       # invalid ids are not placed
+        ids[4, 0] = E
+    sorted_ids, expert_ids, total, cumsum = oracle.moe_align_block_size(ids, E, block)
+    flat = ids.reshape(-1)
+    numel = flat.size
+    bound = numel * block if numel < E else numel + E * (block - 1)
+    assert sorted_ids.size == bound and total <= bound and total % block == 0
+    assert cumsum[0] == 0 and cumsum[-1] == total
+    placed = np.zeros(bound, dtype=bool)
+    for e in range(E):
+        mine = np.flatnonzero(flat == e)
+        seg = sorted_ids[cumsum[e]:cumsum[e + 1]]
+        assert cumsum[e + 1] - cumsum[e] == -(-mine.size // block) * block
+        assert np.array_equal(seg[:mine.size], mine)
+        assert np.all(seg[mine.size:] == numel)
+        placed[cumsum[e]:cumsum[e] + mine.size] = True
+        assert np.all(expert_ids[cumsum[e] // block:cumsum[e + 1] // block] == e)
+    assert np.all(sorted_ids[~placed] == numel)
+    assert expert_ids.size == total // block
+
+
+def test_moe_sum_oracle_orders():
+    """Inputs with exact fp32 sums that tell the orders apart: three slots
+    where per-add bf16 rounding loses what a single rounding keeps (the
+    reference kernel's bf16 accumulator for top_k <= 4), and eight slots
+    where round-robin accumulators cancel 2^24 before adding the ones (the
+    order of at::sum_out) while a left-to-right fp32 sum absorbs them."""
+    def bits(rows):
+        return oracle.f32_to_bf16_bits(np.array(rows, dtype=np.float32)[None, :, None])
+    one_ulp_half = 2.0 ** -8
+    got = oracle.bf16_bits_to_f32(oracle.moe_sum(bits([1.0, one_ulp_half, one_ulp_half])))[0, 0]
+    assert got == 1.0                                  # single rounding would give 1 + 2^-7
+    got2 = oracle.bf16_bits_to_f32(oracle.moe_sum(bits([1.0, one_ulp_half])))[0, 0]
+    assert got2 == 1.0
+    v = [2.0 ** 24, 1.0, 1.0, 0.0, -(2.0 ** 24), 0.0, 0.0, 0.0]
+    assert oracle.bf16_bits_to_f32(oracle.moe_sum(bits(v)))[0, 0] == 2.0   # left to right would give 0
+    v9 = v + [3.0]
+    assert oracle.bf16_bits_to_f32(oracle.moe_sum(bits(v9)))[0, 0] == 5.0
+    # one slot is the identity; random rows stay within one bf16 rounding of float64
+    x = oracle.f32_to_bf16_bits(np.random.default_rng(2).standard_normal((4, 1, 64)).astype(np.float32))
+    assert np.array_equal(oracle.moe_sum(x), x[:, 0])
+    xr = np.random.default_rng(3).standard_normal((16, 8, 256)).astype(np.float32)
+    xb = oracle.f32_to_bf16_bits(xr)
+    ref = oracle.bf16_bits_to_f32(xb).astype(np.float64).sum(1)
+    got = oracle.bf16_bits_to_f32(oracle.moe_sum(xb)).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-6)
+
+
+def test_fused_moe_gemm_oracle_bruteforce():
+    """Tiny sorted-token GEMM in float64 from the decoded operands, with
+    routed weights, an invalid pair and the naive one-pair blocks."""
+    rng = np.random.default_rng(11)
+    M, k, E, N, K, block = 5, 2, 3, 130, 256, 4
+    ids = rng.integers(0, E, size=(M, k))
+    ids[2, 1] = -1
+    A = _rand_fp8((M, K), rng, 6)
+    sA = (2.0 ** rng.integers(-4, 4, (M, K // 128))).astype(np.float32) * np.float32(1.25)
+    B = _rand_fp8((E, N, K), rng, 6)
+    sB = (2.0 ** rng.integers(-4, 4, (E, 2, K // 128))).astype(np.float32) * np.float32(0.75)
+    w = rng.uniform(0.1, 1.0, (M, k)).astype(np.float32)
+    sorted_ids, expert_ids, total, _ = oracle.moe_align_block_size(ids, E, block)
+    got = oracle.fused_moe_gemm_sample(A, sA, B, sB, sorted_ids, expert_ids, total, block, M * k, k, w)
+    a = oracle.e4m3_decode(A).astype(np.float64)
+    b = oracle.e4m3_decode(B).astype(np.float64)
+    flat = ids.reshape(-1)
+    assert sorted(got) == [t for t in range(M * k) if flat[t] >= 0]
+    for t, row in got.items():
+        e, m = flat[t], t // k
+        ref = np.zeros(N)
+        for kb in range(K // 128):
+            ks = slice(kb * 128, kb * 128 + 128)
+            ref += sA[m, kb] * np.repeat(sB[e, :, kb], 128)[:N] * (b[e][:, ks] @ a[m, ks])
+        assert np.allclose(row, ref * w.reshape(-1)[t], rtol=1e-12, atol=1e-12)
+    # naive: block b holds pair b alone, expert ids are the flat routing
+    flat_ok = np.where(flat >= 0, flat, 0).astype(np.int32)
+    nv = oracle.fused_moe_gemm_sample(A, sA, B, sB, None, flat_ok, M * k * block, block, M * k, k, None,
+                                      naive=True)
+    assert sorted(nv) == list(range(M * k))
+    t = 3
+    assert np.allclose(nv[t], got[t] / w.reshape(-1)[t], rtol=1e-12)
