@@ -39,7 +39,6 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit dword format (gfx9 family)
 
 // FP32 scale contract: s = 2^(byte - 127) * mant with byte the biased
 // exponent field (the block-scaled MFMA's E8M0 operand, exact) and mant the
@@ -127,7 +126,6 @@ __device__ __forceinline__ void wait_dma_n() {
 }
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-constexpr int kOob = (int)0x80000000;  // offset beyond any range: reads zero
 
 // LDS row layout.  A stage holds one 128-K scale block per row (128 B =
 // eight 16-B chunks); chunk c of row r lives in slot c ^ swz(r).  A

@@ -51,6 +51,8 @@ inline int cu_count() {
 // ------------------------------------------------------------ constants ---
 
 constexpr int kGroup = 128;          // 1x128 activation groups, 128x128 weight blocks
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer descriptor word 3: 32-bit dword format (gfx9 family)
+constexpr int kOob = (int)0x80000000;         // buffer offset beyond any range: loads read zero, stores are dropped
 constexpr float kFp8Max = 448.0f;    // float8_e4m3fn max finite
 
 // ------------------------------------------------------- device helpers ---
@@ -73,6 +75,20 @@ __device__ __forceinline__ float ue8m0_ceil(float r) {
     uint32_t e = (u >> 23) & 0xFFu;
     if (u & 0x7FFFFFu) e += 1;
     return __uint_as_float(e << 23);
+}
+
+// ue8m0_ceil(amax / 448) without the division.  With amax = m 2^e, m in
+// [1, 2): for m <= 1.75 the quotient m/1.75 2^(e-8) lies in (2^(e-9), 2^(e-8)]
+// (rounding can at most reach 2^(e-8)), for m > 1.75 in (2^(e-8), 2^(e-7)) (it
+// exceeds 2^(e-8) by at least 2^-23/1.75 relative, more than half an ulp), so
+// the power of two is 2^(e-8) or 2^(e-7) by a compare of the mantissa with
+// 1.75's (0x600000).  Zero, subnormal, tiny (result not normal), infinite and
+// NaN amax take the division.
+__device__ __forceinline__ float ue8m0_ceil_div448(float amax) {
+    const uint32_t u = __float_as_uint(amax);
+    const uint32_t e = (u >> 23) & 0xFFu;
+    if (e <= 9u || e == 255u) return ue8m0_ceil(amax / kFp8Max);
+    return __uint_as_float((e - 8u + ((u & 0x7FFFFFu) > 0x600000u ? 1u : 0u)) << 23);
 }
 
 // Biased exponent byte (E8M0) of ue8m0_ceil(r): the per-operand scale

@@ -8,25 +8,31 @@
 //   per 1x128 group: s = ceil_pow2(max(max|v|, 1e-10) / 448); q = e4m3(v / s)
 //   fused add also writes x <- bf16(v).
 //
-// One wavefront per token at a time, four per workgroup; each wavefront walks
-// tokens with a grid stride and, for rows up to 8192 (plain) or 4096 (fused)
-// columns, loads the next token's row before normalizing the current one, so
-// reads overlap stores.  The weight vector is staged in LDS once per
-// workgroup.  Lane l owns the 16-byte chunks at c*512 + 8l (c = 0 .. kC-1):
-// the whole row stays in registers between the sum of squares and the
-// normalize+quant pass, so HBM sees one read of the row and one write of the
-// codes.  A 1x128 group is 16 lanes of
-// one chunk (lanes 16j .. 16j+15), so its absmax is the same 4-step DPP max as
-// the standalone quant kernel.  The sum of squares is fmaf in chunk then
-// element order per lane, then an xor butterfly over the 64 lanes (every lane
-// ends with the same value); inv uses the correctly rounded sqrt and divide.
+// One workgroup of W wavefronts per token at a time (W = 8 for rows of 4096
+// or more columns, else 4).  Chunk c of a row is the 512 elements c*512 ..
+// c*512+511 (16 bytes per lane); wavefront w owns chunks c = W*i + w, keeps
+// their weights in registers as fp32 for all its tokens, and requests the
+// chunks of the token after next as soon as the current ones have been
+// summed, so two tokens' reads overlap the normalize, quant and stores.  HBM sees one read of each row and one write
+// of the codes.  A 1x128 group is 16 lanes of one chunk, so its absmax is the
+// 4-step DPP max of the standalone quant kernel.  Sum of squares: each lane
+// applies fmaf over its chunks (increasing c) and their 8 elements, an xor
+// butterfly sums the wavefront's 64 lanes, and the W wavefront sums meet in
+// LDS, added in wavefront order (((P0 + P1) + P2) + ...); inv uses the
+// correctly rounded sqrt and divide.  When the row's sum of squares is finite and the wavefront's
+// weights are finite and below 2^100, every normalized value is finite and
+// |v / s| <= 448 (1 + 2^-23)^2, where the hardware conversion already gives
+// the clamped code, so the clamp is skipped; other rows take it.
 #include "kbn_common.h"
+
+#include <algorithm>
+#include <type_traits>
 
 namespace kbn {
 namespace {
 
-constexpr int kNormWaves = 4;
-constexpr float kGroupEps = 1e-10f;   // absmax floor of the scale (rmsnorm_quant.cu:75)
+constexpr int kNormMaxWgPerCu = 8;     // bound on the resident workgroups per CU the grid is sized for
+constexpr float kGroupEps = 1e-10f;    // absmax floor of the scale (rmsnorm_quant.cu:75)
 
 struct NormArgs {
     uint16_t* x;          // [M, H] bf16, row stride ld_x (fused add: overwritten with bf16(v))
@@ -38,6 +44,7 @@ struct NormArgs {
     int64_t ld_q;
     float* s;             // scale (m, g) at s[m * s_m + g * s_g]
     int64_t s_m, s_g;
+    int s_bytes;          // bytes the scale view spans from s
     int M, H;
     float eps;
 };
@@ -47,32 +54,30 @@ __device__ __forceinline__ float bf16_at(const u32x4& v, int j) {
     return (j & 1) ? bf16hi(word) : bf16lo(word);
 }
 
-// Row registers of one token: x (and, fused add, the residual) as 16-byte
-// chunks c*512 + 8*lane.
-template <int kC, bool kAdd>
+// This wavefront's chunks of one token: x (and, fused add, the residual).
+template <int kCW, bool kAdd>
 struct NormRow {
-    u32x4 x[kC];
-    u32x4 r[kAdd ? kC : 1];
+    u32x4 x[kCW];
+    u32x4 r[kAdd ? kCW : 1];
 };
 
-template <int kC, bool kAdd>
-__device__ __forceinline__ void load_row(const NormArgs& a, int m, int lane, NormRow<kC, kAdd>& row) {
-    const uint16_t* xr = a.x + (int64_t)m * a.ld_x;
-    const uint16_t* rr = kAdd ? a.r + (int64_t)m * a.ld_r : nullptr;
+// Row descriptor: `bytes` bytes from p; buffer accesses past them read zero
+// or are dropped, so no access is branched around and every token issues the
+// same memory instructions (which keeps the compiler's counter waits exact).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, (int)kRsrcWord3);
+}
+
+template <int kW, int kCW, bool kAdd>
+__device__ __forceinline__ void load_row(const NormArgs& a, int m, int wave, int lane, NormRow<kCW, kAdd>& row,
+                                         int dep = 0) {
+    const __amdgpu_buffer_rsrc_t xr = row_rsrc(a.x + (int64_t)m * a.ld_x, 2 * a.H);
+    const __amdgpu_buffer_rsrc_t rr = row_rsrc(kAdd ? a.r + (int64_t)m * a.ld_r : a.x, kAdd ? 2 * a.H : 0);
 #pragma unroll
-    for (int c = 0; c < kC; ++c) {
-        const int e0 = c * 512 + 8 * lane;
-        if ((c + 1) * 512 <= a.H) {   // uniform: the whole chunk is in the row
-            row.x[c] = *reinterpret_cast<const u32x4*>(xr + e0);
-            if constexpr (kAdd) row.r[c] = *reinterpret_cast<const u32x4*>(rr + e0);
-        } else {
-            row.x[c] = u32x4{0u, 0u, 0u, 0u};
-            if (e0 < a.H) row.x[c] = *reinterpret_cast<const u32x4*>(xr + e0);
-            if constexpr (kAdd) {
-                row.r[c] = u32x4{0u, 0u, 0u, 0u};
-                if (e0 < a.H) row.r[c] = *reinterpret_cast<const u32x4*>(rr + e0);
-            }
-        }
+    for (int i = 0; i < kCW; ++i) {
+        const int off = 2 * ((kW * i + wave) * 512 + 8 * lane) + dep;   // lanes past the row read zeros
+        row.x[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+        if constexpr (kAdd) row.r[i] = __builtin_amdgcn_raw_buffer_load_b128(rr, off, 0, 0);
     }
 }
 
@@ -81,147 +86,207 @@ __device__ __forceinline__ void load_row(const NormArgs& a, int m, int lane, Nor
 // semantics (NaN -> -448).
 __device__ __forceinline__ float clamp448(float v) { return __builtin_amdgcn_fmed3f(v, -kFp8Max, kFp8Max); }
 
-// Normalize and quantize one token whose row is in registers; `wl` is the
-// weight vector in LDS, chunk-major like the row.
-template <int kC, bool kAdd>
-__device__ __forceinline__ void norm_row(const NormArgs& a, int m, int lane, NormRow<kC, kAdd>& row,
-                                         const u32x4* wl) {
+// Normalize and quantize one token.  `wf` holds this wavefront's weights,
+// `part` the LDS slots of the W wavefront sums (double-buffered by token
+// parity, so one barrier per token suffices), `wok` whether this wavefront's
+// weights allow skipping the clamp.
+template <int kW, int kCW, bool kAdd, typename Prefetch>
+__device__ __forceinline__ void norm_row(const NormArgs& a, int m, int wave, int lane, NormRow<kCW, kAdd>& row,
+                                         const float (&wf)[kCW][8], float* part, bool wok, Prefetch prefetch) {
 #pragma clang fp contract(off)
-    uint16_t* xr = a.x + (int64_t)m * a.ld_x;
+    const __amdgpu_buffer_rsrc_t xw = row_rsrc(a.x + (int64_t)m * a.ld_x, kAdd ? 2 * a.H : 0);
+    const __amdgpu_buffer_rsrc_t rw = row_rsrc(kAdd ? a.r + (int64_t)m * a.ld_r : a.x, kAdd ? 2 * a.H : 0);
+    const __amdgpu_buffer_rsrc_t qw = row_rsrc(a.q + (int64_t)m * a.ld_q, a.H);
+    const __amdgpu_buffer_rsrc_t sw = row_rsrc(a.s, a.s_bytes);
     // ---- sum of squares (fused add: of the unrounded sums, whose bf16
-    // roundings replace the residual and are what gets normalized)
+    // roundings replace the residual and are what gets normalized); chunks
+    // past the row hold zeros and add nothing
     float p = 0.f;
+    float base[kCW][8];   // the values to normalize, fp32 (fused add: the bf16-rounded sums)
 #pragma unroll
-    for (int c = 0; c < kC; ++c) {
-        const int e0 = c * 512 + 8 * lane;
-        if (e0 >= a.H) continue;
+    for (int i = 0; i < kCW; ++i) {
+        const int c = kW * i + wave;
         u32x4 nr = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            float av = bf16_at(row.x[c], j);
+            float av = bf16_at(row.x[i], j);
+            base[i][j] = av;
             if constexpr (kAdd) {
-                av = bf16_at(row.r[c], j) + av;
-                nr[j >> 1] |= f32_to_bf16_rne(av) << (16 * (j & 1));
+                av = bf16_at(row.r[i], j) + av;
+                const uint32_t h = f32_to_bf16_rne(av);
+                nr[j >> 1] |= h << (16 * (j & 1));
+                base[i][j] = __uint_as_float(h << 16);
             }
             p = fmaf(av, av, p);
         }
-        if constexpr (kAdd) {
-            row.r[c] = nr;
-            *reinterpret_cast<u32x4*>(a.r + (int64_t)m * a.ld_r + e0) = nr;
-        }
+        if constexpr (kAdd) __builtin_amdgcn_raw_buffer_store_b128(nr, rw, 2 * (c * 512 + 8 * lane), 0, 0);
     }
+    // the next token's loads go out only now that this token's data has
+    // arrived, so waiting for it never waits for them: their offsets depend
+    // on p through an opaque zero, which no code motion can hoist above p
+    int dep;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(dep) : "v"(p));
+    prefetch(dep);
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) p = p + __shfl_xor(p, d, 64);
+    if (lane == 0) part[wave] = p;
+    __syncthreads();
+    p = part[0];
+#pragma unroll
+    for (int w = 1; w < kW; ++w) p = p + part[w];
     const float inv = 1.0f / sqrtf(p / (float)a.H + a.eps);
+    const bool noclamp = wok && p < __builtin_inff();   // uniform per wavefront
 
-    // ---- normalize and quantize, one chunk (4 groups per wavefront) at a time
+    // ---- normalize and quantize, one chunk (4 groups per wavefront) at a time;
+    // the clamped and unclamped passes are separate code (a row-level branch,
+    // not a per-value select) that only compute; the stores follow the branch,
+    // so every path issues the same memory instructions
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 codes[kCW];
+    float scl[kCW];
+    float vout[kAdd ? kCW : 1][8];
+    auto quant_pass = [&](auto clamp_tag) {
+        constexpr bool kClamp = decltype(clamp_tag)::value;
 #pragma unroll
-    for (int c = 0; c < kC; ++c) {
-        const int e0 = c * 512 + 8 * lane;
-        if (c * 512 >= a.H) break;   // uniform: no lane of this chunk is in the row
-        const bool full = (c + 1) * 512 <= a.H;   // uniform
-        const bool live = full || e0 < a.H;
-        const u32x4 wv = wl[c * 64 + lane];
-        const u32x4& base = kAdd ? row.r[c] : row.x[c];
-        float v[8];
-        float amax = 0.f;
+        for (int i = 0; i < kCW; ++i) {
+            float v[8];
+            float amax = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            // lanes past the row hold zeros (loads and weights), so v = 0 there
-            v[j] = (bf16_at(base, j) * inv) * bf16_at(wv, j);
-            amax = fmaxf(amax, fabsf(v[j]));
-        }
-        amax = __uint_as_float(row16_max_u32(__float_as_uint(amax)));
-        amax = fmaxf(amax, kGroupEps);
-        const float sc = ue8m0_ceil(amax / kFp8Max);
-        const float is = pow2_recip(sc);
-        if (live) {
-            const uint32_t lo = pack4_e4m3(clamp448(v[0] * is), clamp448(v[1] * is), clamp448(v[2] * is),
-                                           clamp448(v[3] * is));
-            const uint32_t hi = pack4_e4m3(clamp448(v[4] * is), clamp448(v[5] * is), clamp448(v[6] * is),
-                                           clamp448(v[7] * is));
-            *reinterpret_cast<uint2*>(a.q + (int64_t)m * a.ld_q + e0) = make_uint2(lo, hi);
-            if ((lane & 15) == 0) a.s[(int64_t)m * a.s_m + (int64_t)(e0 >> 7) * a.s_g] = sc;
-            if constexpr (kAdd) {
-                u32x4 o;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) o[k] = f32_to_bf16_rne(v[2 * k]) | (f32_to_bf16_rne(v[2 * k + 1]) << 16);
-                *reinterpret_cast<u32x4*>(xr + e0) = o;
+            for (int j = 0; j < 8; ++j) {
+                // lanes past the row hold zeros (loads and weights), so v = 0 there
+                v[j] = (base[i][j] * inv) * wf[i][j];
+                amax = fmaxf(amax, fabsf(v[j]));
+                if constexpr (kAdd) vout[i][j] = v[j];
             }
+            amax = __uint_as_float(row16_max_u32(__float_as_uint(amax)));
+            amax = fmaxf(amax, kGroupEps);
+            const float sc = ue8m0_ceil_div448(amax);
+            const float is = pow2_recip(sc);
+            float t[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) t[j] = kClamp ? clamp448(v[j] * is) : v[j] * is;
+            codes[i] = u32x2{pack4_e4m3(t[0], t[1], t[2], t[3]), pack4_e4m3(t[4], t[5], t[6], t[7])};
+            scl[i] = sc;
+        }
+    };
+    if (noclamp) quant_pass(std::false_type{});
+    else quant_pass(std::true_type{});
+#pragma unroll
+    for (int i = 0; i < kCW; ++i) {
+        const int e0 = (kW * i + wave) * 512 + 8 * lane;
+        // past the row: dropped by the descriptor ranges
+        __builtin_amdgcn_raw_buffer_store_b64(codes[i], qw, e0, 0, 0);
+        const bool owner = (lane & 15) == 0 && e0 < a.H;
+        __builtin_amdgcn_raw_buffer_store_b32(
+            __float_as_uint(scl[i]), sw, owner ? (int)(4 * ((int64_t)m * a.s_m + (int64_t)(e0 >> 7) * a.s_g)) : kOob,
+            0, 0);
+        if constexpr (kAdd) {
+            u32x4 o;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                o[k] = f32_to_bf16_rne(vout[i][2 * k]) | (f32_to_bf16_rne(vout[i][2 * k + 1]) << 16);
+            __builtin_amdgcn_raw_buffer_store_b128(o, xw, 2 * e0, 0, 0);
         }
     }
 }
 
 // Token placement.  Consecutive workgroup ids are dispatched round-robin over
 // the 8 XCDs; each XCD instead gets a contiguous range of workgroup slots, and
-// slot s owns tokens [s * 4T, (s + 1) * 4T) (T = tokens per wavefront),
-// wavefront w of it tokens s*4T + w, + 4, + 8, ...  So the 32 tokens that
-// share a 128-byte line of the column-major scales are written from one XCD
-// and the line merges in its L2.  With kPrefetch, the next token's row is
-// loaded before the current one is normalized, so its reads overlap the
-// current stores.
-template <int kC, bool kAdd, bool kPrefetch>
-__global__ __launch_bounds__(64 * kNormWaves) void rmsnorm_quant_kernel(const NormArgs a, int tpw) {
-    __shared__ u32x4 wl[kC * 64];
-    for (int i = threadIdx.x; i < kC * 64; i += 64 * kNormWaves) {
-        const int e0 = (i >> 6) * 512 + 8 * (i & 63);
-        wl[i] = e0 < a.H ? *reinterpret_cast<const u32x4*>(a.w + e0) : u32x4{0u, 0u, 0u, 0u};
-    }
-    __syncthreads();
+// slot s owns tokens [s * T, (s + 1) * T) (T tokens per workgroup), so the 32
+// tokens that share a 128-byte line of the column-major scales are written
+// from one XCD and the line merges in its L2.
+template <int kW, int kCW, bool kAdd>
+__global__ __launch_bounds__(64 * kW) void rmsnorm_quant_kernel(const NormArgs a, int tpw) {
+    __shared__ float part[2][kW];
     const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // this wavefront's weights, fp32; lanes past the row hold zeros
+    float wf[kCW][8];
+    bool wok = true;
+#pragma unroll
+    for (int i = 0; i < kCW; ++i) {
+        const int e0 = (kW * i + wave) * 512 + 8 * lane;
+        u32x4 wv = u32x4{0u, 0u, 0u, 0u};
+        if (e0 < a.H) wv = *reinterpret_cast<const u32x4*>(a.w + e0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            wf[i][j] = bf16_at(wv, j);
+            wok = wok && fabsf(wf[i][j]) <= 0x1p100f;   // false for NaN and infinities
+        }
+    }
+    wok = __all(wok);
     const int nblk = gridDim.x, bid = blockIdx.x;
     const int xcd = bid & 7, per = nblk >> 3, rem = nblk & 7;
     const int slot = xcd * per + (xcd < rem ? xcd : rem) + (bid >> 3);
-    const int first = slot * kNormWaves * tpw + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int last = min(a.M, (slot + 1) * kNormWaves * tpw);   // exclusive
-    int m = first;
-    if (m >= last) return;
-    if constexpr (kPrefetch) {
-        NormRow<kC, kAdd> cur, nxt;
-        load_row<kC, kAdd>(a, m, lane, cur);
-        for (;;) {
-            const int mn = m + kNormWaves;
-            if (mn < last) load_row<kC, kAdd>(a, mn, lane, nxt);
-            norm_row<kC, kAdd>(a, m, lane, cur, wl);
-            if (mn >= last) break;
-            m = mn;
-            const int mm = m + kNormWaves;
-            if (mm < last) load_row<kC, kAdd>(a, mm, lane, cur);
-            norm_row<kC, kAdd>(a, m, lane, nxt, wl);
-            if (mm >= last) break;
-            m = mm;
-        }
-    } else {
-        for (; m < last; m += kNormWaves) {
-            NormRow<kC, kAdd> cur;
-            load_row<kC, kAdd>(a, m, lane, cur);
-            norm_row<kC, kAdd>(a, m, lane, cur, wl);
-        }
+    int m = slot * tpw;
+    const int last = min(a.M, (slot + 1) * tpw);   // exclusive
+    if (m >= last) return;                         // uniform over the workgroup
+    // ring of three rows: token m + 2 is requested while token m is
+    // normalized
+    NormRow<kCW, kAdd> b0, b1, b2;
+    load_row<kW, kCW, kAdd>(a, m, wave, lane, b0);
+    if (m + 1 < last) load_row<kW, kCW, kAdd>(a, m + 1, wave, lane, b1);
+    // as many stores as a token issues, all dropped (zero-length range): the
+    // loop is entered with memory instructions in flight after the row loads
+    // as on its back edge, so the compiler's wait for the first token lets the
+    // previous token's stores stay in flight
+    {
+        const __amdgpu_buffer_rsrc_t none = row_rsrc(a.q, 0);
+#pragma unroll
+        for (int k = 0; k < kCW * (kAdd ? 4 : 2); ++k)   // distinct offsets, so none is merged away
+            __builtin_amdgcn_raw_buffer_store_b32((uint32_t)k, none, kOob + 4 * k, 0, 0);
+    }
+    for (;;) {
+        norm_row<kW, kCW, kAdd>(a, m, wave, lane, b0, wf, part[m & 1], wok, [&](int dep) {
+            if (m + 2 < last) load_row<kW, kCW, kAdd>(a, m + 2, wave, lane, b2, dep);
+        });
+        if (++m >= last) break;
+        norm_row<kW, kCW, kAdd>(a, m, wave, lane, b1, wf, part[m & 1], wok, [&](int dep) {
+            if (m + 2 < last) load_row<kW, kCW, kAdd>(a, m + 2, wave, lane, b0, dep);
+        });
+        if (++m >= last) break;
+        norm_row<kW, kCW, kAdd>(a, m, wave, lane, b2, wf, part[m & 1], wok, [&](int dep) {
+            if (m + 2 < last) load_row<kW, kCW, kAdd>(a, m + 2, wave, lane, b1, dep);
+        });
+        if (++m >= last) break;
     }
 }
 
-// Wavefronts in the grid: one token each up to two per SIMD; beyond that two
-// per SIMD, each walking several tokens with the prefetch.
-int norm_waves(int M) {
-    const int cap = cu_count() * 8;
-    return M <= cap ? M : cap;
+// Workgroups of one instantiation resident per CU (from its register use),
+// queried once per process.
+template <int kW, int kCW, bool kAdd>
+int norm_occupancy() {
+    static int occ = 0;
+    if (occ == 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, rmsnorm_quant_kernel<kW, kCW, kAdd>, 64 * kW, 0) !=
+                hipSuccess || n <= 0)
+            n = 1;
+        occ = std::min(n, kNormMaxWgPerCu);
+    }
+    return occ;
 }
 
+// One wave of resident workgroups, each walking an equal share of the tokens.
+template <int kW, int kCW, bool kAdd>
+void launch_norm_cfg(const NormArgs& a, hipStream_t st) {
+    const int64_t cap = (int64_t)cu_count() * norm_occupancy<kW, kCW, kAdd>();
+    const int wgs = (int)std::min<int64_t>(a.M, cap);
+    const int tpw = (a.M + wgs - 1) / wgs;                    // tokens per workgroup
+    const int blocks = (a.M + tpw - 1) / tpw;                 // every slot owns >= 1 token
+    rmsnorm_quant_kernel<kW, kCW, kAdd><<<dim3((unsigned)blocks), dim3(64 * kW), 0, st>>>(a, tpw);
+}
+
+// Wavefronts per token: 8 from 8 chunks (4096 columns) up, else 4.
 template <bool kAdd>
 int launch_norm(const NormArgs& a, hipStream_t st) {
     const int chunks = (a.H + 511) / 512;
-    const int waves = norm_waves(a.M);
-    const int tpw = (a.M + waves - 1) / waves;                            // tokens per wavefront
-    const int blocks = (a.M + kNormWaves * tpw - 1) / (kNormWaves * tpw);  // every slot owns >= 1 token
-    const dim3 grid((unsigned)blocks), block(64 * kNormWaves);
-    if (chunks <= 2) rmsnorm_quant_kernel<2, kAdd, true><<<grid, block, 0, st>>>(a, tpw);
-    else if (chunks <= 4) rmsnorm_quant_kernel<4, kAdd, true><<<grid, block, 0, st>>>(a, tpw);
-    else if (chunks <= 8) rmsnorm_quant_kernel<8, kAdd, true><<<grid, block, 0, st>>>(a, tpw);
-    else if (chunks <= 16) rmsnorm_quant_kernel<16, kAdd, !kAdd><<<grid, block, 0, st>>>(a, tpw);
-    else {
-        if constexpr (kAdd) return 1;
-        else rmsnorm_quant_kernel<32, false, false><<<grid, block, 0, st>>>(a, tpw);
-    }
+    if (chunks <= 4) launch_norm_cfg<4, 1, kAdd>(a, st);
+    else if (chunks < 8) launch_norm_cfg<4, 2, kAdd>(a, st);
+    else if (chunks <= 8) launch_norm_cfg<8, 1, kAdd>(a, st);
+    else if (chunks <= 16) launch_norm_cfg<8, 2, kAdd>(a, st);
+    else if (chunks <= 32 && !kAdd) launch_norm_cfg<8, 4, false>(a, st);
+    else return 1;
     return 0;
 }
 
@@ -245,6 +310,7 @@ extern "C" int kbn_rmsnorm_fp8_quant(void* x_bf16, int64_t M, int64_t H, int64_t
                   "%s: input and weight must be 16-byte aligned, input row stride >= H and a multiple of 8", what);
     KBN_CHECK_ARG(ld_q >= H && ld_q % 8 == 0 && (reinterpret_cast<uintptr_t>(q_fp8) & 7u) == 0,
                   "%s: output rows must be 8-byte aligned with a stride >= H", what);
+    KBN_CHECK_ARG((reinterpret_cast<uintptr_t>(scale) & 3u) == 0, "%s: scales must be 4-byte aligned", what);
     if (add)
         KBN_CHECK_ARG(aligned16(residual_bf16) && ld_r >= H && ld_r % 8 == 0,
                       "%s: residual must be 16-byte aligned with a row stride >= H and a multiple of 8", what);
@@ -260,6 +326,9 @@ extern "C" int kbn_rmsnorm_fp8_quant(void* x_bf16, int64_t M, int64_t H, int64_t
     a.s = scale;
     a.s_m = s_stride_m;
     a.s_g = s_stride_g;
+    const int64_t s_bytes = ((M - 1) * s_stride_m + ((H + 127) / 128 - 1) * s_stride_g + 1) * 4;
+    KBN_CHECK_ARG(s_bytes < 0x7FFFFFFFLL, "%s: the scales span 2 GiB or more", what);
+    a.s_bytes = (int)s_bytes;
     a.M = (int)M;
     a.H = (int)H;
     a.eps = eps;

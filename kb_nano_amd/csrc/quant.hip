@@ -104,7 +104,7 @@ __device__ __forceinline__ float quant8_store(const float (&v)[8], float eps, in
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
     amax = __uint_as_float(row16_max_u32(__float_as_uint(amax)));
     amax = fmaxf(amax, eps);
-    float sc = amax / kFp8Max;
+    float sc = kUe8m0 ? ue8m0_ceil_div448(amax) : amax / kFp8Max;
     // The reference clamps v / sc to [-448, 448] before the cast.  Here that
     // clamp can never act on a finite value: sc >= fl(amax / 448), so
     // |v / sc| <= 448 (1 + 2^-23)^2 < 464, and the hardware conversion rounds
@@ -114,7 +114,6 @@ __device__ __forceinline__ float quant8_store(const float (&v)[8], float eps, in
     // (quant) of kernel time.
     uint32_t lo, hi;
     if (kUe8m0) {
-        sc = ue8m0_ceil(sc);
         const float inv = pow2_recip(sc);
         lo = pack4_e4m3(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
         hi = pack4_e4m3(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);

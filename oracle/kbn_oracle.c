@@ -308,11 +308,14 @@ int orc_grouped_gemm_nt_sample(const uint8_t* A, const float* sA, int64_t sA_sm,
  *   q = e4m3_rne(fminf(fmaxf(v / s, -448), 448)); fused: x <- bf16(v)
  * The reference sums in whatever order its thread layout gives and takes
  * rsqrtf; this restatement fixes the order the gfx950 kernel uses, so the
- * kernel can be checked bit for bit: 64 lanes, lane l owns the 8-element
- * chunks starting at c*512 + 8l (c = 0, 1, ...), accumulates a*a with fmaf in
- * chunk then element order, and the 64 partials are combined by the xor
- * butterfly p[l] + p[l ^ d] for d = 32, 16, ..., 1.  inv uses the correctly
- * rounded sqrt and divide.  r == NULL selects the plain variant.
+ * kernel can be checked bit for bit: W groups of 64 lanes (W = 8 when the row
+ * has at least 8 chunks of 512, i.e. H > 3584, else 4); lane l of group w
+ * owns the 8-element chunks starting at c*512 + 8l for c = w, w+W, w+2W, ...,
+ * accumulates a*a with fmaf in chunk then element order; each group's 64
+ * partials are combined by the xor butterfly p[l] + p[l ^ d] for d = 32, 16,
+ * ..., 1, and the group sums in group order, ((P0 + P1) + P2) + ... .  inv
+ * uses the correctly rounded sqrt and divide.  r == NULL selects the plain
+ * variant.
  * H % 8 == 0; scale (m, g) at s[m*s_m + g*s_g] for g < ceil(H/128). */
 int orc_rmsnorm_quant(uint16_t* x, int64_t M, int64_t H, int64_t ld_x, const uint16_t* w, uint16_t* r,
                       int64_t ld_r, uint8_t* q, int64_t ld_q, float* s, int64_t s_m, int64_t s_g, float eps) {
@@ -325,10 +328,13 @@ int orc_rmsnorm_quant(uint16_t* x, int64_t M, int64_t H, int64_t ld_x, const uin
         if (!base) { bad = 1; continue; }
         uint16_t* xr = x + m * ld_x;
         uint16_t* rr = r ? r + m * ld_r : NULL;
+        const int W = C >= 8 ? 8 : 4;
+        float P[8];
+        for (int wv = 0; wv < W; ++wv) {
         float part[64];
         for (int l = 0; l < 64; ++l) {
             float p = 0.0f;
-            for (int64_t c = 0; c < C; ++c) {
+            for (int64_t c = wv; c < C; c += W) {
                 const int64_t e0 = c * 512 + 8 * l;
                 if (e0 >= H) continue;
                 for (int j = 0; j < 8; ++j) {
@@ -352,7 +358,11 @@ int orc_rmsnorm_quant(uint16_t* x, int64_t M, int64_t H, int64_t ld_x, const uin
             for (int l = 0; l < 64; ++l) t[l] = part[l] + part[l ^ d];
             memcpy(part, t, sizeof(t));
         }
-        const float mean = part[0] / (float)H;
+        P[wv] = part[0];
+        }
+        float ptot = P[0];
+        for (int wv = 1; wv < W; ++wv) ptot = ptot + P[wv];
+        const float mean = ptot / (float)H;
         const float inv = 1.0f / sqrtf(mean + eps);
         for (int64_t g = 0; g < G; ++g) {
             const int64_t e1 = (g + 1) * 128 < H ? (g + 1) * 128 : H;

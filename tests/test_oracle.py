@@ -732,3 +732,22 @@ def test_fused_moe_gemm_oracle_bruteforce():
     assert sorted(nv) == list(range(M * k))
     t = 3
     assert np.allclose(nv[t], got[t] / w.reshape(-1)[t], rtol=1e-12)
+
+
+def test_ue8m0_scale_without_division_identity():
+    """The kernels' division-free UE8M0 scale (kbn_common.h ue8m0_ceil_div448):
+    for amax = m 2^e, ceil_pow2(fl(amax / 448)) is 2^(e-8) when m <= 1.75 and
+    2^(e-7) otherwise.  Checked against the definition (float32 division, then
+    the oracle's exponent rounding) for every mantissa at a spread of
+    exponents, including both sides of 1.75 and the edges of the range the
+    kernels use the formula for (biased exponent 10 .. 254)."""
+    mant = np.arange(1 << 23, dtype=np.uint32)
+    for e in (10, 11, 60, 100, 126, 127, 128, 160, 200, 253, 254):
+        u = (np.uint32(e) << np.uint32(23)) | mant
+        amax = u.view(np.float32)
+        ratio = (amax / np.float32(448.0)).astype(np.float32)
+        # definition: exponent bits of the quotient, plus one if its mantissa is not zero
+        ru = ratio.view(np.uint32)
+        want = ((ru >> 23) & 0xFF) + ((ru & 0x7FFFFF) != 0)
+        got = np.uint32(e) - 8 + (mant > 0x600000)
+        assert np.array_equal(got, want.astype(np.uint32)), e
