@@ -434,7 +434,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): this build covers the "
-              "single-GPU hot path; see DESIGN.md for how it would shard.", file=sys.stderr)
+              "single-GPU hot path (one GPU per box; the multi-GPU sharding is a design, not a measured run).",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
