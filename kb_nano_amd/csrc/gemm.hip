@@ -112,6 +112,13 @@ __device__ __forceinline__ void dma_b128(const v4i& desc, uint32_t lds, int voff
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(desc)
                  : "memory");
 }
+// The same load with the non-temporal hint: the weight rows of a tile are
+// read once per workgroup and should not push the activation rows (read by
+// every workgroup of a tile row) out of L2.
+__device__ __forceinline__ void dma_b128_nt(const v4i& desc, uint32_t lds, int voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(lds), "v"(voff), "s"(desc)
+                 : "memory");
+}
 __device__ __forceinline__ void dma_b32(const v4i& desc, uint32_t lds, int voff) {
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(desc)
                  : "memory");
@@ -286,6 +293,11 @@ gemm_bs_kernel(const GemmArgs a) {
     const int sw_kstep = sw_live ? 4 : 0;
     const int sw_off0 = sw_live ? (n0 / 128 + lane) * (int)a.sW_ld * 4 + kb0 * 4 : kOob;
     constexpr int kDma = kAInstr + kBInstr + 2;  // DMA instructions per wave per stage
+    // Weight rows stream past L2 (non-temporal) where the weights dominate the
+    // traffic: the 128-column dense tiles (chosen only for M <= 128) and the
+    // grouped and sorted MoE tiles.  The large dense tiles keep the default,
+    // which measures faster where A and W tiles are both re-read from L2.
+    constexpr bool kWeightNt = (BN == 128) || kGrouped || kSorted;
 
     // DMA instruction d (0 <= d < kDma) of K block s -> LDS buffer s % kStages:
     // the two scale vectors, then the A rows, then the W rows.  `live` false
@@ -306,8 +318,10 @@ gemm_bs_kernel(const GemmArgs a) {
             dma_b128(dA, base + (wave * kAInstr + i) * 1024, live ? off : kOob);
         } else {
             const int i = d - 2 - kAInstr;
-            dma_b128(dW, base + kA + (wave * kBInstr + i) * 1024,
-                     live ? ((i & 1) ? w_o : w_e) + (int)(i * 8 * a.ldw) + k0 : kOob);
+            const uint32_t dst = base + kA + (wave * kBInstr + i) * 1024;
+            const int off = live ? ((i & 1) ? w_o : w_e) + (int)(i * 8 * a.ldw) + k0 : kOob;
+            if constexpr (kWeightNt) dma_b128_nt(dW, dst, off);
+            else dma_b128(dW, dst, off);
         }
     };
 
