@@ -85,9 +85,12 @@ int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int64_t sA_stri
 /*
  * kbn_fp8_gemm_nt with a caller-provided workspace: shapes whose tile grid
  * would leave CUs idle (small M, or few N tiles) split K across workgroups,
- * write fp32 partial sums into `workspace` and reduce them in a second
- * launch on the same stream (in a fixed order, so results are deterministic
- * and equal for any split count up to fp32 summation order).
+ * write fp32 partial sums into `workspace` and sum them in a fixed order (so
+ * results are deterministic and equal for any split count up to fp32
+ * summation order): for M <= 16 the last workgroup of each tile does it in
+ * the same launch, using per-tile arrival counters the library keeps in a
+ * static device array per stream (or per stream capture); otherwise, or
+ * when those run out, a second launch on the same stream does it.
  * kbn_fp8_gemm_nt_workspace_bytes returns the bytes this needs for a shape on
  * the current device (0: no split, workspace unused).  A null or smaller
  * workspace runs the unsplit kernel.  The workspace must be 16-byte aligned

@@ -32,6 +32,9 @@
 #include "kbn_common.h"
 
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <tuple>
 
 namespace kbn {
 
@@ -76,6 +79,10 @@ struct GemmArgs {
     float* P;
     int64_t ws_bytes;            // bytes at P
     int splits, kb_per_split;
+    // Arrival counters of the split launch, one per tile (nullptr: a separate
+    // splitk_reduce_kernel launch sums the slabs).  Zero on entry; the last
+    // workgroup of a tile to finish sums the slabs and resets its counter.
+    unsigned* flags;
     // Sorted-token layout (fused MoE): row R of the tile grid holds routed pair
     // sorted_ids[R] (or, with no list, pair R / block_m on the first row of
     // each block and nothing elsewhere); a pair t >= num_valid is padding.
@@ -176,6 +183,60 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
     const bf16x2 p = __builtin_convertvector((f32x2{lo, hi}), bf16x2);  // v_cvt_pk_bf16_f32, RNE
     return __builtin_bit_cast(uint32_t, p);
 }
+// Cache-policy operand of the split-K slab stores and loads: the SC1 bit,
+// which the compiler emits for agent-scope relaxed atomic accesses.  Such an
+// access is coherent across the XCDs' L2s, and a store is visible device-wide
+// once it has completed (vmcnt), so a slab written this way needs no L2
+// write-back before its arrival is counted.
+constexpr int kDeviceCoherent = 16;
+
+// Split-K sum of rows [r, r_end) step r_step of one tile's slabs:
+// D = bf16(((s_0 + s_1) + s_2) + ...), in split order, one float4 run of
+// columns per lane (c = the run's first column within the tile).
+template <int BM, int BN, int kAux>
+__device__ __forceinline__ void splitk_sum_rows(const GemmArgs& a, int trel, int m0, int n0, int r, int r_end,
+                                                int r_step, int c) {
+    const int slab = a.tile_count * BM * BN * 4;   // bytes between splits (the workspace is below 2 GiB)
+    const __amdgpu_buffer_rsrc_t dP = __builtin_amdgcn_make_buffer_rsrc(
+        a.P + (int64_t)trel * BM * BN, (short)0, (int)((a.splits - 1) * slab + BM * BN * 4), (int)kRsrcWord3);
+    auto ld = [&](int off) {
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(dP, off, 0, kAux));
+    };
+    for (; r < r_end; r += r_step) {
+        const int o = (r * BN + c) * 4;
+        float4 acc = ld(o);
+        int sp = 1;
+        for (; sp + 3 < a.splits; sp += 4) {
+            const float4 v0 = ld(o + sp * slab);
+            const float4 v1 = ld(o + (sp + 1) * slab);
+            const float4 v2 = ld(o + (sp + 2) * slab);
+            const float4 v3 = ld(o + (sp + 3) * slab);
+            acc.x = (((acc.x + v0.x) + v1.x) + v2.x) + v3.x;
+            acc.y = (((acc.y + v0.y) + v1.y) + v2.y) + v3.y;
+            acc.z = (((acc.z + v0.z) + v1.z) + v2.z) + v3.z;
+            acc.w = (((acc.w + v0.w) + v1.w) + v2.w) + v3.w;
+        }
+        for (; sp < a.splits; ++sp) {
+            const float4 v = ld(o + sp * slab);
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+        const int n = n0 + c;
+        uint16_t* d = a.D + (int64_t)(m0 + r) * a.ldd + n;
+        const uint32_t lo = pack_bf16(acc.x, acc.y), hi = pack_bf16(acc.z, acc.w);
+        if (a.vec_store && n + 3 < a.N) {
+            *reinterpret_cast<uint2*>(d) = make_uint2(lo, hi);
+        } else {
+            if (n < a.N) d[0] = (uint16_t)lo;
+            if (n + 1 < a.N) d[1] = (uint16_t)(lo >> 16);
+            if (n + 2 < a.N) d[2] = (uint16_t)hi;
+            if (n + 3 < a.N) d[3] = (uint16_t)(hi >> 16);
+        }
+    }
+}
+
 // Block-scaled GEMM tile kernel: BM x BN output tile, four wavefronts in a
 // 2 x 2 grid, each owning a (BM/2) x (BN/2) block of 32x32 MFMA fragments.
 //
@@ -546,7 +607,11 @@ gemm_bs_kernel(const GemmArgs a) {
                     const int voff = roff + (ncol + j * 32 + 8 * p) * 4;
                     const v4i v = {__float_as_int(acc[i][j][4 * p]), __float_as_int(acc[i][j][4 * p + 1]),
                                    __float_as_int(acc[i][j][4 * p + 2]), __float_as_int(acc[i][j][4 * p + 3])};
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), dP, voff, 0, 0);
+                    if (a.flags)
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), dP, voff, 0,
+                                                               kDeviceCoherent);
+                    else
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), dP, voff, 0, 0);
                 }
         }
     };
@@ -627,10 +692,37 @@ gemm_bs_kernel(const GemmArgs a) {
         }
     };
 
-    if constexpr (kSplitK)
+    if constexpr (kSplitK) {
         epilogue_partial();
-    else
+        if (a.flags) {
+            // Fused reduction: every wavefront's (device-coherent) slab stores
+            // have completed before its workgroup counts itself in; the
+            // workgroup that brings the tile's count to `splits` sums all
+            // slabs (its own included, in split order, with device-coherent
+            // loads) and leaves the counter at zero.  No workgroup waits for
+            // another, so nothing depends on residency.
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();  // also: the main loop's LDS reads are done, smem is free
+            unsigned* last = reinterpret_cast<unsigned*>(smem);
+            if (threadIdx.x == 0) {
+                const unsigned prev =
+                    __hip_atomic_fetch_add(a.flags + trel, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const unsigned is_last = prev + 1 == (unsigned)a.splits;
+                if (is_last) __hip_atomic_store(a.flags + trel, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                *last = is_last;
+            }
+            __syncthreads();
+            if (*last) {
+                constexpr int kRuns = BN / 4, kRowStep = 64 * kWaves / kRuns;
+                static_assert((64 * kWaves) % kRuns == 0, "whole rows per pass");
+                splitk_sum_rows<BM, BN, kDeviceCoherent>(a, trel, m0, n0, (int)threadIdx.x / kRuns,
+                                                         min(a.M - m0, BM), kRowStep,
+                                        ((int)threadIdx.x % kRuns) * 4);
+            }
+        }
+    } else {
         epilogue();
+    }
 }
 
 // Split-K reduction: D = bf16(sum_s slab[s]) summed in split order
@@ -654,43 +746,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a) {
         tn = w / gm;
     }
     const int m0 = tm * BM, n0 = tn * BN;
-    const int64_t slab = (int64_t)a.tile_count * BM * BN;
-    const float* P = a.P + (int64_t)trel * BM * BN;
-    for (int r = strip * 8 + threadIdx.x / kRuns; r < strip * 8 + 8; r += kRows) {
-        if (m0 + r >= a.M) break;
-        const int c = (threadIdx.x % kRuns) * 4;
-        const float* p = P + r * BN + c;
-        float4 acc = *reinterpret_cast<const float4*>(p);
-        int sp = 1;
-        for (; sp + 3 < a.splits; sp += 4) {
-            const float4 v0 = *reinterpret_cast<const float4*>(p + sp * slab);
-            const float4 v1 = *reinterpret_cast<const float4*>(p + (sp + 1) * slab);
-            const float4 v2 = *reinterpret_cast<const float4*>(p + (sp + 2) * slab);
-            const float4 v3 = *reinterpret_cast<const float4*>(p + (sp + 3) * slab);
-            acc.x = (((acc.x + v0.x) + v1.x) + v2.x) + v3.x;
-            acc.y = (((acc.y + v0.y) + v1.y) + v2.y) + v3.y;
-            acc.z = (((acc.z + v0.z) + v1.z) + v2.z) + v3.z;
-            acc.w = (((acc.w + v0.w) + v1.w) + v2.w) + v3.w;
-        }
-        for (; sp < a.splits; ++sp) {
-            const float4 v = *reinterpret_cast<const float4*>(p + sp * slab);
-            acc.x += v.x;
-            acc.y += v.y;
-            acc.z += v.z;
-            acc.w += v.w;
-        }
-        const int n = n0 + c;
-        uint16_t* d = a.D + (int64_t)(m0 + r) * a.ldd + n;
-        const uint32_t lo = pack_bf16(acc.x, acc.y), hi = pack_bf16(acc.z, acc.w);
-        if (a.vec_store && n + 3 < a.N) {
-            *reinterpret_cast<uint2*>(d) = make_uint2(lo, hi);
-        } else {
-            if (n < a.N) d[0] = (uint16_t)lo;
-            if (n + 1 < a.N) d[1] = (uint16_t)(lo >> 16);
-            if (n + 2 < a.N) d[2] = (uint16_t)hi;
-            if (n + 3 < a.N) d[3] = (uint16_t)(hi >> 16);
-        }
-    }
+    splitk_sum_rows<BM, BN, 0>(a, trel, m0, n0, strip * 8 + (int)threadIdx.x / kRuns,
+                               min(strip * 8 + 8, a.M - m0), kRows, ((int)threadIdx.x % kRuns) * 4);
 }
 
 // LDS bytes of a tile configuration; configurations that fit twice into a
@@ -746,6 +803,52 @@ static void plan_tail(Schedule& s, int64_t M, int KBT) {
     }
 }
 
+// Arrival counters of the fused split-K reduction, in a region of a static
+// device array.  A region serves one stream's eager launches (launches on
+// one stream never overlap) or all launches captured under one stream
+// capture (a captured graph is never replayed concurrently with itself);
+// distinct streams and captures get distinct regions, so concurrent launches
+// never share a counter.  Every launch leaves its counters at zero.  When
+// the regions are used up (or the array's address cannot be had), launches
+// fall back to the separate reduction kernel.
+constexpr int kFusedReduceRows = 16;
+constexpr int kFlagRegion = 1024;   // tail tiles per launch; a tail is below 2 x CUs tiles
+constexpr int kFlagRegions = 512;
+constexpr int kFlagDevices = 64;
+__device__ __attribute__((aligned(256))) unsigned g_splitk_flags[kFlagRegions * kFlagRegion];
+
+static unsigned* splitk_flags_for(hipStream_t st, int64_t tail_tiles) {
+    static std::mutex mu;
+    static unsigned* base[kFlagDevices] = {};
+    static int used[kFlagDevices] = {};
+    static std::map<std::tuple<int, int, uint64_t>, int> region;  // (device, captured, stream or capture id)
+    if (tail_tiles > kFlagRegion) return nullptr;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kFlagDevices) return nullptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    unsigned long long cid = 0;
+    if (hipStreamGetCaptureInfo(st, &cs, &cid) != hipSuccess) return nullptr;
+    if (cs != hipStreamCaptureStatusNone && cs != hipStreamCaptureStatusActive) return nullptr;
+    const bool cap = cs == hipStreamCaptureStatusActive;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!base[dev]) {
+        if (cap) return nullptr;   // resolved on the first eager launch, not inside a capture
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_splitk_flags)) != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        base[dev] = static_cast<unsigned*>(p);
+    }
+    const auto key = std::make_tuple(dev, cap ? 1 : 0, cap ? (uint64_t)cid : (uint64_t)(uintptr_t)st);
+    auto it = region.find(key);
+    if (it == region.end()) {
+        if (used[dev] >= kFlagRegions) return nullptr;
+        it = region.emplace(key, used[dev]++).first;
+    }
+    return base[dev] + (int64_t)it->second * kFlagRegion;
+}
+
 template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, int kWaves = 4>
 static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const char* what) {
     a.tiles_m = (a.M + BM - 1) / BM;
@@ -766,21 +869,30 @@ static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const cha
         KBN_CHECK_ARG(sc.bm == BM && sc.bn == BN && sc.tiles == tiles, "%s: split plan does not match the %dx%d tiles",
                       what, BM, BN);
         const int64_t need = (int64_t)sc.splits * (tiles - dp) * BM * BN * 4;
+        KBN_CHECK_ARG(need < 0x7FFFFFFFLL, "%s: split slabs span >= 2 GiB", what);
         KBN_CHECK_ARG(sc.splits >= 2 && sc.kb_per_split >= 1 && need <= a.ws_bytes,
                       "%s: workspace of %lld bytes is smaller than the %lld the split plan writes", what,
                       (long long)a.ws_bytes, (long long)need);
-        KBN_CHECK_ARG((int64_t)sc.splits * sc.kb_per_split >= a.K / kRowB, "%s: split plan does not cover K", what);
+        KBN_CHECK_ARG((int64_t)sc.splits * sc.kb_per_split >= a.K / kRowB &&
+                          (int64_t)(sc.splits - 1) * sc.kb_per_split < a.K / kRowB,
+                      "%s: split plan does not cover K in %d non-empty splits", what, sc.splits);
         a.tile_base = (int)dp;
         a.tile_count = (int)(tiles - dp);
         a.splits = sc.splits;
         a.kb_per_split = sc.kb_per_split;
         const int64_t blocks = (tiles - dp) * sc.splits;
         KBN_CHECK_ARG(blocks <= 0x7FFFFFFFLL, "%s: too many tiles", what);
+        // Few rows: the tile's last workgroup sums the slabs (one launch
+        // less).  More rows: that sum would run on one workgroup per tile at
+        // the end of the launch, so the separate kernel spreads it instead.
+        a.flags = a.M <= kFusedReduceRows ? splitk_flags_for(st, tiles - dp) : nullptr;
         gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped && false, true, kWaves>
             <<<dim3((unsigned)blocks), dim3(64 * kWaves), 0, st>>>(a);
         KBN_CHECK_LAUNCH(what);
-        splitk_reduce_kernel<BM, BN><<<dim3((unsigned)((tiles - dp) * (BM / 8))), dim3(256), 0, st>>>(a);
-        KBN_CHECK_LAUNCH(what);
+        if (!a.flags) {
+            splitk_reduce_kernel<BM, BN><<<dim3((unsigned)((tiles - dp) * (BM / 8))), dim3(256), 0, st>>>(a);
+            KBN_CHECK_LAUNCH(what);
+        }
     }
     return 0;
 }

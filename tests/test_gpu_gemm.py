@@ -373,3 +373,67 @@ def test_grouped_gemm_fp32_contract_equals_ue8m0_on_power_of_two_scales(gpu_devi
     _ops.m_grouped_gemm_nt_contiguous(*args, C0, idt, disable_ue8m0_cast=True)
     torch.cuda.synchronize()
     assert torch.equal(C0, C1)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 8192, 8192), (8, 7168, 16384), (16, 1024, 28672), (64, 1024, 28672)])
+def test_gemm_split_fused_reduction_repeats_on_streams_and_graphs(gpu_device, M, N, K):
+    """Up to 16 rows, the split-K tail is summed by the last workgroup of
+    each tile to finish, counted with per-tile arrival counters that each
+    launch leaves at zero (more rows: a separate reduction launch, M=64
+    here).  The sum runs in split order whichever workgroup is last, so
+    every call gives the same bits: repeated calls on one stream, calls on
+    two streams in flight together, and replays of a captured graph (with
+    eager calls between replays) all equal the first call.  Outputs start as
+    NaN, so a tile whose reduction did not run is caught."""
+    from kb_nano_amd import _ops
+    from kb_nano_amd._lib import lib
+    from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
+    assert lib().kbn_fp8_gemm_nt_workspace_bytes(M, N, K, 1) > 0, "shape expected to split its tail"
+    qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=M + N + K)
+    A = to_fp8(qa, gpu_device)
+    sA = _alloc_colmajor_scale(M, K // 128, gpu_device)
+    sA.copy_(torch.from_numpy(sa))
+    W, sW = to_fp8(qw, gpu_device), torch.from_numpy(sw).to(gpu_device)
+
+    def fresh():
+        return torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu_device)
+
+    D0 = fresh()
+    _ops.fp8_gemm_nt(A, sA, W, sW, D0, use_ue8m0=True)
+    torch.cuda.synchronize()
+    cols = np.unique(np.concatenate([[0, N - 1], np.random.default_rng(K).integers(0, N, 94)]))
+    ref = oracle.gemm_nt_sample(qa, sa, qw, sw, ue8m0=True, cols=cols)
+    assert_gemm_close(D0[:, torch.from_numpy(cols).to(gpu_device)], ref, f"fused split {M}x{N}x{K}")
+    bits0 = bf16_bits(D0)
+
+    for i in range(3):
+        D = fresh()
+        _ops.fp8_gemm_nt(A, sA, W, sW, D, use_ue8m0=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(bf16_bits(D), bits0), f"repeat {i}"
+
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = [fresh() for _ in range(6)]
+    torch.cuda.synchronize()
+    for i, D in enumerate(outs):   # no synchronisation between: the two streams' launches may overlap
+        with torch.cuda.stream(s1 if i % 2 == 0 else s2):
+            _ops.fp8_gemm_nt(A, sA, W, sW, D, use_ue8m0=True)
+    torch.cuda.synchronize()
+    for i, D in enumerate(outs):
+        assert np.array_equal(bf16_bits(D), bits0), f"two-stream call {i}"
+
+    Dg = fresh()
+    _ops.fp8_gemm_nt(A, sA, W, sW, Dg, use_ue8m0=True)   # warm the caching allocator on this stream
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _ops.fp8_gemm_nt(A, sA, W, sW, Dg, use_ue8m0=True)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        Dg.fill_(float("nan"))
+        De = fresh()
+        _ops.fp8_gemm_nt(A, sA, W, sW, De, use_ue8m0=True)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bf16_bits(Dg), bits0), f"graph replay {rep}"
+        assert np.array_equal(bf16_bits(De), bits0), f"eager call between replays {rep}"
