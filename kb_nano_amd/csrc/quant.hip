@@ -45,7 +45,12 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #define KBN_QUANT_PER_CU 2
 #endif
 constexpr int kThreads = 1024;       // 16 wavefronts
-constexpr int kUnroll = 2;           // 4-group blocks per wavefront per pass
+// 4-group blocks per wavefront per pass (per operand): the SiLU kernel runs
+// one workgroup per CU (its LDS table), so it takes more blocks per pass to
+// keep as many bytes in flight (measured at cfg2: 4 -> 129 us, 2 -> 132 us,
+// 5..8 -> 136-140 us; the quant kernel is best at 2).
+template <bool kSilu>
+constexpr int kUnrollOf = kSilu ? 4 : 2;
 constexpr int kXcds = 8;             // MI355X: workgroups are dealt round-robin to 8 XCDs
 constexpr int kLineRows = 32;        // rows sharing one 128-B line of column-major scales
 
@@ -145,6 +150,7 @@ __global__ __launch_bounds__(kThreads) void group_quant_kernel(const QuantArgs a
     const int xcd = blockIdx.x % kXcds, local = blockIdx.x / kXcds;
     const int row_begin = xcd * a.rows_per_xcd;
     const int row_end = min(a.M, row_begin + a.rows_per_xcd);
+    constexpr int kUnroll = kUnrollOf<kSilu>;
     const int64_t t0 = ((int64_t)local * (kThreads / 64) + wave) * (4 * kUnroll) + (lane >> 4);
     GroupCursor c{row_begin + (int)(t0 / a.G), (int)(t0 % a.G)};
     while (c.row < row_end) {
@@ -191,10 +197,10 @@ __global__ void silu_bf16_debug_kernel(const uint16_t* __restrict__ g, uint16_t*
 
 // Row slices per XCD (multiples of 32 rows) and the number of workgroups
 // per XCD: at most `per_cu` per CU, never more than the slice needs.
-static int plan(QuantArgs& a, int per_cu) {
+static int plan(QuantArgs& a, int per_cu, int unroll) {
     const int slice = (a.M + kXcds - 1) / kXcds;
     a.rows_per_xcd = (slice + kLineRows - 1) / kLineRows * kLineRows;
-    const int64_t per_block = (int64_t)(kThreads / 64) * 4 * kUnroll;  // groups per workgroup pass
+    const int64_t per_block = (int64_t)(kThreads / 64) * 4 * unroll;  // groups per workgroup pass
     const int64_t need = ((int64_t)a.rows_per_xcd * a.G + per_block - 1) / per_block;
     const int per_xcd = (int)std::max<int64_t>(1, std::min<int64_t>(need, (int64_t)cu_count() / kXcds * per_cu));
     const int64_t stride = (int64_t)per_xcd * per_block;
@@ -231,7 +237,7 @@ extern "C" int kbn_per_token_group_quant_fp8(const void* x_bf16, int64_t M, int6
     KBN_CHECK_ARG(ld_x >= K, "%s: input row stride smaller than K", what);
     QuantArgs a{(const uint16_t*)x_bf16, ld_x, 0, (uint8_t*)q_fp8, ld_q, scale, s_stride_m, s_stride_g,
                 (int)M, (int)(K / kGroup), 0, 0, 0, eps};
-    const int blocks = plan(a, KBN_QUANT_PER_CU);
+    const int blocks = plan(a, KBN_QUANT_PER_CU, kUnrollOf<false>);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (use_ue8m0)
         group_quant_kernel<false, true><<<blocks, kThreads, 0, st>>>(a);
@@ -250,7 +256,7 @@ extern "C" int kbn_silu_mul_quant_fp8(const void* in_bf16, int64_t M, int64_t N_
     KBN_CHECK_ARG(ld_in >= 2 * N_half, "%s: input row stride smaller than 2*N/2", what);
     QuantArgs a{(const uint16_t*)in_bf16, ld_in, N_half, (uint8_t*)q_fp8, ld_q, scale, s_stride_m, s_stride_g,
                 (int)M, (int)(N_half / kGroup), 0, 0, 0, eps};
-    const int blocks = plan(a, 1);  // the LDS table allows one workgroup per CU
+    const int blocks = plan(a, 1, kUnrollOf<true>);  // the LDS table allows one workgroup per CU
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (use_ue8m0)
         group_quant_kernel<true, true><<<blocks, kThreads, 0, st>>>(a);
