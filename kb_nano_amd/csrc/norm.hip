@@ -49,6 +49,14 @@ struct NormArgs {
     float eps;
 };
 
+// Two floats rounded to bf16 (nearest even) and packed, lo in the low half:
+// one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), bf16x2));
+}
+
 __device__ __forceinline__ float bf16_at(const u32x4& v, int j) {
     const uint32_t word = v[j >> 1];
     return (j & 1) ? bf16hi(word) : bf16lo(word);
@@ -108,16 +116,20 @@ __device__ __forceinline__ void norm_row(const NormArgs& a, int m, int wave, int
         const int c = kW * i + wave;
         u32x4 nr = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            float av = bf16_at(row.x[i], j);
-            base[i][j] = av;
+        for (int j = 0; j < 8; j += 2) {
+            float a0 = bf16_at(row.x[i], j), a1 = bf16_at(row.x[i], j + 1);
+            base[i][j] = a0;
+            base[i][j + 1] = a1;
             if constexpr (kAdd) {
-                av = bf16_at(row.r[i], j) + av;
-                const uint32_t h = f32_to_bf16_rne(av);
-                nr[j >> 1] |= h << (16 * (j & 1));
+                a0 = bf16_at(row.r[i], j) + a0;
+                a1 = bf16_at(row.r[i], j + 1) + a1;
+                const uint32_t h = pack_bf16_rne(a0, a1);
+                nr[j >> 1] = h;
                 base[i][j] = __uint_as_float(h << 16);
+                base[i][j + 1] = __uint_as_float(h & 0xFFFF0000u);
             }
-            p = fmaf(av, av, p);
+            p = fmaf(a0, a0, p);
+            p = fmaf(a1, a1, p);
         }
         if constexpr (kAdd) __builtin_amdgcn_raw_buffer_store_b128(nr, rw, 2 * (c * 512 + 8 * lane), 0, 0);
     }
@@ -183,8 +195,7 @@ __device__ __forceinline__ void norm_row(const NormArgs& a, int m, int wave, int
         if constexpr (kAdd) {
             u32x4 o;
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                o[k] = f32_to_bf16_rne(vout[i][2 * k]) | (f32_to_bf16_rne(vout[i][2 * k + 1]) << 16);
+            for (int k = 0; k < 4; ++k) o[k] = pack_bf16_rne(vout[i][2 * k], vout[i][2 * k + 1]);
             __builtin_amdgcn_raw_buffer_store_b128(o, xw, 2 * e0, 0, 0);
         }
     }

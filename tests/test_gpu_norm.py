@@ -107,3 +107,45 @@ def test_rmsnorm_quant_rejects_off_path_inputs(gpu_device):
         FusedAddRMSNormFP8Quant()(torch.zeros(2, 8200, dtype=torch.bfloat16, device=dev),
                                   torch.zeros(2, 8200, dtype=torch.bfloat16, device=dev),
                                   torch.ones(8200, dtype=torch.bfloat16, device=dev))
+
+
+def test_fused_add_rounding_edge_cases(gpu_device):
+    """The residual sums r + x are rounded to bf16 once (nearest even) and the
+    rounded values are what gets normalized: ties at 1 + k 2^-8 (odd k ties,
+    even k exact), sums k 2^-133 that are fp32 denormals (kept, not flushed),
+    sums just below and above the bf16 overflow threshold, and a random row.  Residual, normalized row, codes and scales
+    equal the oracle bit for bit."""
+    from kb_nano_amd import FusedAddRMSNormFP8Quant
+    dev = gpu_device
+    H = 1024
+    rng = np.random.default_rng(5)
+    f32 = np.float32
+    rows_x, rows_r = [], []
+    k = np.arange(H) % 16
+    sign = np.where(rng.random(H) < 0.5, f32(-1), f32(1))
+    rows_r.append(sign * f32(1.0))
+    rows_x.append(sign * (k * f32(2.0 ** -8)).astype(np.float32))
+    tiny = f32(2.0 ** -126)
+    kk = (np.arange(H) % 8).astype(np.float32)
+    rows_r.append(sign * tiny)
+    rows_x.append(-sign * (tiny - kk * f32(2.0 ** -133)))   # sums k 2^-133: fp32 denormals, exact in bf16
+    bf = lambda a: torch.from_numpy(np.asarray(a, np.float32)).bfloat16().float().numpy()
+    big = bf(np.full(H, 1.69e38))   # sums 3.38e38 (finite) to 3.44e38 (fp32 overflow)
+    rows_r.append(big * sign)
+    rows_x.append(bf(1.69e38 + (np.arange(H) % 4) * 0.01e38) * sign)
+    rows_r.append(bf(rng.standard_normal(H) * 4))
+    rows_x.append(bf(rng.standard_normal(H)))
+    to_bits = lambda a: torch.from_numpy(np.stack(a)).bfloat16()
+    x, r = to_bits(rows_x), to_bits(rows_r)
+    # the inputs must themselves be exact bf16 values (the sums are what is tested)
+    assert torch.equal(x.float(), torch.from_numpy(np.stack(rows_x)))
+    w = torch.from_numpy(rng.standard_normal(H).astype(np.float32)).bfloat16()
+    xd, rd = x.to(dev), r.to(dev)
+    q, s, _ = FusedAddRMSNormFP8Quant()(xd, rd, w.to(dev), 1e-6)
+    torch.cuda.synchronize()
+    q_ref, s_ref, r_ref, x_ref = oracle.rmsnorm_quant(bf16_bits(x), bf16_bits(w), eps=1e-6,
+                                                      residual_bits=bf16_bits(r))
+    assert np.array_equal(bf16_bits(rd), r_ref)
+    assert np.array_equal(bf16_bits(xd), x_ref)
+    assert np.array_equal(fp8_codes(q), q_ref)
+    assert np.array_equal(s.cpu().numpy(), s_ref, equal_nan=True)
