@@ -351,7 +351,7 @@ __global__ __launch_bounds__(kSumThreads) void moe_sum_kernel(const MoeSumArgs a
     float r[8];
     if (a.vec && nc == 8) {
         topk_sum8(a.top_k, [&](int j, float (&x)[8]) {
-            const u32x4 w = *reinterpret_cast<const u32x4*>(row0 + (int64_t)j * a.ld_x);
+            const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row0 + (int64_t)j * a.ld_x));
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 x[2 * q] = bf16lo(w[q]);
@@ -427,7 +427,9 @@ __global__ __launch_bounds__(kUnpermThreads) void moe_unpermute_kernel(const Unp
                 const int64_t wi = (int64_t)m * a.top_k + j;
                 wt[u] = a.w_bf16 ? __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(a.w)[wi] << 16)
                                  : reinterpret_cast<const float*>(a.w)[wi];
-                if (use[u]) v[u] = *reinterpret_cast<const u32x4*>(a.y + (int64_t)r * a.ld_y + (int64_t)c8 * 8);
+                if (use[u])
+                    v[u] = __builtin_nontemporal_load(
+                        reinterpret_cast<const u32x4*>(a.y + (int64_t)r * a.ld_y + (int64_t)c8 * 8));
             }
         }
 #pragma unroll

@@ -76,6 +76,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* p, int by
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, (int)kRsrcWord3);
 }
 
+// Cache-policy operand of the row loads: non-temporal (each row is read once;
+// at H = 7168, M = 4096 this is 20.5 against 22.4 us plain and 55.6 against
+// 58.2 us with the residual add).
+constexpr int kNtLoad = 2;
+
 template <int kW, int kCW, bool kAdd>
 __device__ __forceinline__ void load_row(const NormArgs& a, int m, int wave, int lane, NormRow<kCW, kAdd>& row,
                                          int dep = 0) {
@@ -84,8 +89,8 @@ __device__ __forceinline__ void load_row(const NormArgs& a, int m, int wave, int
 #pragma unroll
     for (int i = 0; i < kCW; ++i) {
         const int off = 2 * ((kW * i + wave) * 512 + 8 * lane) + dep;   // lanes past the row read zeros
-        row.x[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
-        if constexpr (kAdd) row.r[i] = __builtin_amdgcn_raw_buffer_load_b128(rr, off, 0, 0);
+        row.x[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, kNtLoad);
+        if constexpr (kAdd) row.r[i] = __builtin_amdgcn_raw_buffer_load_b128(rr, off, 0, kNtLoad);
     }
 }
 

@@ -55,9 +55,10 @@ __global__ __launch_bounds__(256) void block_requant_kernel(const RequantArgs a)
 #pragma unroll
         for (int c = 0; c < 16; ++c) {
             const int r = r0 + 8 * c;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (col_ok && r < rows) v = *reinterpret_cast<const float4*>(src + (int64_t)r * a.K);
-            x[4 * c] = v.x; x[4 * c + 1] = v.y; x[4 * c + 2] = v.z; x[4 * c + 3] = v.w;
+            u32x4 v = u32x4{0u, 0u, 0u, 0u};
+            if (col_ok && r < rows) v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + (int64_t)r * a.K));
+            x[4 * c] = __uint_as_float(v.x); x[4 * c + 1] = __uint_as_float(v.y);
+            x[4 * c + 2] = __uint_as_float(v.z); x[4 * c + 3] = __uint_as_float(v.w);
         }
     } else {
         const int r0 = t >> 3, col = (t & 7) * 16;
@@ -68,7 +69,7 @@ __global__ __launch_bounds__(256) void block_requant_kernel(const RequantArgs a)
         for (int c = 0; c < 4; ++c) {
             const int r = r0 + 32 * c;
             u32x4 v = u32x4{0u, 0u, 0u, 0u};
-            if (col_ok && r < rows) v = *reinterpret_cast<const u32x4*>(src + (int64_t)r * a.K);
+            if (col_ok && r < rows) v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + (int64_t)r * a.K));
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
                 const int w = (int)v[d];
