@@ -193,7 +193,7 @@ __device__ __forceinline__ void wave_row(const uint8_t* src, uint8_t* dst, int b
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int w = v0 + u * 64;
-            if (w < nv) d[w] = t[u];
+            if (w < nv) __builtin_nontemporal_store(t[u], d + w);
         }
     }
 }
