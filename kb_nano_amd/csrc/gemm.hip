@@ -156,9 +156,9 @@ constexpr int kRowB = 128;   // LDS row bytes = K per stage = one scale block
 // sequence so the tiles resident on one XCD (and its L2) share A row panels
 // and W panels, and walk that sequence in column groups of kGroupM row tiles
 // (the K splits of one tile are neighbours).
+template <int kGroupM>
 __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int tile_base, int splits, int& tm, int& tn,
                                             int& trel, int& split) {
-    constexpr int kGroupM = 4;
     const int nblk = gridDim.x;
     const int bid = blockIdx.x;
     const int xcd = bid & 7, i = bid >> 3;
@@ -274,7 +274,11 @@ gemm_bs_kernel(const GemmArgs a) {
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)smem);
 
     int tm, tn, trel = 0, split = 0;
-    tile_coords(a.tiles_m, a.tiles_n, a.tile_base, kSplitK ? a.splits : 1, tm, tn, trel, split);
+    // MoE tiles walk 8 tile rows per column group: an expert's row tiles then
+    // share its weight panel in L2 more often (cfg4: 1% faster than 4; dense
+    // tiles keep 4, which the split reduction's tile order also assumes)
+    tile_coords<(kGrouped || kSorted) ? 8 : 4>(a.tiles_m, a.tiles_n, a.tile_base, kSplitK ? a.splits : 1, tm, tn,
+                                               trel, split);
     const int m0 = tm * BM, n0 = tn * BN;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
