@@ -98,3 +98,23 @@ def test_grouped_gemm_and_norm_compile_without_graph_breaks(gpu_device):
     q1, s1 = _compiled(lambda a: norm(a, w, 1e-6))(x)
     torch.cuda.synchronize()
     assert np.array_equal(fp8_codes(q1), fp8_codes(q0)) and torch.equal(s1, s0)
+
+
+def test_fused_add_norm_compiles_and_mutates_in_place(gpu_device):
+    """The fused residual-add variant writes its two bf16 inputs in place; under
+    the compiled graph the same buffers must end up with the same bits."""
+    from kb_nano_amd import FusedAddRMSNormFP8Quant
+    print("compile fused add rmsnorm", flush=True)
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(64, 7168, generator=g).bfloat16().to(gpu_device)
+    r = (torch.randn(64, 7168, generator=g) * 4).bfloat16().to(gpu_device)
+    w = torch.randn(7168, generator=g).bfloat16().to(gpu_device)
+    norm = FusedAddRMSNormFP8Quant()
+    x0, r0 = x.clone(), r.clone()
+    q0, s0, _ = norm(x0, r0, w, 1e-6)
+    x1, r1 = x.clone(), r.clone()
+    q1, s1, r_ret = _compiled(lambda a, b: norm(a, b, w, 1e-6))(x1, r1)
+    torch.cuda.synchronize()
+    assert np.array_equal(fp8_codes(q1), fp8_codes(q0)) and torch.equal(s1, s0)
+    assert np.array_equal(bf16_bits(x1), bf16_bits(x0)) and np.array_equal(bf16_bits(r1), bf16_bits(r0))
+    assert np.array_equal(bf16_bits(r_ret), bf16_bits(r0))
