@@ -62,12 +62,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
-// Round-to-nearest-even float -> bf16 bits (inputs here are never NaN).
-__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
-    uint32_t u = __float_as_uint(f);
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
-
 // Smallest power of two >= r for a positive normal float r (exponent bits,
 // +1 when any mantissa bit is set): the UE8M0 rounding of the scale.
 __device__ __forceinline__ float ue8m0_ceil(float r) {
