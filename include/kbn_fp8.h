@@ -89,7 +89,8 @@ int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int64_t sA_stri
  * results are deterministic and equal for any split count up to fp32
  * summation order): for M <= 16 the last workgroup of each tile does it in
  * the same launch, using per-tile arrival counters the library keeps in a
- * static device array per stream (or per stream capture); otherwise, or
+ * static device array per stream (per capturing stream under capture,
+ * streams forked into one capture included); otherwise, or
  * when those run out, a second launch on the same stream does it.
  * kbn_fp8_gemm_nt_workspace_bytes returns the bytes this needs for a shape on
  * the current device (0: no split, workspace unused).  A null or smaller
@@ -281,9 +282,10 @@ int kbn_moe_sum(const void* x_bf16, int64_t M, int64_t top_k, int64_t H, int64_t
  * and the DeepGEMM per_block_cast_to_fp8 it calls (:497-499, :543-545).
  *   w_in    [E, N, K] contiguous: fp8 codes (in_f32 = 0), dequantized with the
  *           block scale s_in[e*s_in_e + nb*s_in_ld + kb], or fp32 values (1)
- *   w_out   fp8 [E, N, K] contiguous, s_out[e*s_out_e + nb*s_out_ld + kb];
- *           both may alias the inputs (in-place requant).  K % 16 == 0,
- *           16-byte aligned weights.
+ *   w_out   fp8 [E, N, K] contiguous, s_out[e*s_out_e + nb*s_out_ld + kb].
+ *           In-place requant of fp8 codes: w_out == w_in and s_out == s_in
+ *           with equal strides.  Any other overlap (and every overlap of
+ *           fp32 input) is rejected.  K % 16 == 0, 16-byte aligned weights.
  *   Per block: sf = max(max|x|, eps) / 448, rounded up to a power of two when
  *   use_ue8m0; codes = e4m3_rne(x * (1/sf)); ragged blocks pad with zeros.
  */

@@ -420,12 +420,22 @@ def moe_sum(x: torch.Tensor, out: torch.Tensor) -> None:
           what)
 
 
+def _overlaps(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Whether the storage byte ranges spanned by two tensors intersect."""
+    def span(t):
+        lo = t.data_ptr()
+        return lo, lo + (sum((n - 1) * st for n, st in zip(t.shape, t.stride())) + 1) * t.element_size()
+    (a0, a1), (b0, b1) = span(a), span(b)
+    return a.numel() > 0 and b.numel() > 0 and a0 < b1 and b0 < a1
+
+
 def fp8_block_requant(w_in: torch.Tensor, s_in: torch.Tensor | None, w_out: torch.Tensor, s_out: torch.Tensor,
                       use_ue8m0: bool, eps: float) -> None:
     """128x128 block quantization of ``w_in`` ([N, K] or [E, N, K]; fp8 codes
     dequantized with the block scales ``s_in``, or fp32) into ``w_out`` (fp8,
-    same shape) and ``s_out`` ([(E,) ceil(N/128), >= ceil(K/128)]); outputs may
-    alias the inputs."""
+    same shape) and ``s_out`` ([(E,) ceil(N/128), >= ceil(K/128)]).  fp8 codes
+    may be requantized in place (``w_out`` is ``w_in``, ``s_out`` is ``s_in``);
+    any other overlap, and every overlap of fp32 input, is rejected."""
     what = "fp8_block_requant"
     _dev_check(what, *[t for t in (w_in, s_in, w_out, s_out) if t is not None])
     in_f32 = w_in.dtype == torch.float32
@@ -451,6 +461,10 @@ def fp8_block_requant(w_in: torch.Tensor, s_in: torch.Tensor | None, w_out: torc
 
     so_e, so_ld = strides(s_out, "s_out")
     si_e, si_ld = strides(s_in, "s_in") if not in_f32 else (0, 0)
+    if _overlaps(w_in, w_out) and (in_f32 or w_in.data_ptr() != w_out.data_ptr()):
+        raise ValueError(f"{what}: w_out overlaps w_in (only fp8 codes requantized exactly in place are allowed)")
+    if not in_f32 and _overlaps(s_in, s_out) and (s_in.data_ptr() != s_out.data_ptr() or (si_e, si_ld) != (so_e, so_ld)):
+        raise ValueError(f"{what}: s_out overlaps s_in with a different layout")
     check(lib().kbn_fp8_block_requant(
         w_in.data_ptr(), int(in_f32), s_in.data_ptr() if not in_f32 else None, si_e, si_ld, E, N, K,
         w_out.data_ptr(), s_out.data_ptr(), so_e, so_ld, int(bool(use_ue8m0)), float(eps), _stream(w_out)), what)

@@ -809,12 +809,14 @@ static void plan_tail(Schedule& s, int64_t M, int KBT) {
 
 // Arrival counters of the fused split-K reduction, in a region of a static
 // device array.  A region serves one stream's eager launches (launches on
-// one stream never overlap) or all launches captured under one stream
-// capture (a captured graph is never replayed concurrently with itself);
-// distinct streams and captures get distinct regions, so concurrent launches
-// never share a counter.  Every launch leaves its counters at zero.  When
-// the regions are used up (or the array's address cannot be had), launches
-// fall back to the separate reduction kernel.
+// one stream never overlap) or the launches captured on one stream under one
+// capture: streams forked into a capture share its id, but the nodes
+// captured on one of them form a dependency chain, and a captured graph is
+// never replayed concurrently with itself.  Distinct (capture, stream) pairs
+// and eager streams get distinct regions, so concurrent launches never share
+// a counter.  Every launch leaves its counters at zero.  When the regions are
+// used up (or the array's address cannot be had), launches fall back to the
+// separate reduction kernel.
 constexpr int kFusedReduceRows = 16;
 constexpr int kFlagRegion = 1024;   // tail tiles per launch; a tail is below 2 x CUs tiles
 constexpr int kFlagRegions = 512;
@@ -825,7 +827,7 @@ static unsigned* splitk_flags_for(hipStream_t st, int64_t tail_tiles) {
     static std::mutex mu;
     static unsigned* base[kFlagDevices] = {};
     static int used[kFlagDevices] = {};
-    static std::map<std::tuple<int, int, uint64_t>, int> region;  // (device, captured, stream or capture id)
+    static std::map<std::tuple<int, uint64_t, uint64_t>, int> region;  // (device, capture id or 0, stream)
     if (tail_tiles > kFlagRegion) return nullptr;
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kFlagDevices) return nullptr;
@@ -844,7 +846,8 @@ static unsigned* splitk_flags_for(hipStream_t st, int64_t tail_tiles) {
         }
         base[dev] = static_cast<unsigned*>(p);
     }
-    const auto key = std::make_tuple(dev, cap ? 1 : 0, cap ? (uint64_t)cid : (uint64_t)(uintptr_t)st);
+    // eager launches key on 0, captured ones on capture id + 1
+    const auto key = std::make_tuple(dev, cap ? (uint64_t)cid + 1 : (uint64_t)0, (uint64_t)(uintptr_t)st);
     auto it = region.find(key);
     if (it == region.end()) {
         if (used[dev] >= kFlagRegions) return nullptr;

@@ -17,8 +17,8 @@
 // column 16*(t%8) of rows t/8 + 32c (c = 0..3); fp32 input, the float4 at
 // column 4*(t%32) of rows t/32 + 8c (c = 0..15).  Block amax: wavefront max,
 // then four partials through LDS.  Every lane reads its inputs (and the block
-// scale) before the barrier and writes after it, so the output may alias the
-// input.
+// scale) before the barrier and writes after it, so fp8 codes may be
+// requantized in place (w_out == w_in, scales at the same positions).
 #include "kbn_common.h"
 
 namespace kbn {
@@ -145,6 +145,23 @@ extern "C" int kbn_fp8_block_requant(const void* w_in, int in_f32, const float* 
     KBN_CHECK_ARG(s_out_ld >= KB && s_out_e >= NB * s_out_ld, "%s: output scale strides too small", what);
     if (!in_f32) KBN_CHECK_ARG(s_in_ld >= KB && s_in_e >= NB * s_in_ld, "%s: input scale strides too small", what);
     KBN_CHECK_ARG(eps >= 1e-30f, "%s: eps must be at least 1e-30 (sf = eps/448 stays a normal float)", what);
+    // In-place requant is safe only where every block reads exactly the bytes
+    // it later writes: fp8 codes over the same layout (w_out == w_in) and
+    // scales at the same positions.  fp32 input is 4 bytes per element, so an
+    // fp8 output over it would overwrite other blocks' unread inputs.
+    const uintptr_t wi = reinterpret_cast<uintptr_t>(w_in), wo = reinterpret_cast<uintptr_t>(w_out);
+    const uintptr_t wi_end = wi + (uintptr_t)(E * N * K * (in_f32 ? 4 : 1)), wo_end = wo + (uintptr_t)(E * N * K);
+    const bool w_overlap = wi < wo_end && wo < wi_end;
+    KBN_CHECK_ARG(!w_overlap || (!in_f32 && wi == wo), "%s: w_out overlaps w_in (%s)", what,
+                  in_f32 ? "fp32 input cannot be requantized in place" : "only w_out == w_in is allowed");
+    if (!in_f32) {
+        const uintptr_t si = reinterpret_cast<uintptr_t>(s_in), so = reinterpret_cast<uintptr_t>(s_out);
+        const uintptr_t si_end = si + (uintptr_t)(((E - 1) * s_in_e + (NB - 1) * s_in_ld + KB) * 4);
+        const uintptr_t so_end = so + (uintptr_t)(((E - 1) * s_out_e + (NB - 1) * s_out_ld + KB) * 4);
+        const bool s_overlap = si < so_end && so < si_end;
+        KBN_CHECK_ARG(!s_overlap || (si == so && s_in_e == s_out_e && s_in_ld == s_out_ld),
+                      "%s: s_out overlaps s_in with a different layout", what);
+    }
     const int64_t blocks = E * NB * KB;
     KBN_CHECK_ARG(blocks <= 0x7FFFFFFFLL, "%s: too many blocks", what);
     RequantArgs a{};

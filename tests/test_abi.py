@@ -340,3 +340,29 @@ def test_sorted_moe_config_block_sizes():
     with pytest.raises(NotImplementedError):
         MoeGroupedGemm()(torch.zeros(4, 256), torch.zeros(2, 256, 256), torch.zeros(8, 256), None, None,
                          torch.zeros(8, dtype=torch.int32), torch.zeros(1, dtype=torch.int32), False, 2)
+
+
+def test_requant_rejects_unsafe_aliasing():
+    """In-place requant is allowed only for fp8 codes over the same layout:
+    fp32 input (4 bytes per element) under an fp8 output, a shifted fp8
+    output, or scales aliased with other strides are rejected before any
+    launch (the pointers are never dereferenced)."""
+    from kb_nano_amd._lib import lib
+    L = lib()
+    E, N, K = 2, 256, 256
+    base = 1 << 20
+    w, s = ctypes.c_void_p(base), ctypes.c_void_p(base + (1 << 24))
+    # fp32 input, fp8 output at the same address
+    assert L.kbn_fp8_block_requant(w, 1, None, 0, 0, E, N, K, w, s, 4, 2, 1, 1e-4, None) == 1
+    assert "in place" in _err()
+    # fp32 input, fp8 output inside its second half
+    w2 = ctypes.c_void_p(base + E * N * K * 2)
+    assert L.kbn_fp8_block_requant(w, 1, None, 0, 0, E, N, K, w2, s, 4, 2, 1, 1e-4, None) == 1
+    # fp8 input, output shifted by one row
+    w3 = ctypes.c_void_p(base + K)
+    assert L.kbn_fp8_block_requant(w, 0, s, 4, 2, E, N, K, w3, ctypes.c_void_p(base + (1 << 25)), 4, 2, 1, 1e-4,
+                                   None) == 1
+    assert "w_out == w_in" in _err()
+    # fp8 input in place, but the output scales alias the input scales with other strides
+    assert L.kbn_fp8_block_requant(w, 0, s, 4, 2, E, N, K, w, s, 8, 2, 1, 1e-4, None) == 1
+    assert "different layout" in _err()

@@ -440,3 +440,61 @@ def test_gemm_split_fused_reduction_repeats_on_streams_and_graphs(gpu_device, M,
         torch.cuda.synchronize()
         assert np.array_equal(bf16_bits(Dg), bits0), f"graph replay {rep}"
         assert np.array_equal(bf16_bits(De), bits0), f"eager call between replays {rep}"
+
+
+def test_gemm_fused_splitk_forked_capture(gpu_device):
+    """Split GEMMs with the fused (counter-based) reduction on two streams
+    forked into one graph capture: the branches share the capture id, so each
+    capturing stream must get its own counter region.  Three GEMMs (two of
+    them the same shape, so their tile counters coincide) run on the main
+    and the side branch of the graph; every replay, with eager calls and NaN
+    refills between replays, must give the bits of the eager calls."""
+    from kb_nano_amd import _ops
+    from kb_nano_amd._lib import lib
+    from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
+    shapes = [(1, 8192, 8192), (8, 7168, 16384), (8, 7168, 16384)]
+    cases = []
+    for i, (M, N, K) in enumerate(shapes):
+        assert M <= 16 and lib().kbn_fp8_gemm_nt_workspace_bytes(M, N, K, 1) > 0, "fused split expected"
+        qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=100 + i)
+        A = to_fp8(qa, gpu_device)
+        sA = _alloc_colmajor_scale(M, K // 128, gpu_device)
+        sA.copy_(torch.from_numpy(sa))
+        W, sW = to_fp8(qw, gpu_device), torch.from_numpy(sw).to(gpu_device)
+        cases.append((A, sA, W, sW, torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu_device)))
+
+    def run(case, out=None):
+        A, sA, W, sW, D = case
+        _ops.fp8_gemm_nt(A, sA, W, sW, D if out is None else out, use_ue8m0=True)
+
+    for c in cases:
+        run(c)
+    torch.cuda.synchronize()
+    eager = [bf16_bits(c[4]) for c in cases]
+    for c, (M, N, K) in zip(cases, shapes):
+        cols = np.arange(0, N, 97)
+        qa, sa = fp8_codes(c[0]), c[1].cpu().numpy()
+        ref = oracle.gemm_nt_sample(qa, sa, fp8_codes(c[2]), c[3].cpu().numpy(), ue8m0=True, cols=cols)
+        assert_gemm_close(c[4][:, torch.from_numpy(cols).to(gpu_device)], ref, f"eager {M}x{N}x{K}")
+
+    side = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        main = torch.cuda.current_stream()
+        side.wait_stream(main)
+        run(cases[0])
+        run(cases[1])
+        with torch.cuda.stream(side):
+            run(cases[2])
+        main.wait_stream(side)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        for c in cases:
+            c[4].fill_(float("nan"))
+        extra = torch.full_like(cases[1][4], float("nan"))
+        run(cases[1], extra)          # an eager call between replays
+        g.replay()
+        torch.cuda.synchronize()
+        for i, c in enumerate(cases):
+            assert np.array_equal(bf16_bits(c[4]), eager[i]), f"replay {rep}, GEMM {i}"
+        assert np.array_equal(bf16_bits(extra), eager[1]), f"eager call between replays {rep}"
