@@ -107,6 +107,25 @@ int kbn_fp8_gemm_nt_ws(const void* A, int64_t lda, const float* sA, int64_t sA_s
                        int scale_ue8m0, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * kbn_fp8_gemm_nt_ws without any allocation by the caller: the split-K slabs
+ * go to a device array the library holds per GPU (`scratch`, of
+ * kbn_fp8_gemm_nt_noalloc_scratch_bytes() = 64 MiB, kept until the process
+ * ends), so results are those of kbn_fp8_gemm_nt_ws with a large enough
+ * workspace, bit for bit.  A shape whose split plan needs more than the
+ * scratch is rejected (code 1); on a 256-CU MI355X no plan does.  Every call
+ * on one GPU uses the same scratch, so calls that may overlap on one GPU
+ * (other streams, forked branches of a graph) race: serialise them.
+ * No counterpart in the reference: this entry point is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).
+ */
+int64_t kbn_fp8_gemm_nt_noalloc_scratch_bytes(void);
+int kbn_fp8_gemm_nt_noalloc(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m, int64_t sA_stride_k,
+                            const void* W, int64_t ldw, const float* sW, int64_t sW_ld,
+                            void* D_bf16, int64_t ldd, int64_t M, int64_t N, int64_t K,
+                            int scale_ue8m0, void* stream);
+
+/*
  * Contiguous-layout grouped FP8 GEMM (MoE experts).
  * Replaces op kb_nano_fp8_moe::m_grouped_gemm_nt_contiguous ->
  * deep_gemm.m_grouped_fp8_gemm_nt_contiguous

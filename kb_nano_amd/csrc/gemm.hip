@@ -1012,10 +1012,47 @@ static int dispatch_dense(const GemmArgs& a, const Schedule& sc, int64_t K, hipS
     return 1;
 }
 
+// Device scratch of the allocation-free GEMM entry point: the split-K slabs
+// of kbn_fp8_gemm_nt_noalloc.  One copy per GPU (its own address on each),
+// held until the process ends.  The size covers every split plan on a
+// 256-CU device: a tail is split only when its split workgroups fit in one
+// wave of at most 256 workgroup slots for the 256x256 tiles, i.e. at most
+// 256 fp32 slabs of 256 x 256.  Calls on one GPU share it.
+constexpr int64_t kScratchBytes = 64ll << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current (host code never uses the symbol itself,
+// which is only a host-side stand-in).  nullptr (and the error set) if the
+// lookup fails.
+static void* scratch_ptr(const char* what) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void* ptr[kMaxDevices] = {};
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        set_error("%s: no current HIP device (or device index >= %d)", what, kMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", what, dev, hipGetErrorString(e));
+            return nullptr;
+        }
+        ptr[dev] = p;
+    }
+    return ptr[dev];
+}
+
 static int gemm_nt_impl(const char* what, const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
                         int64_t sA_stride_k, const void* W, int64_t ldw, const float* sW, int64_t sW_ld, void* D_bf16,
                         int64_t ldd, int64_t M, int64_t N, int64_t K, int scale_ue8m0, void* workspace,
-                        int64_t workspace_bytes, void* stream) {
+                        int64_t workspace_bytes, void* stream, bool use_scratch = false) {
     if (int rc = check_common(what, A, lda, W, ldw, D_bf16, ldd, M, N, K)) return rc;
     if (M == 0 || N == 0) return 0;
     KBN_CHECK_ARG(K > 0, "%s: K must be positive", what);
@@ -1033,7 +1070,16 @@ static int gemm_nt_impl(const char* what, const void* A, int64_t lda, const floa
     a.vec_store = (reinterpret_cast<uintptr_t>(D_bf16) % 16 == 0) && (ldd % 8 == 0);
     a.expert_ids = nullptr;
     a.M = (int)M; a.N = (int)N; a.K = (int)K; a.E = 1;
-    Schedule sc = dense_schedule(M, N, K, scale_ue8m0, workspace != nullptr);
+    Schedule sc = dense_schedule(M, N, K, scale_ue8m0, workspace != nullptr || use_scratch);
+    if (use_scratch && sc.splits > 1) {
+        KBN_CHECK_ARG(sc.ws_bytes <= kScratchBytes,
+                      "%s: the split plan of M=%lld N=%lld K=%lld needs %lld bytes of scratch, more than the %lld "
+                      "this library holds per GPU",
+                      what, (long long)M, (long long)N, (long long)K, (long long)sc.ws_bytes, (long long)kScratchBytes);
+        workspace = scratch_ptr(what);
+        if (!workspace) return 1;
+        workspace_bytes = kScratchBytes;
+    }
     if (sc.splits > 1) {
         if (workspace_bytes >= sc.ws_bytes) {
             KBN_CHECK_ARG(aligned16(workspace), "%s: workspace must be 16-byte aligned", what);
@@ -1066,6 +1112,16 @@ extern "C" int kbn_fp8_gemm_nt_ws(const void* A, int64_t lda, const float* sA, i
                                   void* workspace, int64_t workspace_bytes, void* stream) {
     return gemm_nt_impl("fp8_gemm_nt_ws", A, lda, sA, sA_stride_m, sA_stride_k, W, ldw, sW, sW_ld, D_bf16, ldd, M,
                         N, K, scale_ue8m0, workspace, workspace_bytes, stream);
+}
+
+extern "C" int64_t kbn_fp8_gemm_nt_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" int kbn_fp8_gemm_nt_noalloc(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
+                                       int64_t sA_stride_k, const void* W, int64_t ldw, const float* sW, int64_t sW_ld,
+                                       void* D_bf16, int64_t ldd, int64_t M, int64_t N, int64_t K, int scale_ue8m0,
+                                       void* stream) {
+    return gemm_nt_impl("fp8_gemm_nt_noalloc", A, lda, sA, sA_stride_m, sA_stride_k, W, ldw, sW, sW_ld, D_bf16, ldd,
+                        M, N, K, scale_ue8m0, nullptr, 0, stream, true);
 }
 
 extern "C" int kbn_fp8_grouped_gemm_nt_contiguous(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,

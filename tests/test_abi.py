@@ -366,3 +366,16 @@ def test_requant_rejects_unsafe_aliasing():
     # fp8 input in place, but the output scales alias the input scales with other strides
     assert L.kbn_fp8_block_requant(w, 0, s, 4, 2, E, N, K, w, s, 8, 2, 1, 1e-4, None) == 1
     assert "different layout" in _err()
+
+
+def test_gemm_noalloc_validates_before_touching_a_device():
+    """The allocation-free GEMM reports its fixed scratch size and rejects
+    bad shapes like the other GEMM entry points, before any device call."""
+    from kb_nano_amd._lib import lib
+    L = lib()
+    assert L.kbn_fp8_gemm_nt_noalloc_scratch_bytes() == 64 << 20
+    assert L.kbn_fp8_gemm_nt_noalloc(None, 128, None, 1, 1, None, 128, None, 1, None, 128, 8, 128, 100, 1,
+                                     None) == 1
+    assert "multiple of 128" in _err()
+    assert L.kbn_fp8_gemm_nt_noalloc(None, 128, None, 1, 1, None, 128, None, 1, None, 128, 0, 128, 128, 1,
+                                     None) == 0
