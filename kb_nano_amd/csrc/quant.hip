@@ -10,15 +10,19 @@
 // wavefront loading kUnroll consecutive 1 KB blocks (4 groups) per operand
 // before any arithmetic; positions advance by a precomputed quotient and
 // remainder, so there is no per-group division.  The absmax of a group is a
-// 4-step DPP max over its 16-lane row; codes leave as one 8-byte store per
-// lane (non-temporal in the SiLU kernel).
+// packed 16-bit max over the lane's bf16 magnitudes, then a 4-step DPP max
+// over its 16-lane row; with UE8M0 scales the codes come from the packed bf16
+// values by the scaled conversion v_cvt_scalef32_pk_fp8_bf16 (no widening to
+// fp32, about 3 VALU instructions per element pair fewer), and leave as one
+// 8-byte store per lane (non-temporal in the SiLU kernel).
 //
 // Numerics follow tasks/baseline/L1/fp8_linear.py:195-215 and
 // tasks/baseline/L1/silu_mul_quant_fp8.py:51-76:
 //   amax = max(max|x|, eps);  s = amax/448 (IEEE divide), rounded up to a
 //   power of two for UE8M0;  q = e4m3_rne(clamp(x/s, +-448)).
-// x/s is an exact multiply by 1/s when s is a power of two, and a correctly
-// rounded division otherwise.
+// x/s is exact when s is a power of two (the scaled conversion, or a multiply
+// by 1/s), and a correctly rounded division otherwise.  NaN inputs give the
+// code 0xFF (gfx950's NaN) whatever their sign.
 //
 // SiLU: silu(g) of a bf16 g has only 65,536 possible inputs, so the fused
 // kernel reads bf16(silu(g)) (correctly rounded, generated at build time by
@@ -39,6 +43,8 @@ __device__ const uint16_t kSiluLut[65536] __attribute__((aligned(16))) = {
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x2 __attribute__((ext_vector_type(2)));
 
 // Launch shape (tunable at build time; defaults are the measured best on MI355X).
 #ifndef KBN_QUANT_PER_CU
@@ -88,26 +94,73 @@ struct GroupCursor {
     }
 };
 
-// bf16(silu(g)) * up for the two bf16 values of each word, rounded to bf16
-// by v_cvt_pk_bf16_f32 and widened back to fp32.
-__device__ __forceinline__ void silu_mul_pair(const uint16_t* __restrict__ lut, uint32_t gw, uint32_t uw, float& y0,
-                                              float& y1) {
+// bf16(silu(g)) * up for the two bf16 values of each word: the exact fp32
+// products rounded to bf16 by one v_cvt_pk_bf16_f32, returned packed.
+__device__ __forceinline__ uint32_t silu_mul_pair(const uint16_t* __restrict__ lut, uint32_t gw, uint32_t uw) {
     const float s0 = __uint_as_float((uint32_t)lut[gw & 0xFFFFu] << 16);
     const float s1 = __uint_as_float((uint32_t)lut[gw >> 16] << 16);
     const bf16x2 p = __builtin_convertvector((f32x2{s0 * bf16lo(uw), s1 * bf16hi(uw)}), bf16x2);
-    const uint32_t pw = __builtin_bit_cast(uint32_t, p);
-    y0 = bf16lo(pw);
-    y1 = bf16hi(pw);
+    return __builtin_bit_cast(uint32_t, p);
 }
 
-// Quantize 8 values owned by this lane (16 lanes per group); returns the
-// group scale (valid in every lane of the group).
+// Largest magnitude of the eight bf16 values in four packed words, as the
+// fp32 bit pattern of that bf16 magnitude.  Magnitude bits of bf16 order
+// like the values they encode (NaN patterns above infinity), so this is a
+// packed 16-bit integer max (v_pk_max_u16) over the sign-cleared words.
+__device__ __forceinline__ uint32_t absmax8_bits(const uint32_t (&w)[4]) {
+    auto mag = [](uint32_t x) { return __builtin_bit_cast(u16x2, x & 0x7FFF7FFFu); };
+    const u16x2 m = __builtin_elementwise_max(__builtin_elementwise_max(mag(w[0]), mag(w[1])),
+                                              __builtin_elementwise_max(mag(w[2]), mag(w[3])));
+    const uint32_t lo = m.x, hi = m.y;
+    return (lo > hi ? lo : hi) << 16;
+}
+
+// Four e4m3 codes of the bf16 pairs w0, w1 divided by the power of two sc,
+// by the gfx950 scaled conversion v_cvt_scalef32_pk_fp8_bf16: for every
+// finite bf16 input and every normal power-of-two sc it gives the codes of
+// v_cvt_pk_fp8_f32(x * (1/sc)) (round to nearest even; checked exhaustively
+// on the device), so no widening to fp32 and no multiply are needed.
+__device__ __forceinline__ uint32_t pack4_e4m3_bf16(uint32_t w0, uint32_t w1, float sc) {
+    s16x2 r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(s16x2{0, 0}, __builtin_bit_cast(bf16x2, w0), sc, false);
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r, __builtin_bit_cast(bf16x2, w1), sc, true);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// Quantize the 8 bf16 values owned by this lane (four packed words; 16
+// lanes per group); returns the group scale (valid in every lane of the
+// group).
 // Codes leave through L2 (plain stores) for the quant kernel: its consumer,
 // the GEMM, reads them next, and at 4096x18432 the cached stores are 7%
 // faster than non-temporal ones (40 against 43 us).  The SiLU kernel's
 // non-temporal stores measure the same either way and are kept.
+//
+// UE8M0 scales: the group absmax comes from the packed magnitudes and the
+// codes from the scaled conversion of the packed values, so the values are
+// never widened to fp32.  A group holding an infinity or a NaN (absmax
+// pattern >= infinity's) takes the general path below, where the absmax
+// ignores NaN as the reference's max does.
 template <bool kUe8m0, bool kNtStore>
-__device__ __forceinline__ float quant8_store(const float (&v)[8], float eps, int sub, uint8_t* __restrict__ qptr) {
+__device__ __forceinline__ float quant8_store(const uint32_t (&w)[4], float eps, int sub,
+                                              uint8_t* __restrict__ qptr) {
+    if constexpr (kUe8m0) {
+        const uint32_t abits = row16_max_u32(absmax8_bits(w));
+        const float sc = ue8m0_ceil_div448(fmaxf(__uint_as_float(abits), eps));
+        // finite absmax and a normal scale (a subnormal one needs eps < 2^-118)
+        if (abits < 0x7F800000u && (__float_as_uint(sc) >> 23) - 1u < 254u) {
+            const u32x2 o{pack4_e4m3_bf16(w[0], w[1], sc), pack4_e4m3_bf16(w[2], w[3], sc)};
+            if constexpr (kNtStore) __builtin_nontemporal_store(o, reinterpret_cast<u32x2*>(qptr + sub * 8));
+            else *reinterpret_cast<u32x2*>(qptr + sub * 8) = o;
+            return sc;
+        }
+    }
+    // general path: the non-UE8M0 contract, and UE8M0 groups with an
+    // infinity, a NaN or a subnormal scale (uniform over the group's 16 lanes)
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = bf16lo(w[i]);
+        v[2 * i + 1] = bf16hi(w[i]);
+    }
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -123,9 +176,20 @@ __device__ __forceinline__ float quant8_store(const float (&v)[8], float eps, in
     // (quant) of kernel time.
     uint32_t lo, hi;
     if (kUe8m0) {
-        const float inv = pow2_recip(sc);
-        lo = pack4_e4m3(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
-        hi = pack4_e4m3(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
+        // an infinite absmax gives an infinite scale: x / inf is +-0 for
+        // finite x (code 0x00 / 0x80) and NaN otherwise, as in the reference
+        if (sc == __builtin_inff()) {
+            uint32_t c[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                c[i] = (fabsf(v[i]) < __builtin_inff()) ? (__float_as_uint(v[i]) >> 24 & 0x80u) : 0xFFu;
+            lo = c[0] | c[1] << 8 | c[2] << 16 | c[3] << 24;
+            hi = c[4] | c[5] << 8 | c[6] << 16 | c[7] << 24;
+        } else {
+            const float inv = pow2_recip(sc);
+            lo = pack4_e4m3(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+            hi = pack4_e4m3(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
+        }
     } else {
         lo = pack4_e4m3(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
         hi = pack4_e4m3(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);
@@ -178,17 +242,16 @@ __global__ __launch_bounds__(kThreads) void group_quant_kernel(const QuantArgs a
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             if (cu[u].row >= row_end) break;  // uniform over the group's 16 lanes; rows grow with u
-            float v[8];
+            uint32_t w[4];
             if constexpr (kSilu) {
-                silu_mul_pair(lut, xa[u].x, xb[u].x, v[0], v[1]);
-                silu_mul_pair(lut, xa[u].y, xb[u].y, v[2], v[3]);
-                silu_mul_pair(lut, xa[u].z, xb[u].z, v[4], v[5]);
-                silu_mul_pair(lut, xa[u].w, xb[u].w, v[6], v[7]);
+                w[0] = silu_mul_pair(lut, xa[u].x, xb[u].x);
+                w[1] = silu_mul_pair(lut, xa[u].y, xb[u].y);
+                w[2] = silu_mul_pair(lut, xa[u].z, xb[u].z);
+                w[3] = silu_mul_pair(lut, xa[u].w, xb[u].w);
             } else {
-                v[0] = bf16lo(xa[u].x); v[1] = bf16hi(xa[u].x); v[2] = bf16lo(xa[u].y); v[3] = bf16hi(xa[u].y);
-                v[4] = bf16lo(xa[u].z); v[5] = bf16hi(xa[u].z); v[6] = bf16lo(xa[u].w); v[7] = bf16hi(xa[u].w);
+                w[0] = xa[u].x; w[1] = xa[u].y; w[2] = xa[u].z; w[3] = xa[u].w;
             }
-            const float sc = quant8_store<kUe8m0, kSilu>(v, a.eps, sub, a.q + (int64_t)cu[u].row * a.ld_q + (int64_t)cu[u].g * kGroup);
+            const float sc = quant8_store<kUe8m0, kSilu>(w, a.eps, sub, a.q + (int64_t)cu[u].row * a.ld_q + (int64_t)cu[u].g * kGroup);
             if (sub == 0) a.s[(int64_t)cu[u].row * a.s_sm + (int64_t)cu[u].g * a.s_sg] = sc;
         }
     }

@@ -194,3 +194,60 @@ def test_silu_mul_quant_golden_fixture(gpu_device):
     for ue8m0, qk, sk in ((True, "q_ue8m0", "s_ue8m0"), (False, "q_fp32", "s_fp32")):
         q, s = _silu_gpu(x, use_ue8m0=ue8m0)
         assert np.array_equal(fp8_codes(q), d[qk]) and np.array_equal(s.cpu().numpy(), d[sk])
+
+
+def _canon_nan(codes: np.ndarray) -> np.ndarray:
+    """e4m3fn has two NaN codes (0x7F, 0xFF); gfx950's conversion always
+    gives 0xFF, the oracle keeps the sign.  Both mean NaN."""
+    c = codes.copy()
+    c[(c & 0x7F) == 0x7F] = 0xFF
+    return c
+
+
+def test_quant_nonfinite_groups(gpu_device):
+    """Groups holding +-inf or NaN: the absmax ignores NaN (the reference's
+    max), an infinite absmax gives an infinite scale and then codes +-0 for
+    the group's finite values (x / inf) and NaN for the rest; a group of
+    only NaN gets the eps scale.  Codes equal the oracle's up to the NaN
+    code's sign bit."""
+    x = seeded_bf16((16, 1024), seed=21).float().numpy()
+    x[0, 5] = np.inf
+    x[1, 130] = -np.inf
+    x[2, 300] = np.nan
+    x[3, :128] = np.nan
+    x[4, 513] = np.inf
+    x[4, 514] = np.nan
+    x[5, 640:768] = np.inf
+    x[6, 900] = -np.inf
+    x[6, 901] = np.inf
+    bits = oracle.f32_to_bf16_bits(x)
+    qo, so = oracle.quant_group128(bits)
+    q, s = _quant_gpu(from_bits(bits, gpu_device))
+    assert np.array_equal(s.cpu().numpy(), so)
+    assert np.array_equal(_canon_nan(fp8_codes(q)), _canon_nan(qo))
+    assert np.isinf(so[0, 0]) and np.all(qo[0, :128][np.isfinite(x[0, :128])] & 0x7F == 0)
+
+
+def test_silu_mul_quant_nonfinite(gpu_device):
+    """SiLU*Mul + quant with infinite and NaN gates and ups (silu(inf) = inf,
+    silu(-inf) = -0, inf * 0 = NaN): codes equal the oracle's up to the NaN
+    code's sign bit, scales exactly."""
+    from kb_nano_amd import _ops
+    M, Nh = 8, 512
+    x = seeded_bf16((M, 2 * Nh), seed=23).float().numpy()
+    x[0, 3] = np.inf                 # gate inf, up finite
+    x[1, 200] = -np.inf              # gate -inf -> silu -0
+    x[2, 7] = np.inf
+    x[2, Nh + 7] = 0.0               # inf * 0 -> NaN
+    x[3, Nh + 100] = np.nan          # up NaN
+    x[4, 260] = np.nan               # gate NaN
+    x[5, Nh + 400] = -np.inf         # up -inf
+    bits = oracle.f32_to_bf16_bits(x)
+    qo, so = oracle.silu_mul_quant(bits)
+    inp = from_bits(bits, gpu_device)
+    q = torch.empty(M, Nh, dtype=torch.float8_e4m3fn, device=gpu_device)
+    s = torch.empty(Nh // 128, M, device=gpu_device).t()
+    _ops.silu_mul_quant_fp8(inp, q, s)
+    torch.cuda.synchronize()
+    assert np.array_equal(s.cpu().numpy(), so)
+    assert np.array_equal(_canon_nan(fp8_codes(q)), _canon_nan(qo))
