@@ -202,6 +202,63 @@ def bench_decode(steps, warmup, dev):
     return out
 
 
+def bench_linear(steps, warmup, dev):
+    """Fp8Linear.forward end to end (1x128 quant + block-scaled GEMM, the hot
+    loop of the reference's kernel runner, bench/kernels/runner.py:160-193),
+    at config 1 and the config-5 qkv shape at M in {1, 8, 32, 64}:
+      eager_us       GPU time per call of back-to-back eager calls (events)
+      eager_host_us  host time per eager call (launch path, no synchronisation)
+      graph_us       time per call replayed from a captured HIP graph
+    The config-5 weights (84 MB) rotate over copies that exceed the 256 MB
+    Infinity Cache; the output buffers are installed so a graph's output
+    stays put (the reference's decode buffers)."""
+    import torch
+    from kb_nano_amd import Fp8Linear, synthetic
+    out = []
+    cases = [("cfg1", 64, 2048, 2048, 0)] + [("cfg5_qkv", M, 10240, 8192, 4) for M in (1, 8, 32, 64)]
+    weights = {}
+    for name, M, N, K, seed in cases:
+        if (N, K) not in weights:
+            w, sw = synthetic.dense_weight(N, K, seed=seed, device=dev)
+            n = _copies_for(N * K, 1) if N * K > 64 * 2 ** 20 else 1
+            weights[(N, K)] = [(w.clone(), sw.clone()) for _ in range(n)]
+            del w, sw
+        ws = weights[(N, K)]
+        n = len(ws)
+        x = synthetic.bf16_normal((M, K), seed=seed + M).to(dev)
+        lins = [Fp8Linear() for _ in range(n)]
+        for lin in lins:
+            lin._ensure_buffers(max(M, 64), K, N, dev)
+        ms_eager = _events_time_ms(lambda i: lins[i % n](x, *ws[i % n]), steps, warmup)
+        torch.cuda.synchronize()
+        reps = max(steps, 50)
+        t0 = time.perf_counter()
+        for i in range(reps):
+            lins[i % n](x, *ws[i % n])
+        host_us = (time.perf_counter() - t0) / reps * 1e6
+        torch.cuda.synchronize()
+        # one graph holds 8 or more calls (a decode step's worth of layers),
+        # so the graph launch itself is spread as in a captured model step
+        per_graph = max(n, 8)
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):          # warm the allocator on the capture stream
+            for i in range(per_graph):
+                lins[i % n](x, *ws[i % n])
+        torch.cuda.current_stream().wait_stream(side)
+        with torch.cuda.graph(g):
+            for i in range(per_graph):
+                lins[i % n](x, *ws[i % n])
+        ms_graph = _events_time_ms(lambda i: g.replay(), max(2, steps // 2), warmup) / per_graph
+        del g
+        out.append({"case": name, "M": M, "N": N, "K": K, "eager_us": ms_eager * 1e3, "eager_host_us": host_us,
+                    "graph_us": ms_graph * 1e3, "rotated_copies": n})
+    del weights
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_moe(steps, warmup, dev):
     """Config 4: 4096 tokens, hidden 7168, 256 experts, top-8 from seeded
     softmax logits, per-expert rows padded to 128; gate_up (N=4096, K=7168)
@@ -427,7 +484,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default="all",
-                    help="comma list of extra sections: quant,norm,requant,dsv3,moe,moe_sorted,decode (default all; 'none' = headline only)")
+                    help="comma list of extra sections: quant,norm,requant,linear,dsv3,moe,moe_sorted,decode (default all; 'none' = headline only)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three 1 GiB device copies (reference for rocprofv3 byte counters)")
@@ -450,7 +507,7 @@ def main():
     from kb_nano_amd._lib import require_gfx950
     require_gfx950(0)
 
-    sections = {"quant", "norm", "requant", "dsv3", "moe", "moe_sorted", "decode"} if args.only == "all" else \
+    sections = {"quant", "norm", "requant", "linear", "dsv3", "moe", "moe_sorted", "decode"} if args.only == "all" else \
         set() if args.only == "none" else set(args.only.split(","))
 
     torch.cuda.synchronize()
@@ -470,6 +527,11 @@ def main():
     if "requant" in sections:
         extra["weight_requant_dsv3_experts"] = bench_requant(**small)
         print(f"[bench] weight requant: {extra['weight_requant_dsv3_experts']}", file=sys.stderr, flush=True)
+    if "linear" in sections:
+        extra["fp8_linear_forward"] = bench_linear(**small)
+        for r in extra["fp8_linear_forward"]:
+            print(f"[bench] Fp8Linear {r['case']} M={r['M']}: eager {r['eager_us']:.1f} us (host {r['eager_host_us']:.1f} us)"
+                  f", graph {r['graph_us']:.1f} us", file=sys.stderr, flush=True)
     if "dsv3" in sections:
         extra["gemm_dsv3_cfg3"] = bench_dsv3(**small)
         for r in extra["gemm_dsv3_cfg3"]:

@@ -107,6 +107,22 @@ int kbn_fp8_gemm_nt_ws(const void* A, int64_t lda, const float* sA, int64_t sA_s
                        int scale_ue8m0, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Fp8Linear.forward's quant + GEMM in one call (tasks/baseline/L1/
+ * fp8_linear.py:436-445: per_token_group_quant_fp8 into column-major scales,
+ * then fp8_gemm_nt): kbn_per_token_group_quant_fp8(x -> q, scale; eps,
+ * quant_ue8m0), then kbn_fp8_gemm_nt_ws(q, scale, W, sW -> D; scale_ue8m0,
+ * workspace), launched on `stream` in that order.  The arguments of both
+ * are checked before either launches.  One host crossing instead of two,
+ * for the eager decode path where the launch path, not the GPU, sets the
+ * time per layer.
+ */
+int kbn_fp8_linear_forward(const void* x_bf16, int64_t M, int64_t K, int64_t ld_x,
+                           void* q_fp8, int64_t ld_q, float* scale, int64_t s_stride_m, int64_t s_stride_g,
+                           float eps, int quant_ue8m0, const void* W, int64_t ldw, const float* sW, int64_t sW_ld,
+                           void* D_bf16, int64_t ldd, int64_t N, int scale_ue8m0,
+                           void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * kbn_fp8_gemm_nt_ws without any allocation by the caller: the split-K slabs
  * go to a device array the library holds per GPU (`scratch`, of
  * kbn_fp8_gemm_nt_noalloc_scratch_bytes() = 64 MiB, kept until the process

@@ -28,20 +28,31 @@ GROUP = 128
 QUANT_EPS = 1e-10  # tasks/baseline/L1/fp8_linear.py:44
 
 
+# The per-call host path is kept short (it is paid on every eager launch):
+# device indices come from Tensor.get_device() and the launch stream from
+# the raw current-stream query, about 0.1 us each where torch.cuda's
+# device/stream objects cost about 2 us.
+_raw_stream = torch._C._cuda_getCurrentRawStream
+_GFX950_DEVICES: set = set()
+
+
 def _stream(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """Raw handle of the current HIP stream of t's device."""
+    return _raw_stream(t.get_device())
 
 
 def _dev_check(what: str, *tensors: torch.Tensor) -> int:
-    dev = tensors[0].device
-    if dev.type != "cuda":
-        raise RuntimeError(f"{what}: tensors must be on a ROCm GPU, got {dev} (no CPU path)")
-    for t in tensors[1:]:
-        if t.device != dev:
-            raise RuntimeError(f"{what}: all tensors must be on {dev}, got {t.device}")
-    idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    require_gfx950(idx)
-    if idx != torch.cuda.current_device():
+    """All tensors on one gfx950 GPU, the current device; returns its index."""
+    idx = tensors[0].get_device()
+    if idx < 0:
+        raise RuntimeError(f"{what}: tensors must be on a ROCm GPU, got {tensors[0].device} (no CPU path)")
+    for t in tensors:
+        if t.get_device() != idx:
+            raise RuntimeError(f"{what}: all tensors must be on {tensors[0].device}, got {t.device}")
+    if idx not in _GFX950_DEVICES:
+        require_gfx950(idx)
+        _GFX950_DEVICES.add(idx)
+    if idx != torch._C._cuda_getDevice():
         raise RuntimeError(f"{what}: tensors are on cuda:{idx} but the current device is "
                            f"cuda:{torch.cuda.current_device()}; wrap the call in torch.cuda.device()")
     return idx
@@ -75,7 +86,7 @@ def per_token_group_quant_fp8(x: torch.Tensor, out_fp8: torch.Tensor, out_scale:
     """1x128 quant of bf16 ``x [M,K]`` into ``out_fp8 [M,K]`` and ``out_scale
     [M,K/128]`` (any strides for the scales, e.g. column-major)."""
     what = "per_token_group_quant_fp8"
-    _dev_check(what, x, out_fp8, out_scale)
+    idx = _dev_check(what, x, out_fp8, out_scale)
     _dtype_check(what, x, torch.bfloat16, "input")
     _dtype_check(what, out_fp8, FP8, "output_fp8")
     _dtype_check(what, out_scale, torch.float32, "output_scale")
@@ -88,10 +99,12 @@ def per_token_group_quant_fp8(x: torch.Tensor, out_fp8: torch.Tensor, out_scale:
         raise ValueError(f"{what}: output_scale must be {(M, K // GROUP)}, got {tuple(out_scale.shape)}")
     if x.stride(1) != 1 or out_fp8.stride(1) != 1:
         raise ValueError(f"{what}: input and output rows must be contiguous")
-    check(lib().kbn_per_token_group_quant_fp8(
+    rc = lib().kbn_per_token_group_quant_fp8(
         x.data_ptr(), M, K, x.stride(0), out_fp8.data_ptr(), out_fp8.stride(0),
         out_scale.data_ptr(), out_scale.stride(0), out_scale.stride(1),
-        float(eps), int(bool(use_ue8m0)), _stream(x)), what)
+        float(eps), int(bool(use_ue8m0)), _raw_stream(idx))
+    if rc:
+        check(rc, what)
 
 
 def silu_mul_quant_fp8(inp: torch.Tensor, out_fp8: torch.Tensor, out_scale: torch.Tensor,
@@ -119,7 +132,7 @@ def fp8_gemm_nt(q_input: torch.Tensor, input_scale: torch.Tensor, weight: torch.
                 weight_scale: torch.Tensor, output: torch.Tensor, use_ue8m0: bool | None = None) -> None:
     """output[M,N] (bf16) = block-scaled q_input[M,K] x weight[N,K]^T."""
     what = "fp8_gemm_nt"
-    _dev_check(what, q_input, input_scale, weight, weight_scale, output)
+    idx = _dev_check(what, q_input, input_scale, weight, weight_scale, output)
     _dtype_check(what, q_input, FP8, "q_input")
     _dtype_check(what, weight, FP8, "weight")
     _dtype_check(what, input_scale, torch.float32, "input_scale")
@@ -145,23 +158,65 @@ def fp8_gemm_nt(q_input: torch.Tensor, input_scale: torch.Tensor, weight: torch.
     # small-M / few-tile shapes split K over more workgroups; the fp32
     # partials live in a workspace from the caching allocator (stream-ordered
     # on the launch stream, so concurrent streams never share one)
-    ws_bytes = _gemm_workspace_bytes(L, output.device, M, N, K, ue8m0)
+    ws_bytes = _gemm_workspace_bytes(L, idx, M, N, K, ue8m0)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=output.device) if ws_bytes else None
-    check(L.kbn_fp8_gemm_nt_ws(
+    rc = L.kbn_fp8_gemm_nt_ws(
         q_input.data_ptr(), q_input.stride(0), input_scale.data_ptr(), input_scale.stride(0), input_scale.stride(1),
         weight.data_ptr(), weight.stride(0), weight_scale.data_ptr(), weight_scale.stride(0),
         output.data_ptr(), output.stride(0), M, N, K, int(ue8m0),
-        ws.data_ptr() if ws is not None else None, ws_bytes, _stream(output)), what)
+        ws.data_ptr() if ws is not None else None, ws_bytes, _raw_stream(idx))
+    if rc:
+        check(rc, what)
+
+
+def fp8_linear_forward(x: torch.Tensor, q_buf: torch.Tensor, s_buf: torch.Tensor, weight: torch.Tensor,
+                       weight_scale: torch.Tensor, out_buf: torch.Tensor, use_ue8m0: bool | None = None) -> None:
+    """Fp8Linear.forward's launches in one library call: the 1x128 UE8M0
+    quant of ``x [M, K]`` into rows [0, M) of ``q_buf`` and ``s_buf`` (any
+    strides, e.g. a column-major buffer of more rows), then
+    ``out_buf[:M] = block-scaled q x weight^T``.  Buffers may hold more than
+    M rows; only the first M are written."""
+    what = "fp8_linear_forward"
+    idx = _dev_check(what, x, q_buf, s_buf, weight, weight_scale, out_buf)
+    if (x.dtype != torch.bfloat16 or q_buf.dtype != FP8 or weight.dtype != FP8 or s_buf.dtype != torch.float32
+            or weight_scale.dtype != torch.float32 or out_buf.dtype != torch.bfloat16):
+        raise TypeError(f"{what}: expected bf16 x, fp8 q_buf/weight, fp32 scales, bf16 out_buf")
+    M, K = x.shape
+    N, K2 = weight.shape
+    KB, NB = -(-K // GROUP), -(-N // GROUP)
+    if (K2 != K or K % GROUP or q_buf.shape[0] < M or q_buf.shape[1] != K or s_buf.shape[0] < M
+            or s_buf.shape[1] != KB or out_buf.shape[0] < M or out_buf.shape[1] != N or weight_scale.dim() != 2
+            or weight_scale.shape[0] < NB or weight_scale.shape[1] < KB):
+        raise ValueError(f"{what}: shapes x {tuple(x.shape)}, q {tuple(q_buf.shape)}, s {tuple(s_buf.shape)}, "
+                         f"W {tuple(weight.shape)}, sW {tuple(weight_scale.shape)}, out {tuple(out_buf.shape)}")
+    if x.stride(1) != 1 or q_buf.stride(1) != 1 or weight.stride(1) != 1 or out_buf.stride(1) != 1 \
+            or weight_scale.stride(1) != 1:
+        raise ValueError(f"{what}: rows must be contiguous")
+    if M == 0 or N == 0:
+        return
+    ue8m0 = is_e8m0_used() if use_ue8m0 is None else bool(use_ue8m0)
+    L = lib()
+    ws_bytes = _gemm_workspace_bytes(L, idx, M, N, K, ue8m0)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=out_buf.device) if ws_bytes else None
+    rc = L.kbn_fp8_linear_forward(
+        x.data_ptr(), M, K, x.stride(0), q_buf.data_ptr(), q_buf.stride(0), s_buf.data_ptr(), s_buf.stride(0),
+        s_buf.stride(1), QUANT_EPS, 1, weight.data_ptr(), weight.stride(0), weight_scale.data_ptr(),
+        weight_scale.stride(0), out_buf.data_ptr(), out_buf.stride(0), N, int(ue8m0),
+        ws.data_ptr() if ws is not None else None, ws_bytes, _raw_stream(idx))
+    if rc:
+        check(rc, what)
 
 
 _WS_CACHE: dict = {}
 
 
-def _gemm_workspace_bytes(L, device, M, N, K, ue8m0) -> int:
-    key = (device.index, M, N, K, ue8m0)
+def _gemm_workspace_bytes(L, idx: int, M, N, K, ue8m0) -> int:
+    """Split-K workspace of a shape on device idx (the plan depends on the
+    device's CU count); cached per (device, shape)."""
+    key = (idx, M, N, K, ue8m0)
     n = _WS_CACHE.get(key)
     if n is None:
-        with torch.cuda.device(device):
+        with torch.cuda.device(idx):
             n = int(L.kbn_fp8_gemm_nt_workspace_bytes(M, N, K, int(ue8m0)))
         _WS_CACHE[key] = n
     return n

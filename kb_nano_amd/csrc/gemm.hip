@@ -1114,6 +1114,33 @@ extern "C" int kbn_fp8_gemm_nt_ws(const void* A, int64_t lda, const float* sA, i
                         N, K, scale_ue8m0, workspace, workspace_bytes, stream);
 }
 
+extern "C" int kbn_per_token_group_quant_fp8(const void* x_bf16, int64_t M, int64_t K, int64_t ld_x, void* q_fp8,
+                                             int64_t ld_q, float* scale, int64_t s_stride_m, int64_t s_stride_g,
+                                             float eps, int use_ue8m0, void* stream);
+
+// Fp8Linear.forward's two launches behind one call: the 1x128 quant of the
+// bf16 input into q / scale, then the block-scaled GEMM of q with W.  Every
+// argument of both is checked before either launches.
+extern "C" int kbn_fp8_linear_forward(const void* x_bf16, int64_t M, int64_t K, int64_t ld_x, void* q_fp8,
+                                      int64_t ld_q, float* scale, int64_t s_stride_m, int64_t s_stride_g, float eps,
+                                      int quant_ue8m0, const void* W, int64_t ldw, const float* sW, int64_t sW_ld,
+                                      void* D_bf16, int64_t ldd, int64_t N, int scale_ue8m0, void* workspace,
+                                      int64_t workspace_bytes, void* stream) {
+    const char* what = "fp8_linear_forward";
+    if (int rc = check_common(what, q_fp8, ld_q, W, ldw, D_bf16, ldd, M, N, K)) return rc;
+    if (M == 0 || N == 0) return 0;
+    KBN_CHECK_ARG(K > 0 && x_bf16 && scale && sW, "%s: null pointer or empty K", what);
+    KBN_CHECK_ARG(aligned16(x_bf16) && ld_x % 8 == 0 && ld_x >= K, "%s: input rows must be 16-byte aligned", what);
+    KBN_CHECK_ARG(M <= 0x3FFFFFFFLL, "%s: shape too large", what);
+    KBN_CHECK_ARG(sW_ld >= K / kGroup, "%s: weight-scale row stride %lld < K/128", what, (long long)sW_ld);
+    if (int rc = check_scale_ranges(what, M, K, s_stride_m, s_stride_g, (N + kGroup - 1) / kGroup, sW_ld)) return rc;
+    if (int rc = kbn_per_token_group_quant_fp8(x_bf16, M, K, ld_x, q_fp8, ld_q, scale, s_stride_m, s_stride_g, eps,
+                                               quant_ue8m0, stream))
+        return rc;
+    return gemm_nt_impl(what, q_fp8, ld_q, scale, s_stride_m, s_stride_g, W, ldw, sW, sW_ld, D_bf16, ldd, M, N, K,
+                        scale_ue8m0, workspace, workspace_bytes, stream);
+}
+
 extern "C" int64_t kbn_fp8_gemm_nt_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
 extern "C" int kbn_fp8_gemm_nt_noalloc(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,

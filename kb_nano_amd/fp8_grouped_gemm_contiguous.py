@@ -20,7 +20,7 @@ import os
 import torch
 import torch.nn as nn
 
-from . import _ops  # noqa: F401  (registers torch.ops.kb_nano_fp8_moe.*)
+from . import _ops  # also registers torch.ops.kb_nano_fp8_moe.*
 from ._ops import is_e8m0_used
 
 _ALIGNMENT = 128
@@ -66,5 +66,9 @@ class Fp8GroupedGemmContiguous(nn.Module):
 
     def forward(self, a_fp8: torch.Tensor, a_scale: torch.Tensor, b_fp8: torch.Tensor,
                 b_scale: torch.Tensor, c_bf16: torch.Tensor, expert_ids: torch.Tensor) -> None:
-        torch.ops.kb_nano_fp8_moe.m_grouped_gemm_nt_contiguous(
-            a_fp8, a_scale, b_fp8, b_scale, c_bf16, expert_ids, self._disable_ue8m0_cast)
+        if torch.compiler.is_compiling():
+            torch.ops.kb_nano_fp8_moe.m_grouped_gemm_nt_contiguous(
+                a_fp8, a_scale, b_fp8, b_scale, c_bf16, expert_ids, self._disable_ue8m0_cast)
+        else:   # eager: the same launch without the dispatcher round trip
+            _ops.m_grouped_gemm_nt_contiguous(a_fp8, a_scale, b_fp8, b_scale, c_bf16, expert_ids,
+                                              self._disable_ue8m0_cast)

@@ -52,14 +52,17 @@ class PerTokenGroupQuantFp8(nn.Module):
     strides (row-major by default, column-major for the dense GEMM)."""
 
     def forward(self, x: torch.Tensor, out_fp8: torch.Tensor, out_scale: torch.Tensor) -> None:
-        torch.ops.kb_nano_fp8.per_token_group_quant_fp8(
-            x if x.is_contiguous() else x.contiguous(), out_fp8, out_scale)
+        x = x if x.is_contiguous() else x.contiguous()
+        if torch.compiler.is_compiling():
+            torch.ops.kb_nano_fp8.per_token_group_quant_fp8(x, out_fp8, out_scale)
+        else:   # eager: the same launch without the dispatcher round trip
+            _ops.per_token_group_quant_fp8(x, out_fp8, out_scale)
 
 
 def _alloc_colmajor_scale(M: int, num_groups: int, device: torch.device) -> torch.Tensor:
     """fp32 scales exposed as [M, num_groups] over [num_groups, M] storage:
     strides (1, M), element (m, g) at g*M + m."""
-    return torch.empty((num_groups, M), device=device, dtype=torch.float32).t()
+    return torch.empty_strided((M, num_groups), (1, max(M, 1)), device=device, dtype=torch.float32)
 
 
 class _Fp8PrefillBufs:
@@ -113,21 +116,27 @@ class Fp8Linear(nn.Module):
         G = (K + self.BLOCK_SIZE - 1) // self.BLOCK_SIZE
         dev = x2.device
 
-        bufs = None
-        if not torch.compiler.is_compiling():
-            if self._a_buf is not None and M <= self._a_buf.shape[0]:
-                bufs = (self._a_buf, self._o_buf)
-            elif self._pf is not None and M <= self._pf.a.shape[0]:
-                bufs = (self._pf.a, self._pf.o)
-        if bufs is not None:
-            q_input, output = bufs[0][:M], bufs[1][:M]
-        else:
+        if torch.compiler.is_compiling():
+            # opaque ops for the compiler (the reference's op boundary)
             q_input = torch.empty(M, K, dtype=FP8, device=dev)
+            input_scale = _alloc_colmajor_scale(M, G, dev)
             output = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-        input_scale = _alloc_colmajor_scale(M, G, dev)
-
-        torch.ops.kb_nano_fp8.per_token_group_quant_fp8(x2, q_input, input_scale, True)
-        torch.ops.kb_nano_fp8.fp8_gemm_nt(q_input, input_scale, weight_fp8, weight_scale_inv, output)
+            torch.ops.kb_nano_fp8.per_token_group_quant_fp8(x2, q_input, input_scale, True)
+            torch.ops.kb_nano_fp8.fp8_gemm_nt(q_input, input_scale, weight_fp8, weight_scale_inv, output)
+        else:
+            # eager: both launches through one library call; the installed
+            # decode / prefill buffers (scales included: any row stride works)
+            # are written in place without slicing, else fresh ones
+            if self._a_buf is not None and M <= self._a_buf.shape[0]:
+                q_buf, s_buf, o_buf = self._a_buf, self._s_buf, self._o_buf
+            elif self._pf is not None and M <= self._pf.a.shape[0]:
+                q_buf, s_buf, o_buf = self._pf.a, self._pf.s, self._pf.o
+            else:
+                q_buf = torch.empty(M, K, dtype=FP8, device=dev)
+                s_buf = _alloc_colmajor_scale(M, G, dev)
+                o_buf = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+            _ops.fp8_linear_forward(x2, q_buf, s_buf, weight_fp8, weight_scale_inv, o_buf)
+            output = o_buf if o_buf.shape[0] == M else o_buf[:M]
 
         if bias is not None:
             output = output + bias

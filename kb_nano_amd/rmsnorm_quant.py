@@ -19,7 +19,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from . import _ops  # noqa: F401  (registers torch.ops.kb_nano_norm.*)
+from . import _ops  # also registers torch.ops.kb_nano_norm.*
 from ._ops import FP8, GROUP
 
 _FP8_GROUP_SIZE = GROUP
@@ -30,7 +30,8 @@ def _outputs(input: torch.Tensor):
     num_tokens = input.numel() // hidden_size
     num_groups = (hidden_size + _FP8_GROUP_SIZE - 1) // _FP8_GROUP_SIZE
     output_fp8 = torch.empty(num_tokens, hidden_size, dtype=FP8, device=input.device)
-    output_scales = torch.empty(num_groups, num_tokens, dtype=torch.float32, device=input.device).transpose(0, 1)
+    output_scales = torch.empty_strided((num_tokens, num_groups), (1, max(num_tokens, 1)), dtype=torch.float32,
+                                        device=input.device)
     return output_fp8, output_scales
 
 
@@ -41,7 +42,10 @@ class RMSNormFP8Quant(nn.Module):
 
     def forward(self, input: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> tuple[torch.Tensor, torch.Tensor]:
         output_fp8, output_scales = _outputs(input)
-        torch.ops.kb_nano_norm.rmsnorm_fp8_quant(output_fp8, output_scales, input, weight, eps)
+        if torch.compiler.is_compiling():
+            torch.ops.kb_nano_norm.rmsnorm_fp8_quant(output_fp8, output_scales, input, weight, eps)
+        else:   # eager: the same launch without the dispatcher round trip
+            _ops.rmsnorm_fp8_quant(output_fp8, output_scales, input, weight, eps)
         return output_fp8, output_scales
 
 
@@ -53,5 +57,8 @@ class FusedAddRMSNormFP8Quant(nn.Module):
     def forward(self, input: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
                 eps: float = 1e-6) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         output_fp8, output_scales = _outputs(input)
-        torch.ops.kb_nano_norm.fused_add_rmsnorm_fp8_quant(output_fp8, output_scales, input, residual, weight, eps)
+        if torch.compiler.is_compiling():
+            torch.ops.kb_nano_norm.fused_add_rmsnorm_fp8_quant(output_fp8, output_scales, input, residual, weight, eps)
+        else:   # eager: the same launch without the dispatcher round trip
+            _ops.rmsnorm_fp8_quant(output_fp8, output_scales, input, weight, eps, residual=residual)
         return output_fp8, output_scales, residual

@@ -13,7 +13,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from . import _ops  # noqa: F401  (registers torch.ops.kb_nano_fp8.*)
+from . import _ops  # also registers torch.ops.kb_nano_fp8.*
 from ._ops import FP8, GROUP
 
 _FP8_INFO = torch.finfo(FP8)
@@ -34,7 +34,10 @@ class SiluMulQuantFp8(nn.Module):
         assert N_2 % _GROUP_SIZE == 0, f"N//2={N_2} must be divisible by {_GROUP_SIZE}"
         if output is None:
             output = torch.empty((M, N_2), dtype=FP8, device=input.device)
-        output_scales = torch.empty((N_2 // _GROUP_SIZE, M), dtype=torch.float32,
-                                    device=input.device).transpose(0, 1)
-        torch.ops.kb_nano_fp8.silu_mul_quant_fp8(input, output, output_scales, bool(use_ue8m0), float(eps))
+        output_scales = torch.empty_strided((M, N_2 // _GROUP_SIZE), (1, M), dtype=torch.float32,
+                                            device=input.device)
+        if torch.compiler.is_compiling():
+            torch.ops.kb_nano_fp8.silu_mul_quant_fp8(input, output, output_scales, bool(use_ue8m0), float(eps))
+        else:   # eager: the same launch without the dispatcher round trip
+            _ops.silu_mul_quant_fp8(input, output, output_scales, bool(use_ue8m0), float(eps))
         return output, output_scales
