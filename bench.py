@@ -472,10 +472,105 @@ def cpu_baseline_silu():
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
     nbytes = M * 2 * Nh * 2 + M * Nh + 4 * M * (Nh // 128)
-    cores = int(os.environ.get("OMP_NUM_THREADS", 0)) or len(os.sched_getaffinity(0))
+    cores = _cpu_threads()
     return {"value": nbytes / t / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
             "sample": f"full config-2 workload (8192 x 36864 bf16) through oracle/kbn_oracle.c "
                       f"(OpenMP, {cores} threads), median of 3 runs = {t:.3f} s"}
+
+
+def _cpu_threads() -> int:
+    n = len(os.sched_getaffinity(0))
+    omp = int(os.environ.get("OMP_NUM_THREADS", 0) or 0)
+    return min(n, omp) if omp else n
+
+
+def _median_time(fn, reps=3):
+    """Median of `reps` wall-clock runs (one run when a run exceeds 30 s)."""
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if times[-1] > 30:
+            break
+    return statistics.median(times), len(times)
+
+
+def cpu_host_info() -> dict:
+    import subprocess
+    import torch
+    model = ""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        model = next((ln.split(":", 1)[1].strip() for ln in out.splitlines() if ln.startswith("Model name")), "")
+    except (OSError, subprocess.SubprocessError):
+        pass
+    info = torch.__config__.parallel_info().strip().splitlines()
+    return {"cpu_model": model, "threads": torch.get_num_threads(),
+            "parallel_info": [ln.strip() for ln in info if ln.strip()][:8]}
+
+
+def _cpu_block_quant(w_bf16):
+    """128x128 UE8M0 block quantization of a CPU bf16 weight in torch (input
+    preparation for the CPU baseline; the GPU rows quantize on the device):
+    fp8 codes and fp32 block scales."""
+    import torch
+    w = w_bf16.float()
+    R, C = w.shape
+    b = w.view(R // 128, 128, C // 128, 128)
+    s = torch.pow(2.0, torch.ceil(torch.log2(b.abs().amax(dim=(1, 3)).clamp_min(1e-10) / 448.0)))
+    q = (b / s[:, None, :, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(R, C)
+    return q, s
+
+
+def cpu_baselines_extra() -> dict:
+    """The reference's CPU path (tasks/reference/L1/fp8_linear.py, restated
+    in torch in oracle/) timed on the host cores, on the configs the GPU rows
+    report: the dense GEMM in its literal form (bf16 input, :96-104) and with
+    the 1x128-quantized input the GPU computes on, at config 1 and at the
+    DeepSeek-V3 o_proj shape at M = 128; the per-token quant (:41-64) at a
+    config-3 activation shape; the contiguous grouped GEMM as a per-expert
+    loop over a bounded sample of config 4's experts.  Median of 3 runs."""
+    import torch
+
+    import oracle
+    from kb_nano_amd import synthetic
+    torch.set_num_threads(_cpu_threads())
+    res = {"host": cpu_host_info()}
+    for tag, M, N, K in (("cfg1", 64, 2048, 2048), ("dsv3_o_proj_M128", 128, 7168, 16384)):
+        a = synthetic.bf16_normal((M, K), seed=0)
+        wc, ws = _cpu_block_quant(synthetic.bf16_normal((N, K), seed=1, std=synthetic.W_STD))
+        q, sc = oracle.torch_quant_group128(a)
+        a_dq = oracle.torch_dequant_group128(q, sc).bfloat16()
+        flop = 2.0 * M * N * K
+        for form, x in (("literal_bf16_input", a), ("quantized_input", a_dq)):
+            t, n = _median_time(lambda: oracle.torch_dense_linear(x, wc, ws))
+            res[f"gemm_{tag}_{form}"] = {"M": M, "N": N, "K": K, "s": t, "GFLOP/s": flop / t / 1e9, "runs": n}
+    M, K = 4096, 7168
+    x = synthetic.bf16_normal((M, K), seed=2)
+    t, n = _median_time(lambda: oracle.torch_quant_group128(x))
+    nbytes = M * K * 3 + 4 * M * (K // 128)
+    res["quant_4096x7168"] = {"s": t, "GB/s": nbytes / t / 1e9, "runs": n}
+    # grouped GEMM: config 4's first 8 experts (their routed rows, padded as in
+    # the contiguous layout), gate_up N = 4096, K = 7168
+    c = synthetic.MOE_CFG4
+    ids, _ = synthetic.moe_routing()
+    sel = list(range(8))
+    counts = [int((ids == e).sum()) for e in sel]
+    rows = sum(-(-n_ // 128) * 128 for n_ in counts)
+    expert_ids = torch.cat([torch.cat([torch.full((n_,), i, dtype=torch.int32),
+                                       torch.full((-(-n_ // 128) * 128 - n_,), -1, dtype=torch.int32)])
+                            for i, n_ in enumerate(counts)])
+    a = synthetic.bf16_normal((rows, c["H"]), seed=3)
+    qa, sa = oracle.torch_quant_group128(a)
+    wq, wsc = zip(*[_cpu_block_quant(synthetic.bf16_normal((c["I2"], c["H"]), seed=3 * 100003 + e,
+                                                            std=synthetic.W_STD)) for e in sel])
+    wq, wsc = torch.stack(wq), torch.stack(wsc)
+    t, n = _median_time(lambda: oracle.torch_grouped_linear(qa, sa, wq, wsc, expert_ids))
+    flop = 2.0 * sum(counts) * c["I2"] * c["H"]
+    res["moe_gate_up_8_experts"] = {"valid_rows": sum(counts), "s": t, "GFLOP/s": flop / t / 1e9, "runs": n,
+                                    "sample": "config 4's experts 0-7 (seed-0 routing), gate_up N=4096 K=7168"}
+    return res
 
 
 def main():
@@ -550,6 +645,9 @@ def main():
                   f"{r['frac_roof'] * 100:.1f}% roof", file=sys.stderr, flush=True)
 
     cpu = None if args.no_cpu_baseline else cpu_baseline_silu()
+    if not args.no_cpu_baseline:
+        extra["cpu_reference_path"] = cpu_baselines_extra()
+        print(f"[bench] cpu reference path: {extra['cpu_reference_path']}", file=sys.stderr, flush=True)
     value = head["gbs"]
     line = {
         "metric": METRIC,

@@ -532,3 +532,74 @@ def rmsnorm_quant(x_bits: np.ndarray, w_bits: np.ndarray, eps: float = 1e-6, res
     if rc:
         raise ValueError(f"orc_rmsnorm_quant failed ({rc})")
     return (q, s) if r is None else (q, s, r, x)
+
+
+# ---------------------------------------------------------------------------
+# The reference's own CPU path, restated in torch (timed as the CPU baseline)
+# ---------------------------------------------------------------------------
+# tasks/reference/L1/fp8_linear.py is the reference's torch-only semantic
+# version of the path: the weight is dequantized per 128x128 block
+# (_expand_weight_scale, :24-38) and multiplied in fp32 by F.linear (:96-104);
+# the activation quant is :41-64.  These restatements run on the host cores
+# for the bench's CPU baseline; they are not checkers (the C routines above
+# are), but the test suite checks them against those.
+
+def torch_expand_weight_scale(scale, rows: int, cols: int):
+    """Per-element fp32 weight scale of a [rows, cols] block-scaled weight
+    (fp8_linear.py:24-38, the [ceil(r/128), ceil(c/128)] case)."""
+    s = scale.float()
+    return s.repeat_interleave(GROUP, dim=-2).repeat_interleave(GROUP, dim=-1)[..., :rows, :cols]
+
+
+def torch_dense_linear(a_bf16, w_codes, w_scale):
+    """Fp8Linear.forward of the reference CPU path (fp8_linear.py:96-104):
+    fp32 dequantized weight, F.linear of the fp32 input, bf16 result.  Pass
+    the bf16 input (the literal form) or its 1x128-quantized-dequantized copy
+    (the form the GPU path computes)."""
+    import torch
+    import torch.nn.functional as F
+    n, k = w_codes.shape
+    w = w_codes.float() * torch_expand_weight_scale(w_scale, n, k)
+    return F.linear(a_bf16.reshape(-1, k).float(), w).to(torch.bfloat16)
+
+
+def torch_quant_group128(x_bf16, use_ue8m0: bool = True, eps: float = EPS):
+    """Per-token-group 1x128 quant of the reference CPU path (fp8_linear.py:
+    41-64): fp32 group absmax clamped below at eps, divided by 448, rounded
+    up to a power of two by 2^ceil(log2(.)), then codes = fp8(clamp(x / s))."""
+    import torch
+    flat = x_bf16.reshape(-1, x_bf16.shape[-1]).float()
+    groups = flat.shape[-1] // GROUP
+    g = flat.view(flat.shape[0], groups, GROUP)
+    scale = g.abs().amax(dim=-1).clamp_min(eps) / FP8_MAX
+    if use_ue8m0:
+        scale = torch.pow(2.0, torch.ceil(torch.log2(scale)))
+    q = torch.clamp(flat / scale.repeat_interleave(GROUP, dim=-1), -FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
+    return q, scale
+
+
+def torch_dequant_group128(q, scale):
+    """fp32 values of 1x128-quantized activations (codes x group scale)."""
+    return q.float() * scale.repeat_interleave(GROUP, dim=-1)
+
+
+def torch_grouped_linear(a_codes, a_scale, w_codes, w_scale, expert_ids):
+    """The contiguous-layout grouped GEMM as a per-expert-segment loop of the
+    reference's dense CPU path (fused_experts.py:32-136 layout; dequantized
+    operands, fp32 matmul, bf16 rows): returns {row: output} for the rows of
+    every expert that expert_ids names."""
+    import torch
+    out = {}
+    ids = expert_ids.tolist()
+    rows = [r for r, e in enumerate(ids) if e >= 0]
+    by_e: dict = {}
+    for r in rows:
+        by_e.setdefault(ids[r], []).append(r)
+    a = torch_dequant_group128(a_codes, a_scale)
+    n, k = w_codes.shape[-2:]
+    for e, rs in by_e.items():
+        w = w_codes[e].float() * torch_expand_weight_scale(w_scale[e], n, k)
+        y = (a[rs] @ w.t()).to(torch.bfloat16)
+        for i, r in enumerate(rs):
+            out[r] = y[i]
+    return out

@@ -751,3 +751,32 @@ def test_ue8m0_scale_without_division_identity():
         want = ((ru >> 23) & 0xFF) + ((ru & 0x7FFFFF) != 0)
         got = np.uint32(e) - 8 + (mant > 0x600000)
         assert np.array_equal(got, want.astype(np.uint32)), e
+
+
+def test_torch_restatements_match_the_c_oracle():
+    """The torch restatements of the reference CPU path (timed as the bench's
+    CPU baseline) agree with the pinned C routines: quant codes and scales
+    bit for bit, the dense and grouped GEMMs within the bf16 tolerance."""
+    import torch
+    from tests._util import bf16_bits, quantized_gemm_inputs, seeded_bf16
+    x = seeded_bf16((33, 512), seed=5, outlier_frac=1e-2)
+    q, s = oracle.torch_quant_group128(x)
+    qo, so = oracle.quant_group128(bf16_bits(x))
+    assert np.array_equal(q.view(torch.uint8).numpy(), qo) and np.array_equal(s.numpy(), so)
+    M, N, K = 17, 256, 384
+    qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=6)
+    a = torch.from_numpy(oracle.e4m3_decode(qa) * np.repeat(sa, 128, axis=1)).bfloat16()
+    y = oracle.torch_dense_linear(a, torch.from_numpy(qw).view(torch.float8_e4m3fn), torch.from_numpy(sw))
+    ref = oracle.gemm_nt_sample(qa, sa, qw, sw)
+    assert np.abs(y.float().numpy() - ref).max() <= 1e-2 * np.abs(ref).max()
+    ids = np.array([1] * 10 + [-1] * 6 + [0] * 16, dtype=np.int32)
+    qa2, sa2, qw2, sw2 = quantized_gemm_inputs(32, 256, 256, seed=7)
+    qb = np.stack([qw2[:128], qw2[128:]])
+    sb = np.stack([sw2[:1], sw2[1:]])
+    got = oracle.torch_grouped_linear(torch.from_numpy(qa2).view(torch.float8_e4m3fn), torch.from_numpy(sa2),
+                                      torch.from_numpy(qb).view(torch.float8_e4m3fn), torch.from_numpy(sb),
+                                      torch.from_numpy(ids))
+    ref2 = oracle.grouped_gemm_nt_sample(qa2, sa2, qb, sb, ids)
+    assert sorted(got) == [r for r in range(32) if ids[r] >= 0]
+    for r, row in got.items():
+        assert np.abs(row.float().numpy() - ref2[r]).max() <= 1e-2 * np.abs(ref2[r]).max() + 1e-6
