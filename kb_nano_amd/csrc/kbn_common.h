@@ -123,4 +123,16 @@ __device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float 
     return (uint32_t)w;
 }
 
+// Four e4m3 codes of a/sc, b/sc, c/sc, d/sc for a normal power of two sc,
+// by the gfx950 scaled conversion v_cvt_scalef32_pk_fp8_f32: the codes of
+// pack4_e4m3(a * (1/sc), ...) (checked on the device against it for 2^21
+// fp32 pairs at each of 67 scales from 2^-100 to 2^100, edge cases and e4m3
+// rounding ties included), without the four multiplies.
+__device__ __forceinline__ uint32_t pack4_e4m3_scaled(float a, float b, float c, float d, float sc) {
+    typedef short s16x2 __attribute__((ext_vector_type(2)));
+    s16x2 r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(s16x2{0, 0}, a, b, sc, false);
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, c, d, sc, true);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
 }  // namespace kbn

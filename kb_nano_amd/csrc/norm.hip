@@ -178,11 +178,18 @@ __device__ __forceinline__ void norm_row(const NormArgs& a, int m, int wave, int
             amax = __uint_as_float(row16_max_u32(__float_as_uint(amax)));
             amax = fmaxf(amax, kGroupEps);
             const float sc = ue8m0_ceil_div448(amax);
-            const float is = pow2_recip(sc);
-            float t[8];
+            if constexpr (kClamp) {
+                const float is = pow2_recip(sc);
+                float t[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) t[j] = kClamp ? clamp448(v[j] * is) : v[j] * is;
-            codes[i] = u32x2{pack4_e4m3(t[0], t[1], t[2], t[3]), pack4_e4m3(t[4], t[5], t[6], t[7])};
+                for (int j = 0; j < 8; ++j) t[j] = clamp448(v[j] * is);
+                codes[i] = u32x2{pack4_e4m3(t[0], t[1], t[2], t[3]), pack4_e4m3(t[4], t[5], t[6], t[7])};
+            } else {
+                // finite row: sc is a normal power of two, and the scaled
+                // conversion divides by it exactly
+                codes[i] = u32x2{pack4_e4m3_scaled(v[0], v[1], v[2], v[3], sc),
+                                 pack4_e4m3_scaled(v[4], v[5], v[6], v[7], sc)};
+            }
             scl[i] = sc;
         }
     };
