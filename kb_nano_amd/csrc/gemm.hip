@@ -190,11 +190,14 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 // write-back before its arrival is counted.
 constexpr int kDeviceCoherent = 16;
 
-// Split-K sum of rows [r, r_end) step r_step of one tile's slabs:
-// D = bf16(((s_0 + s_1) + s_2) + ...), in split order, one float4 run of
-// columns per lane (c = the run's first column within the tile).
-template <int BM, int BN, int kAux>
-__device__ __forceinline__ void splitk_sum_rows(const GemmArgs& a, int trel, int m0, int n0, int r, int r_end,
+// Split-K sum of rows r0, r0 + r_step, ... (< r_end, at most kPass of them)
+// of one tile's slabs: D = bf16(((s_0 + s_1) + s_2) + ...), in split order,
+// one float4 run of columns per lane (c = the run's first column within the
+// tile).  Every row's loads of one split are issued together (two splits per
+// step), so a workgroup that sums a whole tile keeps kPass x 2 loads in
+// flight instead of walking its rows one dependent pass at a time.
+template <int BM, int BN, int kAux, int kPass>
+__device__ __forceinline__ void splitk_sum_rows(const GemmArgs& a, int trel, int m0, int n0, int r0, int r_end,
                                                 int r_step, int c) {
     const int slab = a.tile_count * BM * BN * 4;   // bytes between splits (the workspace is below 2 GiB)
     const __amdgpu_buffer_rsrc_t dP = __builtin_amdgcn_make_buffer_rsrc(
@@ -202,30 +205,46 @@ __device__ __forceinline__ void splitk_sum_rows(const GemmArgs& a, int trel, int
     auto ld = [&](int off) {
         return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(dP, off, 0, kAux));
     };
-    for (; r < r_end; r += r_step) {
-        const int o = (r * BN + c) * 4;
-        float4 acc = ld(o);
-        int sp = 1;
-        for (; sp + 3 < a.splits; sp += 4) {
-            const float4 v0 = ld(o + sp * slab);
-            const float4 v1 = ld(o + (sp + 1) * slab);
-            const float4 v2 = ld(o + (sp + 2) * slab);
-            const float4 v3 = ld(o + (sp + 3) * slab);
-            acc.x = (((acc.x + v0.x) + v1.x) + v2.x) + v3.x;
-            acc.y = (((acc.y + v0.y) + v1.y) + v2.y) + v3.y;
-            acc.z = (((acc.z + v0.z) + v1.z) + v2.z) + v3.z;
-            acc.w = (((acc.w + v0.w) + v1.w) + v2.w) + v3.w;
+    int off[kPass];
+    float4 acc[kPass];
+#pragma unroll
+    for (int p = 0; p < kPass; ++p) {
+        const int r = r0 + p * r_step;
+        off[p] = r < r_end ? (r * BN + c) * 4 : kOob;   // rows past the tile's last read zeros, never stored
+        acc[p] = ld(off[p]);
+    }
+    int sp = 1;
+    for (; sp + 1 < a.splits; sp += 2) {
+        float4 v0[kPass], v1[kPass];
+#pragma unroll
+        for (int p = 0; p < kPass; ++p) {
+            v0[p] = ld(off[p] == kOob ? kOob : off[p] + sp * slab);
+            v1[p] = ld(off[p] == kOob ? kOob : off[p] + (sp + 1) * slab);
         }
-        for (; sp < a.splits; ++sp) {
-            const float4 v = ld(o + sp * slab);
-            acc.x += v.x;
-            acc.y += v.y;
-            acc.z += v.z;
-            acc.w += v.w;
+#pragma unroll
+        for (int p = 0; p < kPass; ++p) {
+            acc[p].x = (acc[p].x + v0[p].x) + v1[p].x;
+            acc[p].y = (acc[p].y + v0[p].y) + v1[p].y;
+            acc[p].z = (acc[p].z + v0[p].z) + v1[p].z;
+            acc[p].w = (acc[p].w + v0[p].w) + v1[p].w;
         }
-        const int n = n0 + c;
-        uint16_t* d = a.D + (int64_t)(m0 + r) * a.ldd + n;
-        const uint32_t lo = pack_bf16(acc.x, acc.y), hi = pack_bf16(acc.z, acc.w);
+    }
+    if (sp < a.splits) {
+#pragma unroll
+        for (int p = 0; p < kPass; ++p) {
+            const float4 v = ld(off[p] == kOob ? kOob : off[p] + sp * slab);
+            acc[p].x += v.x;
+            acc[p].y += v.y;
+            acc[p].z += v.z;
+            acc[p].w += v.w;
+        }
+    }
+    const int n = n0 + c;
+#pragma unroll
+    for (int p = 0; p < kPass; ++p) {
+        if (off[p] == kOob) continue;
+        uint16_t* d = a.D + (int64_t)(m0 + r0 + p * r_step) * a.ldd + n;
+        const uint32_t lo = pack_bf16(acc[p].x, acc[p].y), hi = pack_bf16(acc[p].z, acc[p].w);
         if (a.vec_store && n + 3 < a.N) {
             *reinterpret_cast<uint2*>(d) = make_uint2(lo, hi);
         } else {
@@ -704,7 +723,8 @@ gemm_bs_kernel(const GemmArgs a) {
 
     if constexpr (kSplitK) {
         epilogue_partial();
-        if (a.flags) {
+        // the fused sum is only planned for the 64-row tiles (M <= 64)
+        if constexpr (BM <= 64) if (a.flags) {
             // Fused reduction: every wavefront's (device-coherent) slab stores
             // have completed before its workgroup counts itself in; the
             // workgroup that brings the tile's count to `splits` sums all
@@ -725,9 +745,9 @@ gemm_bs_kernel(const GemmArgs a) {
             if (*last) {
                 constexpr int kRuns = BN / 4, kRowStep = 64 * kWaves / kRuns;
                 static_assert((64 * kWaves) % kRuns == 0, "whole rows per pass");
-                splitk_sum_rows<BM, BN, kDeviceCoherent>(a, trel, m0, n0, (int)threadIdx.x / kRuns,
-                                                         min(a.M - m0, BM), kRowStep,
-                                        ((int)threadIdx.x % kRuns) * 4);
+                splitk_sum_rows<BM, BN, kDeviceCoherent, (BM + kRowStep - 1) / kRowStep>(
+                    a, trel, m0, n0, (int)threadIdx.x / kRuns, min(a.M - m0, BM), kRowStep,
+                    ((int)threadIdx.x % kRuns) * 4);
             }
         }
     } else {
@@ -756,8 +776,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a) {
         tn = w / gm;
     }
     const int m0 = tm * BM, n0 = tn * BN;
-    splitk_sum_rows<BM, BN, 0>(a, trel, m0, n0, strip * 8 + (int)threadIdx.x / kRuns,
-                               min(strip * 8 + 8, a.M - m0), kRows, ((int)threadIdx.x % kRuns) * 4);
+    splitk_sum_rows<BM, BN, 0, (8 + kRows - 1) / kRows>(a, trel, m0, n0, strip * 8 + (int)threadIdx.x / kRuns,
+                                                        min(strip * 8 + 8, a.M - m0), kRows,
+                                                        ((int)threadIdx.x % kRuns) * 4);
 }
 
 // LDS bytes of a tile configuration; configurations that fit twice into a
@@ -823,7 +844,7 @@ static void plan_tail(Schedule& s, int64_t M, int KBT) {
 // a counter.  Every launch leaves its counters at zero.  When the regions are
 // used up (or the array's address cannot be had), launches fall back to the
 // separate reduction kernel.
-constexpr int kFusedReduceRows = 32;
+constexpr int kFusedReduceRows = 32;   // 64 rows measure the same as the separate launch
 constexpr int kFlagRegion = 1024;   // tail tiles per launch; a tail is below 2 x CUs tiles
 constexpr int kFlagRegions = 512;
 constexpr int kFlagDevices = 64;
@@ -898,7 +919,7 @@ static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const cha
         // Few rows: the tile's last workgroup sums the slabs (one launch
         // less).  More rows: that sum would run on one workgroup per tile at
         // the end of the launch, so the separate kernel spreads it instead.
-        a.flags = a.M <= kFusedReduceRows ? splitk_flags_for(st, tiles - dp) : nullptr;
+        a.flags = (BM <= 64 && a.M <= kFusedReduceRows) ? splitk_flags_for(st, tiles - dp) : nullptr;
         gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped && false, true, kWaves>
             <<<dim3((unsigned)blocks), dim3(64 * kWaves), 0, st>>>(a);
         KBN_CHECK_LAUNCH(what);
