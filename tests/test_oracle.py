@@ -142,14 +142,24 @@ def test_silu_table_vs_decimal_exhaustive():
 
 
 def test_silu_literal_torch_mismatch_rate_is_small():
-    """Informational pin: the literal fp32 restatement F.silu(g).bf16 differs
-    from the correctly rounded table only near bf16 rounding midpoints."""
+    """Where the correctly rounded table departs from the literal fp32 form
+    g / (1 + exp(-g)) of tasks/baseline/L1/silu_mul_quant_fp8.py:57-59 (run
+    here as torch's F.silu on fp32, then rounded to bf16): 145 of the 65,280
+    finite gates (0.22%).  Every mismatch is either one bf16 ulp (the fp32
+    roundings of exp, the add and the divide landing on the other side of a
+    bf16 rounding midpoint) or a gate below -88.72, where the fp32 exp(-g)
+    overflows and the literal form gives -0 while the true value is a tiny
+    negative number that bf16 still represents."""
     bits = ALL_BF16[_finite_mask(ALL_BF16)]
     g = _bf16_tensor(bits).float()
     lit = torch.nn.functional.silu(g).bfloat16().view(torch.int16).numpy().astype(np.uint16)
     table = oracle.silu_bf16_table()[bits]
-    rate = np.mean(lit != table)
-    assert rate < 0.01
+    mism = lit != table
+    assert np.mean(mism) < 0.005
+    ulp1 = np.abs(lit.astype(np.int32) - table.astype(np.int32)) == 1
+    overflow = (g.numpy() < -88.72) & (lit == 0x8000)
+    assert np.all(ulp1[mism] | overflow[mism])
+    assert np.all(table[overflow] & 0x8000)        # still negative (or -0) in the table
 
 
 # ------------------------------------------------------------------- quant
