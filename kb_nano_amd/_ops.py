@@ -33,7 +33,10 @@ QUANT_EPS = 1e-10  # tasks/baseline/L1/fp8_linear.py:44
 # the raw current-stream query, about 0.1 us each where torch.cuda's
 # device/stream objects cost about 2 us.
 _raw_stream = torch._C._cuda_getCurrentRawStream
+_cur_device = torch._C._cuda_getDevice
 _GFX950_DEVICES: set = set()
+_BF16 = torch.bfloat16
+_F32 = torch.float32
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -86,23 +89,28 @@ def per_token_group_quant_fp8(x: torch.Tensor, out_fp8: torch.Tensor, out_scale:
     """1x128 quant of bf16 ``x [M,K]`` into ``out_fp8 [M,K]`` and ``out_scale
     [M,K/128]`` (any strides for the scales, e.g. column-major)."""
     what = "per_token_group_quant_fp8"
-    idx = _dev_check(what, x, out_fp8, out_scale)
-    _dtype_check(what, x, torch.bfloat16, "input")
-    _dtype_check(what, out_fp8, FP8, "output_fp8")
-    _dtype_check(what, out_scale, torch.float32, "output_scale")
-    if x.dim() != 2 or out_fp8.shape != x.shape:
+    idx = x.get_device()
+    shape = x.shape
+    if (idx not in _GFX950_DEVICES or idx != _cur_device() or out_fp8.get_device() != idx
+            or out_scale.get_device() != idx):
+        _dev_check(what, x, out_fp8, out_scale)
+    if x.dtype is not _BF16 or out_fp8.dtype is not FP8 or out_scale.dtype is not _F32:
+        _dtype_check(what, x, torch.bfloat16, "input")
+        _dtype_check(what, out_fp8, FP8, "output_fp8")
+        _dtype_check(what, out_scale, torch.float32, "output_scale")
+    if len(shape) != 2 or out_fp8.shape != shape:
         raise ValueError(f"{what}: expected 2-D input and matching output, got {tuple(x.shape)} / {tuple(out_fp8.shape)}")
-    M, K = x.shape
+    M, K = shape
     if K % GROUP:
         raise ValueError(f"{what}: K={K} must be a multiple of {GROUP}")
-    if tuple(out_scale.shape) != (M, K // GROUP):
+    if out_scale.shape != (M, K // GROUP):
         raise ValueError(f"{what}: output_scale must be {(M, K // GROUP)}, got {tuple(out_scale.shape)}")
-    if x.stride(1) != 1 or out_fp8.stride(1) != 1:
+    xs, qs, ss = x.stride(), out_fp8.stride(), out_scale.stride()
+    if xs[1] != 1 or qs[1] != 1:
         raise ValueError(f"{what}: input and output rows must be contiguous")
     rc = lib().kbn_per_token_group_quant_fp8(
-        x.data_ptr(), M, K, x.stride(0), out_fp8.data_ptr(), out_fp8.stride(0),
-        out_scale.data_ptr(), out_scale.stride(0), out_scale.stride(1),
-        float(eps), int(bool(use_ue8m0)), _raw_stream(idx))
+        x.data_ptr(), M, K, xs[0], out_fp8.data_ptr(), qs[0], out_scale.data_ptr(), ss[0], ss[1],
+        float(eps), 1 if use_ue8m0 else 0, _raw_stream(idx))
     if rc:
         check(rc, what)
 
@@ -112,44 +120,58 @@ def silu_mul_quant_fp8(inp: torch.Tensor, out_fp8: torch.Tensor, out_scale: torc
     """y = bf16(silu(gate) * up) for ``inp = [gate | up]`` (bf16 [M, 2N']),
     quantized 1x128 into ``out_fp8 [M,N']`` and ``out_scale [M, N'/128]``."""
     what = "silu_mul_quant_fp8"
-    _dev_check(what, inp, out_fp8, out_scale)
-    _dtype_check(what, inp, torch.bfloat16, "input")
-    _dtype_check(what, out_fp8, FP8, "output")
-    _dtype_check(what, out_scale, torch.float32, "output_scales")
+    idx = inp.get_device()
+    if (idx not in _GFX950_DEVICES or idx != _cur_device() or out_fp8.get_device() != idx
+            or out_scale.get_device() != idx):
+        _dev_check(what, inp, out_fp8, out_scale)
+    if inp.dtype is not _BF16 or out_fp8.dtype is not FP8 or out_scale.dtype is not _F32:
+        _dtype_check(what, inp, torch.bfloat16, "input")
+        _dtype_check(what, out_fp8, FP8, "output")
+        _dtype_check(what, out_scale, torch.float32, "output_scales")
     M, N = inp.shape
     Nh = N // 2
-    if tuple(out_fp8.shape) != (M, Nh) or tuple(out_scale.shape) != (M, Nh // GROUP):
+    if out_fp8.shape != (M, Nh) or out_scale.shape != (M, Nh // GROUP):
         raise ValueError(f"{what}: bad output shapes {tuple(out_fp8.shape)} / {tuple(out_scale.shape)}")
-    if inp.stride(1) != 1 or out_fp8.stride(1) != 1:
+    xs, qs, ss = inp.stride(), out_fp8.stride(), out_scale.stride()
+    if xs[1] != 1 or qs[1] != 1:
         raise ValueError(f"{what}: input and output rows must be contiguous")
-    check(lib().kbn_silu_mul_quant_fp8(
-        inp.data_ptr(), M, Nh, inp.stride(0), out_fp8.data_ptr(), out_fp8.stride(0),
-        out_scale.data_ptr(), out_scale.stride(0), out_scale.stride(1),
-        float(eps), int(bool(use_ue8m0)), _stream(inp)), what)
+    rc = lib().kbn_silu_mul_quant_fp8(
+        inp.data_ptr(), M, Nh, xs[0], out_fp8.data_ptr(), qs[0], out_scale.data_ptr(), ss[0], ss[1],
+        float(eps), 1 if use_ue8m0 else 0, _raw_stream(idx))
+    if rc:
+        check(rc, what)
 
 
 def fp8_gemm_nt(q_input: torch.Tensor, input_scale: torch.Tensor, weight: torch.Tensor,
                 weight_scale: torch.Tensor, output: torch.Tensor, use_ue8m0: bool | None = None) -> None:
     """output[M,N] (bf16) = block-scaled q_input[M,K] x weight[N,K]^T."""
     what = "fp8_gemm_nt"
-    idx = _dev_check(what, q_input, input_scale, weight, weight_scale, output)
-    _dtype_check(what, q_input, FP8, "q_input")
-    _dtype_check(what, weight, FP8, "weight")
-    _dtype_check(what, input_scale, torch.float32, "input_scale")
-    _dtype_check(what, weight_scale, torch.float32, "weight_scale")
-    _dtype_check(what, output, torch.bfloat16, "output")
+    idx = q_input.get_device()
+    if (idx not in _GFX950_DEVICES or idx != _cur_device() or input_scale.get_device() != idx
+            or weight.get_device() != idx or weight_scale.get_device() != idx or output.get_device() != idx):
+        _dev_check(what, q_input, input_scale, weight, weight_scale, output)
+    if (q_input.dtype is not FP8 or weight.dtype is not FP8 or input_scale.dtype is not _F32
+            or weight_scale.dtype is not _F32 or output.dtype is not _BF16):
+        _dtype_check(what, q_input, FP8, "q_input")
+        _dtype_check(what, weight, FP8, "weight")
+        _dtype_check(what, input_scale, torch.float32, "input_scale")
+        _dtype_check(what, weight_scale, torch.float32, "weight_scale")
+        _dtype_check(what, output, torch.bfloat16, "output")
     M, K = q_input.shape
     N, K2 = weight.shape
     if K2 != K:
         raise ValueError(f"{what}: K mismatch {K} vs {K2}")
-    if tuple(output.shape) != (M, N):
+    if output.shape != (M, N):
         raise ValueError(f"{what}: output must be {(M, N)}, got {tuple(output.shape)}")
     KB, NB = -(-K // GROUP), -(-N // GROUP)
-    if tuple(input_scale.shape) != (M, KB):
+    if input_scale.shape != (M, KB):
         raise ValueError(f"{what}: input_scale must be {(M, KB)}, got {tuple(input_scale.shape)}")
-    if weight_scale.dim() != 2 or weight_scale.shape[0] < NB or weight_scale.shape[1] < KB:
+    sws = weight_scale.shape
+    if len(sws) != 2 or sws[0] < NB or sws[1] < KB:
         raise ValueError(f"{what}: weight_scale must be at least {(NB, KB)}, got {tuple(weight_scale.shape)}")
-    if q_input.stride(1) != 1 or weight.stride(1) != 1 or output.stride(1) != 1 or weight_scale.stride(1) != 1:
+    qs, ss, ws_, sws_, os_ = q_input.stride(), input_scale.stride(), weight.stride(), weight_scale.stride(), \
+        output.stride()
+    if qs[1] != 1 or ws_[1] != 1 or os_[1] != 1 or sws_[1] != 1:
         raise ValueError(f"{what}: operands must be contiguous along K (and N for the output)")
     ue8m0 = is_e8m0_used() if use_ue8m0 is None else bool(use_ue8m0)
     if M == 0 or N == 0:
@@ -161,9 +183,8 @@ def fp8_gemm_nt(q_input: torch.Tensor, input_scale: torch.Tensor, weight: torch.
     ws_bytes = _gemm_workspace_bytes(L, idx, M, N, K, ue8m0)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=output.device) if ws_bytes else None
     rc = L.kbn_fp8_gemm_nt_ws(
-        q_input.data_ptr(), q_input.stride(0), input_scale.data_ptr(), input_scale.stride(0), input_scale.stride(1),
-        weight.data_ptr(), weight.stride(0), weight_scale.data_ptr(), weight_scale.stride(0),
-        output.data_ptr(), output.stride(0), M, N, K, int(ue8m0),
+        q_input.data_ptr(), qs[0], input_scale.data_ptr(), ss[0], ss[1], weight.data_ptr(), ws_[0],
+        weight_scale.data_ptr(), sws_[0], output.data_ptr(), os_[0], M, N, K, 1 if ue8m0 else 0,
         ws.data_ptr() if ws is not None else None, ws_bytes, _raw_stream(idx))
     if rc:
         check(rc, what)
@@ -177,20 +198,25 @@ def fp8_linear_forward(x: torch.Tensor, q_buf: torch.Tensor, s_buf: torch.Tensor
     ``out_buf[:M] = block-scaled q x weight^T``.  Buffers may hold more than
     M rows; only the first M are written."""
     what = "fp8_linear_forward"
-    idx = _dev_check(what, x, q_buf, s_buf, weight, weight_scale, out_buf)
-    if (x.dtype != torch.bfloat16 or q_buf.dtype != FP8 or weight.dtype != FP8 or s_buf.dtype != torch.float32
-            or weight_scale.dtype != torch.float32 or out_buf.dtype != torch.bfloat16):
+    idx = x.get_device()
+    if (idx not in _GFX950_DEVICES or idx != _cur_device() or q_buf.get_device() != idx
+            or s_buf.get_device() != idx or weight.get_device() != idx or weight_scale.get_device() != idx
+            or out_buf.get_device() != idx):
+        _dev_check(what, x, q_buf, s_buf, weight, weight_scale, out_buf)
+    if (x.dtype is not _BF16 or q_buf.dtype is not FP8 or weight.dtype is not FP8 or s_buf.dtype is not _F32
+            or weight_scale.dtype is not _F32 or out_buf.dtype is not _BF16):
         raise TypeError(f"{what}: expected bf16 x, fp8 q_buf/weight, fp32 scales, bf16 out_buf")
     M, K = x.shape
     N, K2 = weight.shape
     KB, NB = -(-K // GROUP), -(-N // GROUP)
-    if (K2 != K or K % GROUP or q_buf.shape[0] < M or q_buf.shape[1] != K or s_buf.shape[0] < M
-            or s_buf.shape[1] != KB or out_buf.shape[0] < M or out_buf.shape[1] != N or weight_scale.dim() != 2
-            or weight_scale.shape[0] < NB or weight_scale.shape[1] < KB):
+    qsh, ssh, osh, wssh = q_buf.shape, s_buf.shape, out_buf.shape, weight_scale.shape
+    if (K2 != K or K % GROUP or qsh[0] < M or qsh[1] != K or ssh[0] < M or ssh[1] != KB or osh[0] < M
+            or osh[1] != N or len(wssh) != 2 or wssh[0] < NB or wssh[1] < KB):
         raise ValueError(f"{what}: shapes x {tuple(x.shape)}, q {tuple(q_buf.shape)}, s {tuple(s_buf.shape)}, "
                          f"W {tuple(weight.shape)}, sW {tuple(weight_scale.shape)}, out {tuple(out_buf.shape)}")
-    if x.stride(1) != 1 or q_buf.stride(1) != 1 or weight.stride(1) != 1 or out_buf.stride(1) != 1 \
-            or weight_scale.stride(1) != 1:
+    xs, qs, ss, ws_, wss, os_ = x.stride(), q_buf.stride(), s_buf.stride(), weight.stride(), \
+        weight_scale.stride(), out_buf.stride()
+    if xs[1] != 1 or qs[1] != 1 or ws_[1] != 1 or os_[1] != 1 or wss[1] != 1:
         raise ValueError(f"{what}: rows must be contiguous")
     if M == 0 or N == 0:
         return
@@ -199,10 +225,9 @@ def fp8_linear_forward(x: torch.Tensor, q_buf: torch.Tensor, s_buf: torch.Tensor
     ws_bytes = _gemm_workspace_bytes(L, idx, M, N, K, ue8m0)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=out_buf.device) if ws_bytes else None
     rc = L.kbn_fp8_linear_forward(
-        x.data_ptr(), M, K, x.stride(0), q_buf.data_ptr(), q_buf.stride(0), s_buf.data_ptr(), s_buf.stride(0),
-        s_buf.stride(1), QUANT_EPS, 1, weight.data_ptr(), weight.stride(0), weight_scale.data_ptr(),
-        weight_scale.stride(0), out_buf.data_ptr(), out_buf.stride(0), N, int(ue8m0),
-        ws.data_ptr() if ws is not None else None, ws_bytes, _raw_stream(idx))
+        x.data_ptr(), M, K, xs[0], q_buf.data_ptr(), qs[0], s_buf.data_ptr(), ss[0], ss[1], QUANT_EPS, 1,
+        weight.data_ptr(), ws_[0], weight_scale.data_ptr(), wss[0], out_buf.data_ptr(), os_[0], N,
+        1 if ue8m0 else 0, ws.data_ptr() if ws is not None else None, ws_bytes, _raw_stream(idx))
     if rc:
         check(rc, what)
 
@@ -337,31 +362,44 @@ def rmsnorm_fp8_quant(output_fp8: torch.Tensor, output_scales: torch.Tensor, inp
     is given, updating both in place as the reference does) quantized 1x128
     into ``output_fp8 [T, H]`` and ``output_scales [T, ceil(H/128)]`` (any
     strides; the reference allocates them column-major)."""
-    what = "fused_add_rmsnorm_fp8_quant" if residual is not None else "rmsnorm_fp8_quant"
-    tensors = (output_fp8, output_scales, input, weight) + ((residual,) if residual is not None else ())
-    _dev_check(what, *tensors)
-    _dtype_check(what, output_fp8, FP8, "output_fp8")
-    _dtype_check(what, output_scales, torch.float32, "output_scales")
-    for t, name in ((input, "input"), (weight, "weight")) + (((residual, "residual"),) if residual is not None else ()):
-        if t.dtype != torch.bfloat16:
-            raise TypeError(f"{what}: {name} must be bfloat16 on this path, got {t.dtype}")
-    H = input.size(-1)
+    idx = input.get_device()
+    add = residual is not None
+    if (idx not in _GFX950_DEVICES or idx != _cur_device() or output_fp8.get_device() != idx
+            or output_scales.get_device() != idx or weight.get_device() != idx
+            or (add and residual.get_device() != idx)):
+        _dev_check("fused_add_rmsnorm_fp8_quant" if add else "rmsnorm_fp8_quant",
+                   *((output_fp8, output_scales, input, weight) + ((residual,) if add else ())))
+    if (output_fp8.dtype is not FP8 or output_scales.dtype is not _F32 or input.dtype is not _BF16
+            or weight.dtype is not _BF16 or (add and residual.dtype is not _BF16)):
+        what = "fused_add_rmsnorm_fp8_quant" if add else "rmsnorm_fp8_quant"
+        _dtype_check(what, output_fp8, FP8, "output_fp8")
+        _dtype_check(what, output_scales, torch.float32, "output_scales")
+        for t, name in ((input, "input"), (weight, "weight")) + (((residual, "residual"),) if add else ()):
+            if t.dtype != torch.bfloat16:
+                raise TypeError(f"{what}: {name} must be bfloat16 on this path, got {t.dtype}")
+    shape = input.shape
+    H = shape[-1] if len(shape) else 1
     T = input.numel() // H if H else 0
     G = -(-H // GROUP)
-    if not input.is_contiguous() or (residual is not None and not residual.is_contiguous()):
-        raise ValueError(f"{what}: input and residual must be contiguous")
-    if residual is not None and residual.shape != input.shape:
-        raise ValueError(f"{what}: residual must match input {tuple(input.shape)}, got {tuple(residual.shape)}")
-    if tuple(weight.shape) != (H,) or not weight.is_contiguous():
-        raise ValueError(f"{what}: weight must be a contiguous [{H}] vector, got {tuple(weight.shape)}")
-    if tuple(output_fp8.shape) != (T, H) or output_fp8.stride(1) != 1:
-        raise ValueError(f"{what}: output_fp8 must be [{T}, {H}] with contiguous rows")
-    if tuple(output_scales.shape) != (T, G):
+    qs, ss = output_fp8.stride(), output_scales.stride()
+    if (not input.is_contiguous() or (add and (not residual.is_contiguous() or residual.shape != shape))
+            or weight.shape != (H,) or not weight.is_contiguous() or output_fp8.shape != (T, H) or qs[1] != 1
+            or output_scales.shape != (T, G)):
+        what = "fused_add_rmsnorm_fp8_quant" if add else "rmsnorm_fp8_quant"
+        if not input.is_contiguous() or (add and not residual.is_contiguous()):
+            raise ValueError(f"{what}: input and residual must be contiguous")
+        if add and residual.shape != shape:
+            raise ValueError(f"{what}: residual must match input {tuple(shape)}, got {tuple(residual.shape)}")
+        if weight.shape != (H,) or not weight.is_contiguous():
+            raise ValueError(f"{what}: weight must be a contiguous [{H}] vector, got {tuple(weight.shape)}")
+        if output_fp8.shape != (T, H) or qs[1] != 1:
+            raise ValueError(f"{what}: output_fp8 must be [{T}, {H}] with contiguous rows")
         raise ValueError(f"{what}: output_scales must be [{T}, {G}], got {tuple(output_scales.shape)}")
-    check(lib().kbn_rmsnorm_fp8_quant(
-        input.data_ptr(), T, H, H, weight.data_ptr(), residual.data_ptr() if residual is not None else None, H,
-        output_fp8.data_ptr(), output_fp8.stride(0), output_scales.data_ptr(), output_scales.stride(0),
-        output_scales.stride(1), float(eps), _stream(input)), what)
+    rc = lib().kbn_rmsnorm_fp8_quant(
+        input.data_ptr(), T, H, H, weight.data_ptr(), residual.data_ptr() if add else None, H,
+        output_fp8.data_ptr(), qs[0], output_scales.data_ptr(), ss[0], ss[1], float(eps), _raw_stream(idx))
+    if rc:
+        check(rc, "fused_add_rmsnorm_fp8_quant" if add else "rmsnorm_fp8_quant")
 
 
 def moe_align_block_size(topk_ids: torch.Tensor, num_experts: int, block_size: int, sorted_token_ids: torch.Tensor,

@@ -5,7 +5,7 @@ modules with the same ``forward`` signatures and column-major scale output,
 and the ops ``kb_nano_norm::rmsnorm_fp8_quant`` /
 ``kb_nano_norm::fused_add_rmsnorm_fp8_quant`` with the reference schemas
 (registered by ``_ops``).  One gfx950 launch (``csrc/norm.hip``) per call,
-one wavefront per token.
+one workgroup of 4 or 8 wavefronts per token.
 
 Numerics (reference ``csrc/rmsnorm_quant.cu:21-201``): the normalized value
 ``(x * inv_rms) * w`` stays fp32 until the UE8M0 1x128 quantization; the
