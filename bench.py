@@ -12,7 +12,8 @@ MoE grouped GEMMs (config 4) and the Llama-3.1-70B decode GEMMs (config 5),
 each with TFLOP/s or GB/s and its roofline fraction.  HBM-bound cases rotate
 through enough buffer copies to exceed the 256 MB Infinity Cache.
 
-All inputs are synthetic (seeded torch generators), weights random-init.
+All inputs are synthetic and seeded; configurations 2-5 follow the BASELINE recipe
+(CPU generators, kb_nano_amd.synthetic), weights random-init.
 """
 from __future__ import annotations
 
@@ -32,14 +33,28 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 FP8_PEAK_TFLOPS = 5000.0     # MI355X dense fp8 MFMA, TFLOP/s
 MALL_BYTES = 256 * 2 ** 20
 METRIC = "FP8 block-scaled GEMM TFLOPS (% fp8 MFMA peak); quant kernels GB/s (% HBM)"
+WARM_MS = 100.0              # minimum GPU-busy warm-up of the GEMM cases in `extra`
 
 
-def _events_time_ms(fn, steps: int, warmup: int) -> float:
-    """Average ms per call of fn() on the current stream, by HIP events."""
+def _events_time_ms(fn, steps: int, warmup: int, min_warm_ms: float = 0.0) -> float:
+    """Average ms per call of fn() on the current stream, by HIP events.
+    At least `warmup` untimed calls, and with `min_warm_ms` as many more as it
+    takes to keep the GPU busy that long: a case whose inputs were just drawn
+    on the CPU starts on an idle GPU, and the power-limited MFMA shapes reach
+    their steady clock only after some tens of milliseconds of load."""
+    import time
     import torch
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
+    if min_warm_ms > 0:
+        t0 = time.perf_counter()
+        i = warmup
+        while (time.perf_counter() - t0) * 1e3 < min_warm_ms:
+            for _ in range(max(1, warmup)):
+                fn(i)
+                i += 1
+            torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -156,19 +171,23 @@ def bench_requant(steps, warmup, dev, E=32, N=4096, K=7168):
     return {"E": E, "N": N, "K": K, "us": ms * 1e3, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
 
 
-def _gemm_case(name, M, N, K, steps, warmup, dev, seed):
+def _gemm_case(name, M, N, K, steps, warmup, dev, seed, act_seed):
+    """One dense GEMM shape, inputs by the BASELINE recipe (CPU generators:
+    the weight from `seed`, the activations from `act_seed`); HBM-bound
+    shapes rotate over copies of the weight that exceed the Infinity Cache."""
     import torch
-    from kb_nano_amd import _ops
-    gen = torch.Generator(device=dev).manual_seed(seed)
+    from kb_nano_amd import _ops, synthetic
     w_bytes = N * K + 4 * (-(-N // 128)) * (K // 128)
     a_bytes = M * K + 4 * M * (K // 128)
     nbytes = w_bytes + a_bytes + 2 * M * N
     n = _copies_for(nbytes) if M <= 256 else 1
-    Ws = [_rand_weight(N, K, gen, dev, torch) for _ in range(n)]
-    A, sA = _quant_act(torch.randn(M, K, generator=gen, device=dev).bfloat16(), torch)
+    w0, s0 = synthetic.dense_weight(N, K, seed=seed, device=dev)
+    Ws = [(w0, s0)] + [(w0.clone(), s0.clone()) for _ in range(n - 1)]
+    del w0, s0
+    A, sA = _quant_act(synthetic.bf16_normal((M, K), seed=act_seed).to(dev), torch)
     D = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
     ms = _events_time_ms(lambda i: _ops.fp8_gemm_nt(A, sA, Ws[i % n][0], Ws[i % n][1], D, use_ue8m0=True),
-                         steps, warmup)
+                         steps, warmup, min_warm_ms=WARM_MS)
     flop = 2.0 * M * N * K
     t = ms * 1e-3
     tflops = flop / t / 1e12
@@ -190,7 +209,7 @@ def bench_dsv3(steps, warmup, dev):
     out = []
     for M in (4096, 128):
         for name, N, K in DSV3:
-            out.append(_gemm_case(name, M, N, K, steps, warmup, dev, seed=2))
+            out.append(_gemm_case(name, M, N, K, steps, warmup, dev, seed=2, act_seed=20))
     return out
 
 
@@ -198,7 +217,7 @@ def bench_decode(steps, warmup, dev):
     out = []
     for name, N, K in LLAMA70B:
         for M in (1, 8, 32, 64):
-            out.append(_gemm_case(name, M, N, K, steps, warmup, dev, seed=4))
+            out.append(_gemm_case(name, M, N, K, steps, warmup, dev, seed=4, act_seed=40 + M))
     return out
 
 
@@ -264,14 +283,12 @@ def bench_moe(steps, warmup, dev):
     softmax logits, per-expert rows padded to 128; gate_up (N=4096, K=7168)
     then down (N=7168, K=2048)."""
     import torch
-    from kb_nano_amd import _ops
+    from kb_nano_amd import _ops, synthetic
     from kb_nano_amd.moe_layout import _deepgemm_permute
     T, H, E, topk, I2, I = 4096, 7168, 256, 8, 4096, 2048
-    g = torch.Generator().manual_seed(0)
-    logits = torch.randn(T, E, generator=g)
-    topk_ids = torch.topk(torch.softmax(logits, -1), topk, dim=-1).indices.to(dev)
-    gen = torch.Generator(device=dev).manual_seed(5)
-    hidden = torch.randn(T, H, generator=gen, device=dev).bfloat16()
+    topk_ids_cpu, topk_w_cpu = synthetic.moe_routing(T, E, topk, seed=0)
+    topk_ids = topk_ids_cpu.to(dev)
+    hidden = synthetic.bf16_normal((T, H), seed=3).to(dev)
     a_tok, s_tok = _quant_act(hidden, torch)
     a_perm, s_perm, expert_ids, _ = _deepgemm_permute(a_tok.view(torch.uint8), s_tok.contiguous(), topk_ids, E, 128)
     a_perm = a_perm.view(torch.float8_e4m3fn)
@@ -279,13 +296,6 @@ def bench_moe(steps, warmup, dev):
     ids = expert_ids.cpu()
     rows_in_segments = int(sum(1 for r in range(0, M_sum, 128) if ids[r] >= 0)) * 128
     valid_rows = int((ids >= 0).sum())
-
-    def experts(N, K):
-        w = torch.empty(E, N, K, dtype=torch.float8_e4m3fn, device=dev)
-        s = torch.empty(E, -(-N // 128), K // 128, device=dev)
-        for e in range(E):
-            w[e], s[e] = _rand_weight(N, K, gen, dev, torch)
-        return w, s
 
     res = {"M_sum": M_sum, "rows_in_segments": rows_in_segments, "valid_rows": valid_rows}
 
@@ -306,8 +316,8 @@ def bench_moe(steps, warmup, dev):
         nbytes = T * H + rows_out * (H + cols * 4) + small_io
         res[tag] = {"us": ms * 1e3, "bytes": nbytes, "GB/s": nbytes / ms / 1e6,
                     "frac_hbm": nbytes / ms / 1e6 / HBM_PEAK_GBS}
-    y = torch.randn(M_sum, H, generator=gen, device=dev).bfloat16()
-    topk_w = torch.softmax(torch.randn(T, topk, generator=g), -1).to(dev)
+    y = synthetic.bf16_normal((M_sum, H), seed=32).to(dev)
+    topk_w = topk_w_cpu.to(dev)
     out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     ms = _events_time_ms(lambda i: _ops.moe_unpermute_reduce(y, inv, topk_w, out), steps, warmup)
     nbytes = n_pairs * H * 2 + T * H * 2 + n_pairs * 8
@@ -315,25 +325,23 @@ def bench_moe(steps, warmup, dev):
                         "frac_hbm": nbytes / ms / 1e6 / HBM_PEAK_GBS}
     del xp, sp, eid, y, out
 
-    w13, s13 = experts(I2, H)
+    # expert stacks by the BASELINE recipe (the seeds of the full-size parity tests)
+    w13, s13 = synthetic.expert_weights(E, I2, H, seed=3, device=dev)
     c1 = torch.empty(M_sum, I2, dtype=torch.bfloat16, device=dev)
     ms1 = _events_time_ms(lambda i: _ops.m_grouped_gemm_nt_contiguous(a_perm, s_perm, w13, s13, c1, expert_ids, False),
-                          steps, warmup)
-    del w13, s13
-    a2 = torch.randn(M_sum, I, generator=gen, device=dev).bfloat16()
-    a2q, a2s = _quant_act(a2, torch)
-    del a2
-    w2, s2 = experts(H, I)
+                          steps, warmup, min_warm_ms=WARM_MS)
+    del c1
+    a2q, a2s = _quant_act(synthetic.bf16_normal((M_sum, I), seed=31).to(dev), torch)
+    w2, s2 = synthetic.expert_weights(E, H, I, seed=30, device=dev)
     c2 = torch.empty(M_sum, H, dtype=torch.bfloat16, device=dev)
     ms2 = _events_time_ms(lambda i: _ops.m_grouped_gemm_nt_contiguous(a2q, a2s, w2, s2, c2, expert_ids, False),
-                          steps, warmup)
+                          steps, warmup, min_warm_ms=WARM_MS)
+    del c2, a2q, a2s
     # the whole experts layer (quant, permute, both GEMMs, SiLU*Mul+quant, unpermute)
     from kb_nano_amd.fused_experts import FusedExperts
-    w13, s13 = experts(I2, H)
-    w2, s2 = experts(H, I)
     layer = FusedExperts()
     ms_layer = _events_time_ms(lambda i: layer(hidden, w13, w2, topk_w, topk_ids, E, w13_scale=s13, w2_scale=s2,
-                                               use_fp8_w8a8=True, block_shape=[128, 128]), steps, warmup)
+                                               use_fp8_w8a8=True, block_shape=[128, 128]), steps, warmup, min_warm_ms=WARM_MS)
     res["layer_us"] = ms_layer * 1e3
     del w13, s13, w2, s2
     for tag, ms, N, K in (("gate_up", ms1, I2, H), ("down", ms2, H, I)):
@@ -355,32 +363,23 @@ def bench_moe_sorted(steps, warmup, dev):
     Reports the align and moe_sum kernels, both sorted-token GEMMs at config 4
     and the whole layer per batch."""
     import torch
-    from kb_nano_amd import VllmFusedExperts, _ops
+    from kb_nano_amd import VllmFusedExperts, _ops, synthetic
     from kb_nano_amd.moe_align import MoeAlign
     from kb_nano_amd.moe_grouped_gemm import get_triton_config
     H, E, topk, I2, I = 7168, 256, 8, 4096, 2048
-    gen = torch.Generator(device=dev).manual_seed(7)
-
-    def experts(N, K):
-        w = torch.empty(E, N, K, dtype=torch.float8_e4m3fn, device=dev)
-        s = torch.empty(E, -(-N // 128), K // 128, device=dev)
-        for e in range(E):
-            w[e], s[e] = _rand_weight(N, K, gen, dev, torch)
-        return w, s
-
-    w13, s13 = experts(I2, H)
-    w2, s2 = experts(H, I)
+    # config 4's expert stacks by the BASELINE recipe (as in the contiguous-layout case)
+    w13, s13 = synthetic.expert_weights(E, I2, H, seed=3, device=dev)
+    w2, s2 = synthetic.expert_weights(E, H, I, seed=30, device=dev)
     wbytes13 = E * (I2 * H + 4 * (I2 // 128) * (H // 128))
     wbytes2 = E * (H * I + 4 * (H // 128) * (I // 128))
     layer = VllmFusedExperts()
     res = {}
     for T in (4096, 64, 4):
-        g = torch.Generator().manual_seed(T)
-        topk_ids = torch.topk(torch.softmax(torch.randn(T, E, generator=g), -1), topk, dim=-1).indices.to(dev)
-        topk_w = torch.softmax(torch.randn(T, topk, generator=g), -1).to(dev)
-        hidden = torch.randn(T, H, generator=gen, device=dev).bfloat16()
+        ids_cpu, w_cpu = synthetic.moe_routing(T, E, topk, seed=0 if T == 4096 else T)
+        topk_ids, topk_w = ids_cpu.to(dev), w_cpu.to(dev)
+        hidden = synthetic.bf16_normal((T, H), seed=3).to(dev)
         ms = _events_time_ms(lambda i: layer(hidden, w13, w2, topk_w, topk_ids, E, s13, s2, [128, 128]),
-                             steps, warmup)
+                             steps, warmup, min_warm_ms=WARM_MS)
         active = int(torch.unique(topk_ids).numel())
         res[f"layer_T{T}"] = {"us": ms * 1e3, "active_experts": active,
                               "weight_GB/s": active * (wbytes13 + wbytes2) / E / ms / 1e6}
@@ -397,7 +396,7 @@ def bench_moe_sorted(steps, warmup, dev):
         c1 = torch.empty(n_pairs, I2, dtype=torch.bfloat16, device=dev)
         EM = sorted_ids.numel()
         ms1 = _events_time_ms(lambda i: _ops.fused_moe_gemm(a1, s_a1, w13, s13, c1, sorted_ids, expert_ids, post, EM,
-                                                            block, topk), steps, warmup)
+                                                            block, topk), steps, warmup, min_warm_ms=WARM_MS)
         # GEMM2's input as the layer makes it: SiLU*Mul + quant of GEMM1's rows
         a2q = torch.empty(n_pairs, I, dtype=torch.float8_e4m3fn, device=dev)
         a2s = torch.empty(I // 128, n_pairs, device=dev).t()
@@ -405,7 +404,7 @@ def bench_moe_sorted(steps, warmup, dev):
         c2 = torch.empty(n_pairs, H, dtype=torch.bfloat16, device=dev)
         wflat = topk_w.reshape(-1).contiguous()
         ms2 = _events_time_ms(lambda i: _ops.fused_moe_gemm(a2q, a2s, w2, s2, c2, sorted_ids, expert_ids, post, EM,
-                                                            block, 1, topk_weights=wflat), steps, warmup)
+                                                            block, 1, topk_weights=wflat), steps, warmup, min_warm_ms=WARM_MS)
         total = int(post.item())
         for tag, ms, N, K, wb in (("gemm1", ms1, I2, H, wbytes13), ("gemm2", ms2, H, I, wbytes2)):
             t = ms * 1e-3
@@ -661,7 +660,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16->fp8_e4m3 (f32 math)",
-        "data": "synthetic (seeded torch RNG; cfg2: N(0,1) gate/up with 0.1% x50 outliers)",
+        "data": "synthetic, seeded CPU torch generators (BASELINE recipe); cfg2: N(0,1) gate/up with 0.1% x50 outliers",
         "config": {"workload": "cfg2 fused SiLU*Mul + 1x128 FP8 quant: bf16 [8192, 36864] -> "
                                "fp8 [8192, 18432] + fp32 column-major scales [8192, 144]",
                    "M": 8192, "N_half": 18432, "algorithmic_bytes": head["bytes"]},

@@ -82,18 +82,17 @@ def test_gemm_single_k_block_special_case(gpu_device):
                                       ("down_proj", 7168, 18432), ("o_proj", 7168, 16384)])
 @pytest.mark.parametrize("M", [128, 4096])
 def test_gemm_dsv3_shapes_sampled(gpu_device, name, N, K, M):
-    """BASELINE config 3 at full size; the oracle is evaluated on 48 sampled
-    rows x 96 sampled columns (including the first/last row and column)."""
-    from kb_nano_amd import _ops
-    g = torch.Generator(device=gpu_device).manual_seed(2)
-    a = torch.randn(M, K, generator=g, device=gpu_device).bfloat16()
-    w = torch.randn(N, K, generator=g, device=gpu_device) * 0.02
-    from kb_nano_amd.fp8_linear import _alloc_colmajor_scale, _block_requant
+    """BASELINE config 3 at full size, inputs drawn on the CPU by the BASELINE
+    recipe (seed 2 for the weights, 20 for the activations); the oracle is
+    evaluated on 48 sampled rows x 96 sampled columns (including the
+    first/last row and column)."""
+    from kb_nano_amd import _ops, synthetic
+    from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
+    a = synthetic.bf16_normal((M, K), seed=20).to(gpu_device)
     A = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=gpu_device)
     sA = _alloc_colmajor_scale(M, K // 128, gpu_device)
     _ops.per_token_group_quant_fp8(a, A, sA)
-    W, sW = _block_requant(w, use_ue8m0=True, eps=1e-10)
-    del w
+    W, sW = synthetic.dense_weight(N, K, seed=2, device=gpu_device)
     D = torch.empty(M, N, dtype=torch.bfloat16, device=gpu_device)
     _ops.fp8_gemm_nt(A, sA, W, sW, D, use_ue8m0=True)
     torch.cuda.synchronize()
