@@ -1,35 +1,11 @@
-// Block-scaled FP8 GEMM  D[M,N] (bf16) = A[M,K] (e4m3) x W[N,K]^T (e4m3)
-// with one fp32 scale per (row, 128-K block) of A and per (128-N, 128-K)
-// block of W, plus the contiguous-layout grouped (MoE) variant.
-//
-// Contract (tasks/baseline/L1/fp8_linear.py:97-110 -> deep_gemm.fp8_gemm_nt,
-// tasks/baseline/L1/fp8_grouped_gemm_contiguous.py:109-118):
-//   D[m,n] = bf16_rne( sum_kb sA[m,kb] * sW[n/128,kb] * sum_{k in kb} A[m,k] W[n,k] )
-// accumulated in fp32.
-//
-// Two scale contracts:
-//  * UE8M0 (the default, DeepGEMM's UE8M0 cast): every scale is rounded up to
-//    a power of two and applied inside the block-scaled MFMA
-//    (v_mfma_scale_f32_32x32x64_f8f6f4) as an E8M0 operand, so one fp32
-//    accumulator set runs across all of K with no promotion epilogue.
-//  * FP32 (disable_ue8m0_cast): scales are used as given.  Each scale splits
-//    exactly into a power of two, applied by the MFMA as above, and a
-//    significand in [1, 2).  The accumulators hold the running sum in units
-//    of the current block's significand product (per row) and are rescaled
-//    by the ratio of consecutive products when a block starts; the last
-//    product multiplies the sum before the store.  Power-of-two scales give
-//    ratios of 1 and skip the rescale, so such scales cost what UE8M0 does.
-//
-// Dataflow per workgroup (256 lanes = 4 wavefronts, one per SIMD):
-//   HBM --buffer_load_dwordx4 ... lds (direct DMA)--> LDS (kStages x (BM+BN) x 128 B)
-//   LDS --ds_read_b128--> VGPR fragments --MFMA 32x32x64--> fp32 accumulators
-// Each LDS row is 128 B (one 128-K scale block); its eight 16-B chunks are
-// XOR-swizzled so the rows read by one ds_read_b128 hit distinct banks.  The
-// swizzle is applied on the global side of the DMA (lane i of a load
-// instruction always writes LDS chunk i), so no extra LDS pass is needed.
-// Out-of-range rows read as zero through the buffer descriptor's range check.
-
-#include "kbn_common.h"
+// Host side of the block-scaled FP8 GEMMs: the tile planner, the split-K
+// arrival counters, the sorted-token launches and the C-ABI entry points.
+// The kernels are in gemm_kernel.h.  This file is built with the VGPR-form
+// MFMA option (kb_nano_amd/_build.py): its tiles keep their accumulators in
+// VGPRs, where the FP32 contract's per-block rescale is one multiply per
+// element instead of a read, multiply and write of an AGPR.  The 256x256
+// tiles are launched from gemm_big.hip, built without it.
+#include "gemm_kernel.h"
 
 #include <algorithm>
 #include <map>
@@ -37,820 +13,6 @@
 #include <tuple>
 
 namespace kbn {
-
-typedef int v8i __attribute__((ext_vector_type(8)));
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef float v16f __attribute__((ext_vector_type(16)));
-
-
-// FP32 scale contract: s = 2^(byte - 127) * mant with byte the biased
-// exponent field (the block-scaled MFMA's E8M0 operand, exact) and mant the
-// significand in [1, 2).  Zero and subnormal scales get byte 0 (2^-127), so
-// their block adds at most 2^-127 of the value it would have at scale 1;
-// inf/NaN scales get 255, the E8M0 NaN.
-__device__ __forceinline__ int scale_exp_byte(float s) { return (int)((__float_as_uint(s) >> 23) & 0xFFu); }
-__device__ __forceinline__ float scale_mant(float s) {
-    return __uint_as_float((__float_as_uint(s) & 0x007FFFFFu) | 0x3F800000u);
-}
-
-struct GemmArgs {
-    const uint8_t* A;
-    int64_t lda;
-    const float* sA;
-    int64_t sA_sm, sA_sk;
-    int64_t sA_bytes;            // byte range of the scale buffer the kernel may read
-    const uint8_t* W;            // [N, K] (dense) or [E, N, K] (grouped)
-    int64_t ldw;
-    int64_t w_estride;           // bytes between experts (grouped)
-    const float* sW;             // [ceil(N/128), KB] (+ expert stride)
-    int64_t sW_ld;
-    int64_t sW_estride;
-    uint16_t* D;
-    int64_t ldd;
-    const int32_t* expert_ids;   // grouped only
-    int M, N, K, E;
-    int tiles_m, tiles_n;
-    int vec_store;               // D rows allow aligned 16-B stores
-    // This launch covers tiles [tile_base, tile_base + tile_count) of the
-    // grouped tile order.  Split-K: workgroup (tile, split) accumulates K
-    // blocks [split * kb_per_split, +kb_per_split) into the fp32 slab
-    // P[split][tile - tile_base][BM][BN], summed by splitk_reduce_kernel.
-    int tile_base, tile_count;
-    float* P;
-    int64_t ws_bytes;            // bytes at P
-    int splits, kb_per_split;
-    // Arrival counters of the split launch, one per tile (nullptr: a separate
-    // splitk_reduce_kernel launch sums the slabs).  Zero on entry; the last
-    // workgroup of a tile to finish sums the slabs and resets its counter.
-    unsigned* flags;
-    // Sorted-token layout (fused MoE): row R of the tile grid holds routed pair
-    // sorted_ids[R] (or, with no list, pair R / block_m on the first row of
-    // each block and nothing elsewhere); a pair t >= num_valid is padding.
-    // A row of pair t: t / a_row_div.  Output row: t.  Expert of block b:
-    // expert_ids[b], blocks at or past *num_post_pad are skipped.
-    const int32_t* sorted_ids;
-    const int32_t* num_post_pad;
-    int block_m, num_valid, a_row_div;
-    int64_t A_bytes;             // bytes at A the gathers may read
-    int64_t D_bytes;             // bytes at D the scattered stores may write
-    const float* row_weight;     // [num_valid] fp32 factors of the output rows, or nullptr
-    int sa_sorted;               // sA already holds row R's scales at R (gathered by sorted_scale_gather_kernel)
-};
-
-// Raw buffer descriptor (base, byte range) built from uniform values so it
-// lives in SGPRs.  Loads past `bytes` return zero.
-__device__ __forceinline__ v4i make_desc(const void* base, int64_t bytes) {
-    const uint64_t p = reinterpret_cast<uint64_t>(base);
-    const uint32_t n = bytes <= 0 ? 0u : (bytes >= 0xFFFFFFFFLL ? 0xFFFFFFFFu : (uint32_t)bytes);
-    v4i r;
-    r[0] = (int)(uint32_t)p;
-    r[1] = (int)((p >> 32) & 0xFFFFu);
-    r[2] = (int)n;
-    r[3] = (int)kRsrcWord3;
-    return r;
-}
-
-// Direct global->LDS DMA.  Issued as inline asm so the compiler's waitcnt
-// pass does not serialise every LDS read behind the in-flight DMA of the
-// other stage; completion is awaited explicitly (wait_dma) before the
-// barrier that publishes a stage.  Lane i writes LDS bytes
-// [lds + 16*i, lds + 16*i + 16) (dwordx4) or [lds + 4*i, lds + 4*i + 4) (dword).
-__device__ __forceinline__ void dma_b128(const v4i& desc, uint32_t lds, int voff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(desc)
-                 : "memory");
-}
-// The same load with the non-temporal hint: the weight rows of a tile are
-// read once per workgroup and should not push the activation rows (read by
-// every workgroup of a tile row) out of L2.
-__device__ __forceinline__ void dma_b128_nt(const v4i& desc, uint32_t lds, int voff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(lds), "v"(voff), "s"(desc)
-                 : "memory");
-}
-__device__ __forceinline__ void dma_b32(const v4i& desc, uint32_t lds, int voff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(desc)
-                 : "memory");
-}
-__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-// Wait until at most N vector-memory loads of this wavefront are outstanding
-// (loads complete in issue order, so everything older than the last N has landed).
-template <int N>
-__device__ __forceinline__ void wait_dma_n() {
-    static_assert(N >= 0 && N <= 63, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-
-
-// LDS row layout.  A stage holds one 128-K scale block per row (128 B =
-// eight 16-B chunks); chunk c of row r lives in slot c ^ swz(r).  A
-// ds_read_b128 is served 16 lanes (256 B, all 64 banks) per cycle; the 16
-// consecutive rows read by 16 lanes alternate between the two halves of a
-// 256-B bank line (r % 2) and take 8 distinct slots per half (r >> 1), so
-// fragment reads are conflict-free.
-__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
-
-constexpr int kRowB = 128;   // LDS row bytes = K per stage = one scale block
-
-// XCD-aware tile order.  Consecutive workgroup ids are dispatched round-robin
-// over the 8 XCDs; give each XCD a contiguous range of the (tile, split)
-// sequence so the tiles resident on one XCD (and its L2) share A row panels
-// and W panels, and walk that sequence in column groups of kGroupM row tiles
-// (the K splits of one tile are neighbours).
-template <int kGroupM>
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int tile_base, int splits, int& tm, int& tn,
-                                            int& trel, int& split) {
-    const int nblk = gridDim.x;
-    const int bid = blockIdx.x;
-    const int xcd = bid & 7, i = bid >> 3;
-    const int per = nblk >> 3, rem = nblk & 7;
-    const int ts = xcd * per + (xcd < rem ? xcd : rem) + i;
-    trel = ts / splits;
-    split = ts - trel * splits;
-    const int t = tile_base + trel;
-    const int group = kGroupM * tiles_n;
-    const int g = t / group;
-    const int first_m = g * kGroupM;
-    const int gm = min(tiles_m - first_m, kGroupM);
-    const int w = t - g * group;
-    tm = first_m + w % gm;
-    tn = w / gm;
-}
-
-// Tile order of the MoE layouts.  Their padded row grid ends in row tiles no
-// expert owns (those workgroups exit at once), so contiguous per-XCD ranges
-// would give the last XCDs nothing but empty tiles (cfg4: two of eight idle).
-// The tile sequence (column groups of kGroupM row tiles, as tile_coords) is
-// split in two parts:
-//   - as many whole column groups as make full rounds of eight are dealt to
-//     the XCDs round-robin: XCD x runs groups x, x + 8, x + 16, ... in order;
-//   - the rest (fewer than eight groups) is cut into eight contiguous ranges.
-// Every XCD then gets the same number of tiles, the empty tail is shared out
-// with the rest, and an expert's row tiles still meet its weight panel in one
-// L2.  The grid has moe_dealt_grid slots; a slot past an XCD's share returns
-// false.
-template <int kGroupM>
-__device__ __forceinline__ bool tile_coords_dealt(int tiles_m, int tiles_n, int& tm, int& tn) {
-    const int bid = blockIdx.x;
-    const int xcd = bid & 7, i = bid >> 3;
-    const int total = tiles_m * tiles_n;
-    const int group = kGroupM * tiles_n;
-    const int rounds = total / group / 8;          // dealt groups per XCD
-    const int dealt = rounds * group;              // dealt tiles per XCD
-    int t;
-    if (i < dealt) {
-        const int j = i / group;
-        t = (xcd + 8 * j) * group + (i - j * group);
-    } else {
-        const int rest = total - 8 * dealt, per = rest >> 3, rem = rest & 7;
-        const int r = i - dealt;
-        if (r >= per + (xcd < rem ? 1 : 0)) return false;
-        t = 8 * dealt + xcd * per + min(xcd, rem) + r;
-    }
-    const int g = t / group;
-    const int first_m = g * kGroupM;
-    const int gm = min(tiles_m - first_m, kGroupM);
-    const int w = t - g * group;
-    tm = first_m + w % gm;
-    tn = w / gm;
-    return true;
-}
-// 16 row tiles per column group measured best at cfg4 (gate_up 1760 us
-// against 1800 with 8, 1770 with 12, 1845 with 24).
-constexpr int kMoeGroupM = 16;
-// Workgroups of a dealt launch over tiles_m x tiles_n tiles.
-static inline int64_t moe_dealt_grid(int64_t tiles_m, int64_t tiles_n) {
-    const int64_t total = tiles_m * tiles_n;
-    if (total <= 0) return 0;
-    const int64_t group = kMoeGroupM * tiles_n;
-    const int64_t dealt = total / group / 8 * group;
-    return 8 * (dealt + (total - 8 * dealt + 7) / 8);
-}
-
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-    const bf16x2 p = __builtin_convertvector((f32x2{lo, hi}), bf16x2);  // v_cvt_pk_bf16_f32, RNE
-    return __builtin_bit_cast(uint32_t, p);
-}
-// Cache-policy operand of the split-K slab stores and loads: the SC1 bit,
-// which the compiler emits for agent-scope relaxed atomic accesses.  Such an
-// access is coherent across the XCDs' L2s, and a store is visible device-wide
-// once it has completed (vmcnt), so a slab written this way needs no L2
-// write-back before its arrival is counted.
-constexpr int kDeviceCoherent = 16;
-
-// Split-K sum of rows r0, r0 + r_step, ... (< r_end, at most kPass of them)
-// of one tile's slabs: D = bf16(((s_0 + s_1) + s_2) + ...), in split order,
-// one float4 run of columns per lane (c = the run's first column within the
-// tile).  Every row's loads of one split are issued together (two splits per
-// step), so a workgroup that sums a whole tile keeps kPass x 2 loads in
-// flight instead of walking its rows one dependent pass at a time.
-template <int BM, int BN, int kAux, int kPass>
-__device__ __forceinline__ void splitk_sum_rows(const GemmArgs& a, int trel, int m0, int n0, int r0, int r_end,
-                                                int r_step, int c) {
-    const int slab = a.tile_count * BM * BN * 4;   // bytes between splits (the workspace is below 2 GiB)
-    const __amdgpu_buffer_rsrc_t dP = __builtin_amdgcn_make_buffer_rsrc(
-        a.P + (int64_t)trel * BM * BN, (short)0, (int)((a.splits - 1) * slab + BM * BN * 4), (int)kRsrcWord3);
-    auto ld = [&](int off) {
-        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(dP, off, 0, kAux));
-    };
-    int off[kPass];
-    float4 acc[kPass];
-#pragma unroll
-    for (int p = 0; p < kPass; ++p) {
-        const int r = r0 + p * r_step;
-        off[p] = r < r_end ? (r * BN + c) * 4 : kOob;   // rows past the tile's last read zeros, never stored
-        acc[p] = ld(off[p]);
-    }
-    int sp = 1;
-    for (; sp + 1 < a.splits; sp += 2) {
-        float4 v0[kPass], v1[kPass];
-#pragma unroll
-        for (int p = 0; p < kPass; ++p) {
-            v0[p] = ld(off[p] == kOob ? kOob : off[p] + sp * slab);
-            v1[p] = ld(off[p] == kOob ? kOob : off[p] + (sp + 1) * slab);
-        }
-#pragma unroll
-        for (int p = 0; p < kPass; ++p) {
-            acc[p].x = (acc[p].x + v0[p].x) + v1[p].x;
-            acc[p].y = (acc[p].y + v0[p].y) + v1[p].y;
-            acc[p].z = (acc[p].z + v0[p].z) + v1[p].z;
-            acc[p].w = (acc[p].w + v0[p].w) + v1[p].w;
-        }
-    }
-    if (sp < a.splits) {
-#pragma unroll
-        for (int p = 0; p < kPass; ++p) {
-            const float4 v = ld(off[p] == kOob ? kOob : off[p] + sp * slab);
-            acc[p].x += v.x;
-            acc[p].y += v.y;
-            acc[p].z += v.z;
-            acc[p].w += v.w;
-        }
-    }
-    const int n = n0 + c;
-#pragma unroll
-    for (int p = 0; p < kPass; ++p) {
-        if (off[p] == kOob) continue;
-        uint16_t* d = a.D + (int64_t)(m0 + r0 + p * r_step) * a.ldd + n;
-        const uint32_t lo = pack_bf16(acc[p].x, acc[p].y), hi = pack_bf16(acc[p].z, acc[p].w);
-        if (a.vec_store && n + 3 < a.N) {
-            *reinterpret_cast<uint2*>(d) = make_uint2(lo, hi);
-        } else {
-            if (n < a.N) d[0] = (uint16_t)lo;
-            if (n + 1 < a.N) d[1] = (uint16_t)(lo >> 16);
-            if (n + 2 < a.N) d[2] = (uint16_t)hi;
-            if (n + 3 < a.N) d[3] = (uint16_t)(hi >> 16);
-        }
-    }
-}
-
-// Block-scaled GEMM tile kernel: BM x BN output tile, four wavefronts in a
-// 2 x 2 grid, each owning a (BM/2) x (BN/2) block of 32x32 MFMA fragments.
-//
-// LDS stage layout (one stage = one 128-K block):
-//   [A: BM x 128 B][W: BN x 128 B][sA: 4 x 64 fp32][sW: 4 x 64 fp32]
-// Every load is a 16-B (or 4-B) direct global->LDS DMA; one A/W instruction
-// moves eight full 128-B rows, so every request the vector cache sends to L2
-// is a whole 128-B line.
-//
-// Pipeline over K blocks kb (LDS buffer kb % kStages), per wavefront:
-//   sub-step 0: MFMAs of K half 0 of block kb, interleaved with the LDS reads
-//               of K half 1 of block kb;
-//   hand-off:   wait until block kb+1 has landed and this wavefront's reads of
-//               block kb are done; barrier (publishes kb+1, frees buffer kb);
-//               DMA block kb+kStages into the freed buffer;
-//   sub-step 1: MFMAs of K half 1 of block kb, interleaved with the LDS reads
-//               of K half 0 (and the scales) of block kb+1.
-// So kStages-1 blocks are in flight while one is consumed, and no fragment
-// register set is ever copied.
-template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, bool kSplitK, int kWaves, bool kSorted = false>
-__global__ __launch_bounds__(64 * kWaves, (kStages * (BM + BN) * 128 + kStages * 512 * kWaves <= 80 * 1024) ? 2 : 1) void
-gemm_bs_kernel(const GemmArgs a) {
-    static_assert(!(kSorted && (kGrouped || kSplitK)), "the sorted-token layout is its own grouped mode");
-    static_assert(kWaves == 4 || kWaves == 8, "2x2 or 2x4 wavefronts");
-    constexpr int WM = 2, WN = kWaves / 2;
-    constexpr int TM = BM / WM, TN = BN / WN;   // wavefront tile
-    constexpr int FM = TM / 32, FN = TN / 32;   // 32x32 fragments per wavefront
-    static_assert(FM >= 1 && FN >= 1 && TM % 32 == 0 && TN % 32 == 0, "fragment tiling");
-    static_assert(BM <= 64 * kWaves && BM % (16 * kWaves) == 0 && BN % (16 * kWaves) == 0, "DMA tiling");
-    static_assert(128 % TN == 0 || TN % 128 == 0, "wave N tile must not straddle a scale block");
-    constexpr int kA = BM * kRowB, kB = BN * kRowB, kSA = kWaves * 256, kSW = kWaves * 256;
-    constexpr int kStage = kA + kB + kSA + kSW;
-    static_assert(kStages >= 2 && kStages * kStage <= 160 * 1024, "LDS budget");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStage];
-    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)smem);
-
-    static_assert(!kGrouped || BM == 128, "grouped tiles cover one 128-row block of the contiguous layout");
-
-    int tm, tn, trel = 0, split = 0;
-    // MoE tiles walk 8 tile rows per column group: an expert's row tiles then
-    // share its weight panel in L2 more often (cfg4: 1% faster than 4; dense
-    // tiles keep 4, which the split reduction's tile order also assumes)
-    if constexpr (kGrouped || kSorted) {
-        static_assert(!kSplitK, "MoE layouts run data-parallel");
-        if (!tile_coords_dealt<kMoeGroupM>(a.tiles_m, a.tiles_n, tm, tn)) return;
-    } else {
-        tile_coords<4>(a.tiles_m, a.tiles_n, a.tile_base, kSplitK ? a.splits : 1, tm, tn, trel, split);
-    }
-    const int m0 = tm * BM, n0 = tn * BN;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave / WN, wn = wave % WN;
-    // K blocks of this workgroup: [kb0, kb0 + KB)
-    const int kb0 = kSplitK ? split * a.kb_per_split : 0;
-    const int KB = kSplitK ? min(a.K / kRowB - kb0, a.kb_per_split) : a.K / kRowB;
-    const int NB = (a.N + kGroup - 1) / kGroup;
-
-    const uint8_t* Wbase = a.W;
-    const float* sWbase = a.sW;
-    int expert = 0;
-    if constexpr (kGrouped) {
-        expert = a.expert_ids[m0];
-        if (expert < 0 || expert >= a.E) return;  // padding block: C rows stay unwritten
-        Wbase += (int64_t)expert * a.w_estride;
-        sWbase += (int64_t)expert * a.sW_estride;
-    }
-    if constexpr (kSorted) {
-        // a tile lies inside one block of block_m rows (BM divides block_m)
-        if (m0 >= a.num_post_pad[0]) return;
-        expert = a.expert_ids[m0 / a.block_m];
-        if (expert < 0 || expert >= a.E) return;
-        Wbase += (int64_t)expert * a.w_estride;
-        sWbase += (int64_t)expert * a.sW_estride;
-    }
-    // routed pair of tile row r, or -1 for padding
-    auto pair_of = [&](int r) -> int {
-        const int R = m0 + r;
-        if (R >= a.M) return -1;
-        const int t = a.sorted_ids ? a.sorted_ids[R] : (R % a.block_m == 0 ? R / a.block_m : -1);
-        return (t >= 0 && t < a.num_valid) ? t : -1;
-    };
-
-    const v4i dA = kSorted ? make_desc(a.A, a.A_bytes)
-                           : make_desc(a.A + (int64_t)m0 * a.lda, (int64_t)(a.M - m0 - 1) * a.lda + a.K);
-    const v4i dW = make_desc(Wbase + (int64_t)n0 * a.ldw, (int64_t)(a.N - n0 - 1) * a.ldw + a.K);
-    const v4i dSA = make_desc(a.sA, a.sA_bytes);
-    const v4i dSW = make_desc(sWbase, (int64_t)NB * a.sW_ld * 4);
-
-    // DMA lane mapping: one instruction = 8 rows x 128 B starting at row
-    // r0 = 8 q; lane i fills slot i % 8 of row r0 + i / 8 with global chunk
-    // (i % 8) ^ swz(r0 + i / 8) = (i % 8) ^ ((i >> 4) | 4 (q & 1)).
-    constexpr int kAInstr = BM / (8 * kWaves), kBInstr = BN / (8 * kWaves);   // 8-row DMAs per wave
-    static_assert(kAInstr % 2 == 0 && kBInstr % 2 == 0, "even instruction counts keep q & 1 == i & 1");
-    const int drow = lane >> 3;
-    const int ch_e = ((lane & 7) ^ (lane >> 4)) << 4;
-    const int ch_o = ((lane & 7) ^ ((lane >> 4) | 4)) << 4;
-    const int a_e = (int)((wave * kAInstr * 8 + drow) * a.lda) + ch_e + kb0 * kRowB;
-    const int a_o = a_e - ch_e + ch_o;
-    const int w_e = (int)((wave * kBInstr * 8 + drow) * a.ldw) + ch_e + kb0 * kRowB;
-    const int w_o = w_e - ch_e + ch_o;
-    // sorted layout: byte offset of each DMA row of this lane's A instructions
-    // (gathered rows; padding reads zeros)
-    int a_row[kSorted ? kAInstr : 1];
-    if constexpr (kSorted) {
-#pragma unroll
-        for (int i = 0; i < kAInstr; ++i) {
-            const int t = pair_of(wave * kAInstr * 8 + i * 8 + drow);
-            a_row[i] = t >= 0 ? (t / a.a_row_div) * (int)a.lda + kb0 * kRowB : kOob;
-        }
-    }
-    const int sa_row = wave * 64 + lane;
-    int sa_src = -1;    // activation-scale row of this lane's tile row
-    if (sa_row < BM) {
-        if constexpr (kSorted) {
-            const int t = pair_of(sa_row);
-            sa_src = t < 0 ? -1 : a.sa_sorted ? m0 + sa_row : t / a.a_row_div;
-        } else {
-            sa_src = m0 + sa_row < a.M ? m0 + sa_row : -1;
-        }
-    }
-    const bool sa_live = sa_src >= 0;
-    const int sa_kstep = sa_live ? (int)(a.sA_sk * 4) : 0;
-    const int sa_off0 = sa_live ? (int)((int64_t)sa_src * a.sA_sm * 4) + kb0 * sa_kstep : kOob;
-    const bool sw_live = (lane < (BN + 127) / 128) & (n0 / 128 + lane < NB);
-    const int sw_kstep = sw_live ? 4 : 0;
-    const int sw_off0 = sw_live ? (n0 / 128 + lane) * (int)a.sW_ld * 4 + kb0 * 4 : kOob;
-    constexpr int kDma = kAInstr + kBInstr + 2;  // DMA instructions per wave per stage
-    // Weight rows stream past L2 (non-temporal) where the weights dominate the
-    // traffic: the 128-column dense tiles (chosen only for M <= 128) and the
-    // grouped and sorted MoE tiles.  The large dense tiles keep the default,
-    // which measures faster where A and W tiles are both re-read from L2.
-    constexpr bool kWeightNt = (BN == 128) || kGrouped || kSorted;
-
-    // DMA instruction d (0 <= d < kDma) of K block s -> LDS buffer s % kStages:
-    // the two scale vectors, then the A rows, then the W rows.  `live` false
-    // turns the load into an out-of-range (zero) read, so the loop never
-    // branches around it and every stage issues the same number of loads.
-    auto issue_one = [&](int s, bool live, int d) {
-        const uint32_t base = lds0 + (s % kStages) * kStage;
-        const int k0 = s * kRowB;
-        if (d == 0) {
-            dma_b32(dSA, base + kA + kB + wave * 256, live ? sa_off0 + s * sa_kstep : kOob);
-        } else if (d == 1) {
-            dma_b32(dSW, base + kA + kB + kSA + wave * 256, live ? sw_off0 + s * sw_kstep : kOob);
-        } else if (d < 2 + kAInstr) {
-            const int i = d - 2;
-            int off;
-            if constexpr (kSorted) off = a_row[i] + ((i & 1) ? ch_o : ch_e) + k0;
-            else off = ((i & 1) ? a_o : a_e) + (int)(i * 8 * a.lda) + k0;
-            dma_b128(dA, base + (wave * kAInstr + i) * 1024, live ? off : kOob);
-        } else {
-            const int i = d - 2 - kAInstr;
-            const uint32_t dst = base + kA + (wave * kBInstr + i) * 1024;
-            const int off = live ? ((i & 1) ? w_o : w_e) + (int)(i * 8 * a.ldw) + k0 : kOob;
-            if constexpr (kWeightNt) dma_b128_nt(dW, dst, off);
-            else dma_b128(dW, dst, off);
-        }
-    };
-
-    const int nb_local = (wn * TN) / 128;  // this wavefront's weight-scale block within the tile
-    // per-lane fragment offsets: row (lane & 31) of a 32-row fragment, chunk
-    // c = 4 kk + 2 (lane >> 5) + h for 16-B half h; swz(row) = (lane >> 1) & 7
-    const int fs = (lane >> 1) & 7;
-    const int frow = (lane & 31) * kRowB;
-
-    v16f acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = v16f{};
-
-    auto stage_ptr = [&](int s) -> const uint8_t* { return smem + (s % kStages) * kStage; };
-    // 16-B read q (0 <= q < 2 (FM + FN)) of K half kk: half q % 2 of fragment
-    // q / 2, A fragments first
-    auto read_half = [&](const uint8_t* st, int kk, int q, v8i (&af)[FM], v8i (&bf)[FN]) {
-        const int f = q >> 1, h = q & 1;
-        const int c = 4 * kk + 2 * (lane >> 5) + h;
-        const uint8_t* tile = f < FM ? st + (wm * TM + f * 32) * kRowB : st + kA + (wn * TN + (f - FM) * 32) * kRowB;
-        const v4i v = *reinterpret_cast<const v4i*>(tile + frow + ((c ^ fs) << 4));
-        if (f < FM) {
-            if (h) af[f].hi = v; else af[f].lo = v;
-        } else {
-            if (h) bf[f - FM].hi = v; else bf[f - FM].lo = v;
-        }
-    };
-    // raw fp32 scales of a stage: per fragment row (lane & 31) and the
-    // wavefront's weight block (converted to E8M0 only when consumed)
-    auto read_scales = [&](const uint8_t* st, float (&sa)[FM], float& sw) {
-        const float* ssa = reinterpret_cast<const float*>(st + kA + kB);
-        const float* ssw = reinterpret_cast<const float*>(st + kA + kB + kSA + wave * 256);
-#pragma unroll
-        for (int i = 0; i < FM; ++i) sa[i] = ssa[wm * TM + i * 32 + (lane & 31)];
-        sw = ssw[nb_local];
-    };
-    v8i fa0[FM], fb0[FN], fa1[FM], fb1[FN];
-    float sa[FM], sw = 0.f, nsa[FM], nsw = 0.f;
-    int ea[FM], eb = 0, nea[FM], neb = 0;
-    // FP32 contract: mantissa product mu = mant(sA) mant(sW) in [1, 4) of the
-    // current block per fragment row, and the rescale ratio mu_prev / mu for
-    // the block about to start (the exponents go to the MFMA).
-    float mu[kUe8m0 ? 1 : FM], ratio[kUe8m0 ? 1 : FM];
-    bool rescale = false;
-    // Grouped FP32 contract: rows of another expert (padding) are never
-    // stored, so their scales, whatever the buffer holds, must not trigger
-    // rescales; they keep a mantissa product of 1.
-    bool row_live[kGrouped && !kUe8m0 ? FM : 1];
-    if constexpr (kGrouped && !kUe8m0) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            const int r = m0 + wm * TM + i * 32 + (lane & 31);
-            row_live[i] = r < a.M && a.expert_ids[r] == expert;
-        }
-    }
-    // E8M0 bytes of raw scales; FP32 contract: the first block's mantissa
-    // products (step < 0), or the ratios to the next block's products, which
-    // then become current (their block follows)
-    auto convert = [&](const float (&s)[FM], float w, int (&e)[FM], int& f, int step) {
-        if constexpr (kUe8m0) {
-#pragma unroll
-            for (int i = 0; i < FM; ++i) e[i] = ue8m0_ceil_byte(s[i]);
-            f = ue8m0_ceil_byte(w);
-        } else {
-            const float mw = scale_mant(w);
-            float m[FM];
-            bool diff = false;
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                e[i] = scale_exp_byte(s[i]);
-                m[i] = scale_mant(s[i]) * mw;
-                if constexpr (kGrouped) m[i] = row_live[i] ? m[i] : 1.f;
-                diff |= m[i] != mu[i];
-            }
-            f = scale_exp_byte(w);
-            if (step >= 0) {
-                // the quotient of two different values in [1, 4) is never 1,
-                // so the divisions are needed exactly when a product changed
-                rescale = __any(diff);
-                if (rescale) {
-#pragma unroll
-                    for (int i = 0; i < FM; ++i) ratio[i] = mu[i] == m[i] ? 1.f : mu[i] / m[i];
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < FM; ++i) mu[i] = m[i];
-        }
-    };
-    // MFMA t (0 <= t < FM FN) of a sub-step.  The product is formed as
-    // D^T = W A^T (W fragment as the MFMA's A operand), so accumulator
-    // register r of lane l holds output row (l % 32) of fragment i and column
-    // 8 (r / 4) + 4 (l / 32) + r % 4 of fragment j: every lane owns runs of
-    // four consecutive columns of one row, ready for packed stores.  The
-    // block's scales enter as E8M0 operands: eb for the W rows, ea[i] per A row.
-    auto mfma_at = [&](int t, const v8i (&fa)[FM], const v8i (&fb)[FN]) {
-        const int i = t / FN, j = t % FN;
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], acc[i][j], 0, 0, 0, eb, 0, ea[i]);
-    };
-    // FP32 contract: bring the running sum to the new block's mantissa base
-    // before the block's first MFMA.  One uniform branch around all of it,
-    // so the accumulators only leave the MFMA registers when a ratio is not 1.
-    auto rescale_all = [&]() {
-        if constexpr (!kUe8m0) {
-            if (rescale) {
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] * ratio[i];
-            }
-        }
-    };
-
-    // Each sub-step is laid out as FM*FN issue slots: one MFMA, then this
-    // slot's share of the LDS fragment reads and (sub-step 1) of the next
-    // stage's DMAs.  sched_barrier keeps the slots in order, so the single
-    // texture-address unit of the CU sees a steady trickle of DMAs from each
-    // wavefront instead of a burst that stalls the MFMA issue behind it.
-    constexpr int kT = FM * FN;           // MFMAs per sub-step
-    constexpr int kR = 2 * (FM + FN);     // 16-B fragment reads per sub-step
-
-    // prologue: blocks 0 .. kStages-1 in flight, block 0 published
-#pragma unroll
-    for (int s = 0; s < kStages; ++s)
-#pragma unroll
-        for (int d = 0; d < kDma; ++d) issue_one(s, s < KB, d);
-    wait_dma_n<(kStages - 1) * kDma>();
-    __syncthreads();
-    read_scales(stage_ptr(0), sa, sw);
-#pragma unroll
-    for (int q = 0; q < kR; ++q) read_half(stage_ptr(0), 0, q, fa0, fb0);
-
-    convert(sa, sw, ea, eb, -1);
-
-    for (int kb = 0; kb < KB; ++kb) {
-        const uint8_t* cur = stage_ptr(kb);
-        rescale_all();
-        // ---- sub-step 0: K half 0 of block kb; read K half 1
-#pragma unroll
-        for (int t = 0; t < kT; ++t) {
-            mfma_at(t, fa0, fb0);
-#pragma unroll
-            for (int q = t * kR / kT; q < (t + 1) * kR / kT; ++q) read_half(cur, 1, q, fa1, fb1);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-
-        // ---- hand-off: publish block kb+1, free buffer kb for block kb+kStages
-        wait_dma_n<(kStages - 2) * kDma>();
-        wait_lds();
-        __syncthreads();
-
-        // ---- sub-step 1: K half 1 of block kb; read K half 0 of block kb+1
-        // (past the last block this reads a zero-filled buffer, unused) and
-        // DMA block kb+kStages into the freed buffer
-        const uint8_t* nxt = stage_ptr(kb + 1);
-        const int snext = kb + kStages;
-        const bool live = snext < KB;
-#pragma unroll
-        for (int t = 0; t < kT; ++t) {
-            mfma_at(t, fa1, fb1);
-            if (t == 0) read_scales(nxt, nsa, nsw);
-            // converted scales of block kb+1, half a sub-step after their
-            // reads (FP32 contract: none past the last block, whose mantissa
-            // products the store needs)
-            if (t == kT / 2) {
-                if constexpr (kUe8m0) convert(nsa, nsw, nea, neb, kb);
-                else if (kb + 1 < KB) convert(nsa, nsw, nea, neb, kb);
-            }
-#pragma unroll
-            for (int q = t * kR / kT; q < (t + 1) * kR / kT; ++q) read_half(nxt, 0, q, fa0, fb0);
-#pragma unroll
-            for (int d = t * kDma / kT; d < (t + 1) * kDma / kT; ++d) issue_one(snext, live, d);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        // FP32 contract: the running sum is kept in units of the current
-        // block's mantissa product, S_kb = S_{kb-1} mu_{kb-1} / mu_kb + 2^e P_kb
-        // (rescale_at applies the ratio as block kb+1 starts), so the true
-        // sum after the last block is S mu_last.  Ratios of 1 (power-of-two
-        // scales, or equal mantissas) skip the multiplies.
-#pragma unroll
-        for (int i = 0; i < FM; ++i) ea[i] = nea[i];
-        eb = neb;
-    }
-    // the trailing (out-of-range) loads still target this workgroup's LDS
-    wait_dma();
-    if constexpr (!kUe8m0) {
-        bool any = false;
-#pragma unroll
-        for (int i = 0; i < FM; ++i) any |= mu[i] != 1.f;
-        if (__any(any)) {
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] * mu[i];
-        }
-    }
-
-    // Epilogue of a tile: fp32 -> bf16 (RNE), written with raw buffer stores
-    // whose range ends at the last row of D, so rows past M (and any offset
-    // set to kOob) are dropped by the hardware and no store is branched
-    // around.  Lanes l and l + 32 hold the two 4-column halves of each
-    // 8-column run of a row; one permlane32 swap per dword pair gives each
-    // lane a whole 16-B run.  D rows that are not 16-B aligned (or N not a
-    // multiple of 8 on a ragged tile) take 2-B element stores instead.
-    // Split-K epilogue: the fp32 partial sums, one 16-B store per run of four
-    // columns, into this (split, tile)'s BM x BN slab (rows past M dropped by
-    // the range).
-    auto epilogue_partial = [&]() {
-        const int64_t bytes = (int64_t)min(a.M - m0, BM) * BN * 4;
-        const __amdgpu_buffer_rsrc_t dP = __builtin_amdgcn_make_buffer_rsrc(
-            a.P + ((int64_t)split * a.tile_count + trel) * BM * BN, (short)0, (int)bytes, (int)kRsrcWord3);
-        const int ncol = wn * TN + 4 * (lane >> 5);
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            const int roff = (wm * TM + i * 32 + (lane & 31)) * BN * 4;
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-#pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                    const int voff = roff + (ncol + j * 32 + 8 * p) * 4;
-                    const v4i v = {__float_as_int(acc[i][j][4 * p]), __float_as_int(acc[i][j][4 * p + 1]),
-                                   __float_as_int(acc[i][j][4 * p + 2]), __float_as_int(acc[i][j][4 * p + 3])};
-                    if (a.flags)
-                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), dP, voff, 0,
-                                                               kDeviceCoherent);
-                    else
-                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), dP, voff, 0, 0);
-                }
-        }
-    };
-
-    // sorted layout: each fragment row's output row (its pair) and factor
-    int out_row[kSorted ? FM : 1];
-    if constexpr (kSorted) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            out_row[i] = pair_of(wm * TM + i * 32 + (lane & 31));
-            if (a.row_weight) {
-                const float f = out_row[i] >= 0 ? a.row_weight[out_row[i]] : 0.f;
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] * f;
-            }
-        }
-    }
-    // row byte offset of fragment row i in D (kOob: not stored)
-    auto out_off = [&](int i) -> int {
-        const int row = wm * TM + i * 32 + (lane & 31);
-        if constexpr (kSorted) return out_row[i] >= 0 ? out_row[i] * (int)a.ldd * 2 : kOob;
-        else if constexpr (kGrouped)
-            return (m0 + row < a.M && a.expert_ids[m0 + row] == expert) ? row * (int)a.ldd * 2 : kOob;
-        else return row * (int)a.ldd * 2;
-    };
-
-    auto epilogue = [&]() {
-        const int64_t bytes = kSorted ? a.D_bytes
-                                      : std::min<int64_t>((int64_t)(a.M - m0 - 1) * a.ldd * 2 + (int64_t)a.N * 2,
-                                                          (int64_t)BM * a.ldd * 2);
-        const __amdgpu_buffer_rsrc_t dD = __builtin_amdgcn_make_buffer_rsrc(
-            kSorted ? a.D : a.D + (int64_t)m0 * a.ldd, (short)0, (int)std::min<int64_t>(bytes, 0x7FFFFFFFLL),
-            (int)kRsrcWord3);
-        const int h = lane >> 5;
-        const int ncol = n0 + wn * TN + 8 * h;
-        const bool vec = a.vec_store && (n0 + BN <= a.N || a.N % 8 == 0);
-        if (vec) {
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                const int roff = out_off(i);
-                const bool ok = roff != kOob;
-#pragma unroll
-                for (int j = 0; j < FN; ++j) {
-#pragma unroll
-                    for (int p = 0; p < 4; p += 2) {
-                        // dwords of runs p (X) and p + 1 (Y): columns 8 p + 4 h + {0..3}
-                        const uint32_t x0 = pack_bf16(acc[i][j][4 * p], acc[i][j][4 * p + 1]);
-                        const uint32_t x1 = pack_bf16(acc[i][j][4 * p + 2], acc[i][j][4 * p + 3]);
-                        const uint32_t y0 = pack_bf16(acc[i][j][4 * p + 4], acc[i][j][4 * p + 5]);
-                        const uint32_t y1 = pack_bf16(acc[i][j][4 * p + 6], acc[i][j][4 * p + 7]);
-                        // lanes < 32 end with run p (own half, then lane + 32's);
-                        // lanes >= 32 with run p + 1 (lane - 32's half, then own)
-                        const auto s0 = __builtin_amdgcn_permlane32_swap(x0, y0, false, false);
-                        const auto s1 = __builtin_amdgcn_permlane32_swap(x1, y1, false, false);
-                        const int n = ncol + j * 32 + 8 * p;
-                        const int voff = (ok && n < a.N) ? roff + n * 2 : kOob;
-                        const u32x4 v = {(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
-                        __builtin_amdgcn_raw_buffer_store_b128(v, dD, voff, 0, 0);
-                    }
-                }
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                const int roff = out_off(i);
-                const bool ok = roff != kOob;
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int n = n0 + wn * TN + j * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                        const int voff = (ok && n < a.N) ? roff + n * 2 : kOob;
-                        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(pack_bf16(acc[i][j][r], 0.f) & 0xFFFFu), dD,
-                                                              voff, 0, 0);
-                    }
-            }
-        }
-    };
-
-    if constexpr (kSplitK) {
-        epilogue_partial();
-        // the fused sum is only planned for the 64-row tiles (M <= 64)
-        if constexpr (BM <= 64) if (a.flags) {
-            // Fused reduction: every wavefront's (device-coherent) slab stores
-            // have completed before its workgroup counts itself in; the
-            // workgroup that brings the tile's count to `splits` sums all
-            // slabs (its own included, in split order, with device-coherent
-            // loads) and leaves the counter at zero.  No workgroup waits for
-            // another, so nothing depends on residency.
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();  // also: the main loop's LDS reads are done, smem is free
-            unsigned* last = reinterpret_cast<unsigned*>(smem);
-            if (threadIdx.x == 0) {
-                const unsigned prev =
-                    __hip_atomic_fetch_add(a.flags + trel, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const unsigned is_last = prev + 1 == (unsigned)a.splits;
-                if (is_last) __hip_atomic_store(a.flags + trel, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                *last = is_last;
-            }
-            __syncthreads();
-            if (*last) {
-                constexpr int kRuns = BN / 4, kRowStep = 64 * kWaves / kRuns;
-                static_assert((64 * kWaves) % kRuns == 0, "whole rows per pass");
-                splitk_sum_rows<BM, BN, kDeviceCoherent, (BM + kRowStep - 1) / kRowStep>(
-                    a, trel, m0, n0, (int)threadIdx.x / kRuns, min(a.M - m0, BM), kRowStep,
-                    ((int)threadIdx.x % kRuns) * 4);
-            }
-        }
-    } else {
-        epilogue();
-    }
-}
-
-// Split-K reduction: D = bf16(sum_s slab[s]) summed in split order
-// (deterministic).  One workgroup per 8-row strip of a tile of the split
-// launch (blockIdx.x = tile * BM/8 + strip), one float4 run per lane.
-template <int BM, int BN>
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a) {
-    constexpr int kRuns = BN / 4, kRows = 256 / kRuns;   // rows per pass of the workgroup
-    constexpr int kStrips = BM / 8;
-    const int trel = blockIdx.x / kStrips, strip = blockIdx.x - trel * kStrips;
-    int tm, tn;
-    {
-        constexpr int kGroupM = 4;
-        const int t = a.tile_base + trel;
-        const int group = kGroupM * a.tiles_n;
-        const int g = t / group;
-        const int first_m = g * kGroupM;
-        const int gm = min(a.tiles_m - first_m, kGroupM);
-        const int w = t - g * group;
-        tm = first_m + w % gm;
-        tn = w / gm;
-    }
-    const int m0 = tm * BM, n0 = tn * BN;
-    splitk_sum_rows<BM, BN, 0, (8 + kRows - 1) / kRows>(a, trel, m0, n0, strip * 8 + (int)threadIdx.x / kRuns,
-                                                        min(strip * 8 + 8, a.M - m0), kRows,
-                                                        ((int)threadIdx.x % kRuns) * 4);
-}
-
-// LDS bytes of a tile configuration; configurations that fit twice into a
-// CU's 160 KB run two workgroups per CU.
-constexpr int gemm_lds_bytes(int bm, int bn, int stages) { return stages * (bm * kRowB + bn * kRowB + 2048); }
-constexpr int gemm_occupancy(int bm, int bn, int stages) { return gemm_lds_bytes(bm, bn, stages) <= 80 * 1024 ? 2 : 1; }
-
-// Launch plan of a dense GEMM.  Whole waves of tiles run data-parallel in
-// one launch; when the last wave would be partly empty, its tiles (the
-// "tail") may instead run split-K in a second launch over all workgroup
-// slots, followed by the reduction.
-struct Schedule {
-    int bm = 0, bn = 0, stages = 0;
-    int64_t tiles = 0;
-    int64_t dp_tiles = 0;         // tiles [0, dp_tiles) data-parallel
-    int splits = 1, kb_per_split = 0;  // the tail [dp_tiles, tiles)
-    int64_t ws_bytes = 0;         // fp32 slabs of the tail
-};
 
 // Only tails whose split workgroups fit in one wave are split.  Cost model
 // in K-block times of one workgroup slot: a pipeline fill of about two
@@ -898,13 +60,12 @@ static void plan_tail(Schedule& s, int64_t M, int KBT) {
 // a counter.  Every launch leaves its counters at zero.  When the regions are
 // used up (or the array's address cannot be had), launches fall back to the
 // separate reduction kernel.
-constexpr int kFusedReduceRows = 32;   // 64 rows measure the same as the separate launch
 constexpr int kFlagRegion = 1024;   // tail tiles per launch; a tail is below 2 x CUs tiles
 constexpr int kFlagRegions = 512;
 constexpr int kFlagDevices = 64;
 __device__ __attribute__((aligned(256))) unsigned g_splitk_flags[kFlagRegions * kFlagRegion];
 
-static unsigned* splitk_flags_for(hipStream_t st, int64_t tail_tiles) {
+unsigned* splitk_flags_for(hipStream_t st, int64_t tail_tiles) {
     static std::mutex mu;
     static unsigned* base[kFlagDevices] = {};
     static int used[kFlagDevices] = {};
@@ -935,57 +96,6 @@ static unsigned* splitk_flags_for(hipStream_t st, int64_t tail_tiles) {
         it = region.emplace(key, used[dev]++).first;
     }
     return base[dev] + (int64_t)it->second * kFlagRegion;
-}
-
-template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, int kWaves = 4>
-static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const char* what) {
-    a.tiles_m = (a.M + BM - 1) / BM;
-    a.tiles_n = (a.N + BN - 1) / BN;
-    const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
-    KBN_CHECK_ARG(tiles <= 0x7FFFFFFFLL, "%s: too many tiles", what);
-    const int64_t dp = (!kGrouped && a.P && sc.splits > 1) ? sc.dp_tiles : tiles;
-    if (dp > 0) {
-        a.tile_base = 0;
-        a.tile_count = (int)dp;
-        a.splits = 1;
-        a.kb_per_split = a.K / kRowB;
-        const int64_t grid = kGrouped ? moe_dealt_grid(a.tiles_m, a.tiles_n) : dp;
-        KBN_CHECK_ARG(grid <= 0x7FFFFFFFLL, "%s: too many tiles", what);
-        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped, false, kWaves>
-            <<<dim3((unsigned)grid), dim3(64 * kWaves), 0, st>>>(a);
-        KBN_CHECK_LAUNCH(what);
-    }
-    if (dp < tiles) {
-        // the plan must be for this tile shape, and its slabs must fit the workspace
-        KBN_CHECK_ARG(sc.bm == BM && sc.bn == BN && sc.tiles == tiles, "%s: split plan does not match the %dx%d tiles",
-                      what, BM, BN);
-        const int64_t need = (int64_t)sc.splits * (tiles - dp) * BM * BN * 4;
-        KBN_CHECK_ARG(need < 0x7FFFFFFFLL, "%s: split slabs span >= 2 GiB", what);
-        KBN_CHECK_ARG(sc.splits >= 2 && sc.kb_per_split >= 1 && need <= a.ws_bytes,
-                      "%s: workspace of %lld bytes is smaller than the %lld the split plan writes", what,
-                      (long long)a.ws_bytes, (long long)need);
-        KBN_CHECK_ARG((int64_t)sc.splits * sc.kb_per_split >= a.K / kRowB &&
-                          (int64_t)(sc.splits - 1) * sc.kb_per_split < a.K / kRowB,
-                      "%s: split plan does not cover K in %d non-empty splits", what, sc.splits);
-        a.tile_base = (int)dp;
-        a.tile_count = (int)(tiles - dp);
-        a.splits = sc.splits;
-        a.kb_per_split = sc.kb_per_split;
-        const int64_t blocks = (tiles - dp) * sc.splits;
-        KBN_CHECK_ARG(blocks <= 0x7FFFFFFFLL, "%s: too many tiles", what);
-        // Few rows: the tile's last workgroup sums the slabs (one launch
-        // less).  More rows: that sum would run on one workgroup per tile at
-        // the end of the launch, so the separate kernel spreads it instead.
-        a.flags = (BM <= 64 && a.M <= kFusedReduceRows) ? splitk_flags_for(st, tiles - dp) : nullptr;
-        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped && false, true, kWaves>
-            <<<dim3((unsigned)blocks), dim3(64 * kWaves), 0, st>>>(a);
-        KBN_CHECK_LAUNCH(what);
-        if (!a.flags) {
-            splitk_reduce_kernel<BM, BN><<<dim3((unsigned)((tiles - dp) * (BM / 8))), dim3(256), 0, st>>>(a);
-            KBN_CHECK_LAUNCH(what);
-        }
-    }
-    return 0;
 }
 
 // Sorted-token layout: the activation scales of every row R below the padded
@@ -1090,12 +200,7 @@ static Schedule dense_schedule(int64_t M, int64_t N, int64_t K, int ue8m0, bool 
 template <bool kUe8m0>
 static int dispatch_dense(const GemmArgs& a, const Schedule& sc, int64_t K, hipStream_t st, const char* what) {
     if constexpr (kUe8m0) {
-        if (sc.bm == 256 && sc.bn == 256) {
-            // short K (few K blocks per tile): two wavefronts per SIMD hide
-            // the per-tile pipeline fill and epilogue better
-            if (K <= 2048) return launch_gemm<256, 256, 2, true, false, 8>(a, sc, st, what);
-            return launch_gemm<256, 256, 2, true, false>(a, sc, st, what);
-        }
+        if (sc.bm == 256 && sc.bn == 256) return launch_gemm_256(a, sc, K, st, what);
     } else {
         if (sc.bm == 128 && sc.bn == 256) return launch_gemm<128, 256, 3, false, false>(a, sc, st, what);
     }
