@@ -115,6 +115,42 @@ def test_fused_moe_gemm_matches_oracle(gpu_device, M, k, E, N, K, block, weighte
         assert bool((C[unplaced] == 7.0).all())
 
 
+def test_fused_moe_gemm_dealt_tile_order(gpu_device):
+    """A padded row grid large enough that whole column groups of row tiles
+    are dealt to the XCDs round-robin (more than 8 groups of 16 row tiles)
+    and whose tail holds row tiles no expert owns: every placed pair matches
+    the oracle on sampled columns of both column tiles, incl. tile edges, and
+    the two unplaceable pairs stay untouched."""
+    from kb_nano_amd import MoeGroupedGemm
+    dev = gpu_device
+    M, k, E, N, K, block = 2048, 8, 64, 512, 256, 128
+    print("fused_moe_gemm dealt tile order", flush=True)
+    ids = _routing(M, k, E, seed=77, invalid=True)
+    a = seeded_bf16((M, K), seed=78)
+    qa, sa = oracle.quant_group128(bf16_bits(a))
+    B, sB = _experts(E, N, K, seed=79)
+    s_ids, e_ids, total, _ = oracle.moe_align_block_size(ids, E, block)
+    padded = s_ids.size                     # rows of the padded grid (the reference's upper bound)
+    assert padded // block >= 8 * 16 * 1 and total < padded - 2 * block   # dealt rounds, empty tail
+    e_buf = np.full(-(-padded // block), -1, dtype=np.int32)
+    e_buf[:e_ids.size] = e_ids
+    C = torch.full((M * k, N), 7.0, dtype=torch.bfloat16, device=dev)
+    MoeGroupedGemm()(to_fp8(qa, dev), to_fp8(B, dev), C, None,
+                     torch.from_numpy(s_ids).to(dev), torch.from_numpy(e_buf).to(dev),
+                     torch.tensor([total], dtype=torch.int32, device=dev), False, k,
+                     config={"BLOCK_SIZE_M": block}, a_scale=torch.from_numpy(sa).to(dev),
+                     b_scale=torch.from_numpy(sB).to(dev), use_fp8_w8a8=True, block_shape=[128, 128])
+    torch.cuda.synchronize()
+    cols = np.array([0, 1, 127, 128, 200, 255, 256, 300, 383, 384, 500, 511])
+    ref = oracle.fused_moe_gemm_sample(qa, sa, B, sB, s_ids, e_ids, total, block, M * k, k, cols=cols)
+    pairs = sorted(ref)
+    assert len(pairs) == M * k - 2
+    got = C[pairs][:, torch.from_numpy(cols).to(dev)]
+    assert_gemm_close(got, np.stack([ref[t] for t in pairs]), "sorted-token GEMM, dealt tiles")
+    unplaced = [t for t in range(M * k) if t not in ref]
+    assert bool((C[unplaced] == 7.0).all())
+
+
 def test_fused_moe_gemm_naive_blocks(gpu_device):
     """No sorted list: block b holds pair b alone (the reference's naive
     assignment for very few tokens)."""
