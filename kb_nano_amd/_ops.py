@@ -178,14 +178,15 @@ def fp8_gemm_nt(q_input: torch.Tensor, input_scale: torch.Tensor, weight: torch.
         return
     L = lib()
     # small-M / few-tile shapes split K over more workgroups; the fp32
-    # partials live in a workspace from the caching allocator (stream-ordered
-    # on the launch stream, so concurrent streams never share one)
+    # partials live in the launch stream's workspace (_workspace), so
+    # concurrent streams never share one
     ws_bytes = _gemm_workspace_bytes(L, idx, M, N, K, ue8m0)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=output.device) if ws_bytes else None
+    st = _raw_stream(idx)
+    ws = _workspace(ws_bytes, idx, st, output.device) if ws_bytes else None
     rc = L.kbn_fp8_gemm_nt_ws(
         q_input.data_ptr(), qs[0], input_scale.data_ptr(), ss[0], ss[1], weight.data_ptr(), ws_[0],
         weight_scale.data_ptr(), sws_[0], output.data_ptr(), os_[0], M, N, K, 1 if ue8m0 else 0,
-        ws.data_ptr() if ws is not None else None, ws_bytes, _raw_stream(idx))
+        ws.data_ptr() if ws is not None else None, ws_bytes, st)
     if rc:
         check(rc, what)
 
@@ -223,16 +224,36 @@ def fp8_linear_forward(x: torch.Tensor, q_buf: torch.Tensor, s_buf: torch.Tensor
     ue8m0 = is_e8m0_used() if use_ue8m0 is None else bool(use_ue8m0)
     L = lib()
     ws_bytes = _gemm_workspace_bytes(L, idx, M, N, K, ue8m0)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=out_buf.device) if ws_bytes else None
+    st = _raw_stream(idx)
+    ws = _workspace(ws_bytes, idx, st, out_buf.device) if ws_bytes else None
     rc = L.kbn_fp8_linear_forward(
         x.data_ptr(), M, K, xs[0], q_buf.data_ptr(), qs[0], s_buf.data_ptr(), ss[0], ss[1], QUANT_EPS, 1,
         weight.data_ptr(), ws_[0], weight_scale.data_ptr(), wss[0], out_buf.data_ptr(), os_[0], N,
-        1 if ue8m0 else 0, ws.data_ptr() if ws is not None else None, ws_bytes, _raw_stream(idx))
+        1 if ue8m0 else 0, ws.data_ptr() if ws is not None else None, ws_bytes, st)
     if rc:
         check(rc, what)
 
 
 _WS_CACHE: dict = {}
+_WS_BUFS: dict = {}
+
+
+def _workspace(nbytes: int, idx: int, stream: int, device) -> torch.Tensor:
+    """Scratch for one launch on ``stream``.  Eager launches on a stream reuse
+    one buffer per (device, stream), grown as needed: launches on a stream
+    run in order, so a buffer is free again when the next launch on that
+    stream reads it, and a replaced buffer goes back to the caching allocator,
+    which hands it out again only in that stream's order.  Under graph capture
+    every launch takes its own buffer from the capture's memory pool, as
+    before (a graph keeps what it was captured with)."""
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    key = (idx, stream)
+    buf = _WS_BUFS.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        _WS_BUFS[key] = buf
+    return buf
 
 
 def _gemm_workspace_bytes(L, idx: int, M, N, K, ue8m0) -> int:
