@@ -14,10 +14,21 @@
 
 namespace kbn {
 
-// Only tails whose split workgroups fit in one wave are split.  Cost model
-// in K-block times of one workgroup slot: a pipeline fill of about two
-// blocks per workgroup, the fp32 partial slab store per split workgroup, and
-// the reduction's slab traffic spread over all CUs plus one launch.
+// Only tails whose split workgroups fit in one wave are split (more waves
+// never measured faster, and the allocation-free entry point's scratch is
+// sized for one wave).  Cost model in microseconds, fitted to sweeps of the
+// split count over the 64x128, 128x128 and 256x256 tiles on MI355X:
+//  * a workgroup streams about 55 KB of A and W tile rows per microsecond,
+//    so a K block takes (bm + bn) * 128 B / 55 KB/us, and every workgroup
+//    pays a pipeline fill of about two blocks;
+//  * a split plan adds a fixed cost (slab stores and the reduction: about
+//    3 us with the separate reduction launch, 2 us when the split launch
+//    sums the slabs itself), a cost per split (the depth of each tile's
+//    sum: 0.2 / 0.4 us) and the slab traffic (0.45 us per MB of fp32
+//    partials).
+// Short K therefore stays unsplit (e.g. 128 x 12288 x 1536: 11.2 us data-
+// parallel against 20.0 us split in two), and long K takes fewer, longer
+// splits than a traffic-only model picks.
 static void plan_tail(Schedule& s, int64_t M, int KBT) {
     const int occ = gemm_occupancy(s.bm, s.bn, s.stages);
     const int cus = cu_count();
@@ -27,17 +38,18 @@ static void plan_tail(Schedule& s, int64_t M, int KBT) {
     s.kb_per_split = KBT;
     const int64_t waves = s.tiles / slots, rem = s.tiles - waves * slots;
     if (rem == 0 || KBT < 8) return;
-    const double fill = 2.0, kblock = (double)(s.bm + s.bn) * kRowB;
-    const double rows = (double)std::min<int64_t>(M, s.bm);
-    const double slab = rows * s.bn * 4 / kblock;               // one partial slab, in K-block times
-    double best = (double)(KBT + fill);                          // the tail as one more data-parallel wave
+    const double fill = 2.0;
+    const double t_block = (double)(s.bm + s.bn) * kRowB / 55e3;            // us per K block
+    const bool fused = s.bm <= 64 && M <= kFusedReduceRows;                  // summed in the split launch
+    const double fixed = fused ? 2.0 : 3.0, per_split = fused ? 0.4 : 0.2, per_mb = 0.45;
+    const double slab_mb = (double)std::min<int64_t>(M, s.bm) * s.bn * 4 / 1e6;   // one partial slab
+    double best = (KBT + fill) * t_block;                                    // the tail as one more data-parallel wave
     for (int sp = 2; sp <= 32 && sp <= KBT / 4; ++sp) {
         const int kbps = (KBT + sp - 1) / sp;
         const int ss = (KBT + kbps - 1) / kbps;
         const int64_t wgs = rem * ss;
-        if (wgs > slots) break;   // a tail that needs more than one wave gains nothing from splitting
-        const double cost = (double)((wgs + slots - 1) / slots) * (kbps + fill + slab) +
-                            (double)ss * rem * slab / cus + 1.0;
+        if (wgs > slots) break;
+        const double cost = (kbps + fill) * t_block + fixed + per_split * ss + per_mb * slab_mb * ss * rem;
         if (cost < best - 1e-9) {
             best = cost;
             s.splits = ss;

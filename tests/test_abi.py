@@ -83,6 +83,36 @@ def test_gemm_workspace_query():
         assert n > 0 and n % (64 * 128 * 4) == 0, (M, N, K, n)
 
 
+def test_gemm_split_plan_choices():
+    """The tail planner's choices on a 256-CU device (the planner's default
+    when no device is visible), pinned to what split-count sweeps measured
+    fastest on MI355X: 12 K blocks stay data-parallel (a split's fixed cost
+    exceeds the six blocks it saves), long K splits, and a deep split is
+    capped where the per-split reduction cost overtakes the shorter K run.
+    The workspace is one fp32 BM x BN slab per (split, tail tile)."""
+    from kb_nano_amd._lib import lib
+    L = lib()
+    if torch.cuda.device_count() > 0 and torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the plan depends on the device's CU count; pinned for 256 CUs")
+
+    def splits(M, N, K, bm, bn):
+        tiles = -(-M // bm) * -(-N // bn)
+        return L.kbn_fp8_gemm_nt_workspace_bytes(M, N, K, 1) // (tiles % 256 * bm * bn * 4) or 1
+
+    # 12 K blocks: data-parallel (measured 10.3 us against 20.1 us split in two)
+    assert splits(128, 12288, 1536, 128, 128) == 1
+    assert splits(128, 4096, 1536, 128, 128) == 1
+    assert splits(64, 12288, 1536, 64, 128) == 1
+    assert splits(8, 12288, 1536, 64, 128) == 1
+    # long K: split, and not deeper than the sweep's best
+    assert splits(128, 12288, 7168, 128, 128) == 2
+    assert splits(128, 7168, 18432, 128, 128) == 4
+    assert splits(8, 10240, 8192, 64, 128) == 3
+    assert splits(64, 8192, 28672, 64, 128) == 4
+    assert 6 <= splits(32, 2048, 7168, 64, 128) <= 8
+    assert splits(512, 4096, 7168, 256, 256) == 4
+
+
 def test_gemm_ws_rejects_bad_shapes():
     from kb_nano_amd._lib import lib
     L = lib()
