@@ -23,7 +23,7 @@ namespace kbn {
 //    pays a pipeline fill of about two blocks;
 //  * a split plan adds a fixed cost (slab stores and the reduction: about
 //    3 us with the separate reduction launch, 2 us when the split launch
-//    sums the slabs itself), a cost per split (the depth of each tile's
+//    sums the slabs itself, as fused_split_sum allows), a cost per split (the depth of each tile's
 //    sum: 0.2 / 0.4 us) and the slab traffic (0.45 us per MB of fp32
 //    partials).
 // Short K therefore stays unsplit (e.g. 128 x 12288 x 1536: 11.2 us data-
@@ -40,8 +40,7 @@ static void plan_tail(Schedule& s, int64_t M, int KBT) {
     if (rem == 0 || KBT < 8) return;
     const double fill = 2.0;
     const double t_block = (double)(s.bm + s.bn) * kRowB / 55e3;            // us per K block
-    const bool fused = s.bm <= 64 && M <= kFusedReduceRows;                  // summed in the split launch
-    const double fixed = fused ? 2.0 : 3.0, per_split = fused ? 0.4 : 0.2, per_mb = 0.45;
+    const double per_mb = 0.45;
     const double slab_mb = (double)std::min<int64_t>(M, s.bm) * s.bn * 4 / 1e6;   // one partial slab
     double best = (KBT + fill) * t_block;                                    // the tail as one more data-parallel wave
     for (int sp = 2; sp <= 32 && sp <= KBT / 4; ++sp) {
@@ -49,11 +48,14 @@ static void plan_tail(Schedule& s, int64_t M, int KBT) {
         const int ss = (KBT + kbps - 1) / kbps;
         const int64_t wgs = rem * ss;
         if (wgs > slots) break;
+        const bool fused = fused_split_sum(s.bm, M, ss);
+        const double fixed = fused ? 2.0 : 3.0, per_split = fused ? 0.4 : 0.2;
         const double cost = (kbps + fill) * t_block + fixed + per_split * ss + per_mb * slab_mb * ss * rem;
         if (cost < best - 1e-9) {
             best = cost;
             s.splits = ss;
             s.kb_per_split = kbps;
+            s.fused = fused;
         }
     }
     if (s.splits > 1) {

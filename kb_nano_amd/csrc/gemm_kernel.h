@@ -776,7 +776,7 @@ gemm_bs_kernel(const GemmArgs a) {
 
     if constexpr (kSplitK) {
         epilogue_partial();
-        // the fused sum is only planned for the 64-row tiles (M <= 64)
+        // the fused sum is only planned for the 64-row tiles (M <= 48)
         if constexpr (BM <= 64) if (a.flags) {
             // Fused reduction: every wavefront's (device-coherent) slab stores
             // have completed before its workgroup counts itself in; the
@@ -849,10 +849,21 @@ struct Schedule {
     int64_t dp_tiles = 0;         // tiles [0, dp_tiles) data-parallel
     int splits = 1, kb_per_split = 0;  // the tail [dp_tiles, tiles)
     int64_t ws_bytes = 0;         // fp32 slabs of the tail
+    bool fused = false;           // the split launch sums the slabs itself
 };
 
-// Split-K tails of at most this many rows are summed by the split launch itself.
-constexpr int kFusedReduceRows = 32;   // 64 rows measure the same as the separate launch
+// Split-K tails of the 64-row tiles summed by the split launch itself (no
+// reduction launch, about 3 us less host time per call): up to 32 rows
+// always, up to 48 rows when a tile has at most 4 splits.  The summing
+// workgroup reads its tile's slabs alone, so more rows or deeper splits
+// measure slower than the separate reduction spread over 8-row strips
+// (64 rows: 1024 x 28672 15.1 -> 17.1 us, 8192 x 28672 44.1 -> 46.3 us;
+// 40-48 rows, 3-4 splits: 10240 x 8192 21.0 -> 19.9 us, 8192 x 8192
+// 18.2 -> 17.2 us).
+constexpr int kFusedReduceRows = 32, kFusedShallowRows = 48, kFusedShallowSplits = 4;
+constexpr bool fused_split_sum(int bm, int64_t M, int splits) {
+    return bm <= 64 && (M <= kFusedReduceRows || (M <= kFusedShallowRows && splits <= kFusedShallowSplits));
+}
 // Arrival counters of the fused split-K reduction for one launch on `st`, or
 // nullptr (then the separate reduction kernel runs); defined in gemm.hip.
 unsigned* splitk_flags_for(hipStream_t st, int64_t tail_tiles);
@@ -901,7 +912,7 @@ static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const cha
         // Few rows: the tile's last workgroup sums the slabs (one launch
         // less).  More rows: that sum would run on one workgroup per tile at
         // the end of the launch, so the separate kernel spreads it instead.
-        a.flags = (BM <= 64 && a.M <= kFusedReduceRows) ? splitk_flags_for(st, tiles - dp) : nullptr;
+        a.flags = (BM <= 64 && sc.fused) ? splitk_flags_for(st, tiles - dp) : nullptr;
         gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped && false, true, kWaves>
             <<<dim3((unsigned)blocks), dim3(64 * kWaves), 0, st>>>(a);
         KBN_CHECK_LAUNCH(what);

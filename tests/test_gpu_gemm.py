@@ -376,14 +376,16 @@ def test_grouped_gemm_fp32_contract_equals_ue8m0_on_power_of_two_scales(gpu_devi
 
 @pytest.mark.parametrize("M,N,K", [(1, 8192, 8192), (8, 7168, 16384), (16, 1024, 28672), (32, 8192, 8192),
                                    (24, 10240, 8192), (64, 1024, 28672),
+                                   # 33-48 rows with at most 4 splits: summed in the split launch
+                                   (48, 8192, 8192), (40, 10240, 8192), (48, 2048, 2048),
                                    # tile counts that are not a multiple of the 8 XCDs: the splits of
                                    # some tiles run on two XCDs and count into the same counter
                                    (1, 1664, 16384), (3, 200, 32768), (16, 1920, 12288)])
 def test_gemm_split_fused_reduction_repeats_on_streams_and_graphs(gpu_device, M, N, K):
-    """Up to 32 rows, the split-K tail is summed by the last workgroup of
-    each tile to finish, counted with per-tile arrival counters that each
-    launch leaves at zero (more rows: a separate reduction launch, M=64
-    here).  The sum runs in split order whichever workgroup is last, so
+    """Up to 32 rows (48 when a tile has at most 4 splits), the split-K tail
+    is summed by the last workgroup of each tile to finish, counted with
+    per-tile arrival counters that each launch leaves at zero (more rows: a
+    separate reduction launch, M=64 here).  The sum runs in split order whichever workgroup is last, so
     every call gives the same bits: repeated calls on one stream, calls on
     two streams in flight together, and replays of a captured graph (with
     eager calls between replays) all equal the first call.  Outputs start as
