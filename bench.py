@@ -235,19 +235,22 @@ def bench_decode(steps, warmup, dev):
 
 
 def bench_linear(steps, warmup, dev):
-    """Fp8Linear.forward end to end (1x128 quant + block-scaled GEMM, the hot
-    loop of the reference's kernel runner, bench/kernels/runner.py:160-193),
-    at config 1 and the config-5 qkv shape at M in {1, 8, 32, 64}:
+    """Fp8Linear.forward end to end (1x128 quant + block-scaled GEMM, or for
+    small M the GEMM that quantizes its bf16 input itself where that is
+    faster; the hot loop of the reference's kernel runner,
+    bench/kernels/runner.py:160-193), at config 1 and the config-5 qkv and o
+    shapes at M in {1, 8, 32, 64}:
       eager_us       GPU time per call of back-to-back eager calls (events)
       eager_host_us  host time per eager call (launch path, no synchronisation)
       graph_us       time per call replayed from a captured HIP graph
-    The config-5 weights (84 MB) rotate over copies that exceed the 256 MB
+    The config-5 weights (84 / 67 MB) rotate over copies that exceed the 256 MB
     Infinity Cache; the output buffers are installed so a graph's output
     stays put (the reference's decode buffers)."""
     import torch
     from kb_nano_amd import Fp8Linear, synthetic
     out = []
-    cases = [("cfg1", 64, 2048, 2048, 0)] + [("cfg5_qkv", M, 10240, 8192, 4) for M in (1, 8, 32, 64)]
+    cases = [("cfg1", 64, 2048, 2048, 0)] + [("cfg5_qkv", M, 10240, 8192, 4) for M in (1, 8, 32, 64)] + \
+        [("cfg5_o", M, 8192, 8192, 4) for M in (1, 8, 32, 64)]
     weights = {}
     for name, M, N, K, seed in cases:
         if (N, K) not in weights:

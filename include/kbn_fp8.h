@@ -123,6 +123,31 @@ int kbn_fp8_linear_forward(const void* x_bf16, int64_t M, int64_t K, int64_t ld_
                            void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Block-scaled GEMM over bf16 activations, M <= 64, the activation quant done
+ * inside the GEMM kernel.  Replaces op kb_nano_fp8::flashinfer_blockscale_gemm
+ * (tasks/baseline/L1/fp8_linear.py:126-153), the bf16-input GEMM that
+ * Fp8Linear.forward takes for M < 32 (:398-417; FlashInfer's SM90 kernel,
+ * which quantizes its input itself).
+ *   x  bf16 [M, K] row stride ld_x (elements, 16-byte aligned rows)
+ *   W, sW, D as kbn_fp8_gemm_nt; eps as kbn_per_token_group_quant_fp8
+ * Every 1x128 group of x is quantized exactly as kbn_per_token_group_quant_fp8
+ * does with use_ue8m0 = 1 (same codes, same power-of-two scales), and the
+ * product is the UE8M0 contract of kbn_fp8_gemm_nt: D equals that quant
+ * followed by kbn_fp8_gemm_nt_ws bit for bit.  No fp8 copy of x is written.
+ * M > 64 is rejected (code 1).  The workspace is as kbn_fp8_gemm_nt_ws's
+ * (split-K slabs; kbn_fp8_gemm_bf16a_workspace_bytes, 0 if none is needed;
+ * a smaller workspace runs the shape without split).
+ */
+int64_t kbn_fp8_gemm_bf16a_workspace_bytes(int64_t M, int64_t N, int64_t K);
+/* 1 when kbn_fp8_gemm_bf16a is expected to be faster on the current device
+ * than kbn_fp8_linear_forward (quant + GEMM) for this shape, else 0 (also for
+ * shapes kbn_fp8_gemm_bf16a rejects).  Fp8Linear.forward routes by it. */
+int kbn_fp8_gemm_bf16a_preferred(int64_t M, int64_t N, int64_t K);
+int kbn_fp8_gemm_bf16a(const void* x_bf16, int64_t ld_x, float eps, const void* W, int64_t ldw,
+                       const float* sW, int64_t sW_ld, void* D_bf16, int64_t ldd,
+                       int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * kbn_fp8_gemm_nt_ws without any allocation by the caller: the split-K slabs
  * go to a device array the library holds per GPU (`scratch`, of
  * kbn_fp8_gemm_nt_noalloc_scratch_bytes() = 64 MiB, kept until the process

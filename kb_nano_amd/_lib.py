@@ -29,6 +29,9 @@ SIGNATURES = {
         [_P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P], _I),
     "kbn_fp8_linear_forward": ([_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _F, _I, _P, _I64, _P, _I64, _P,
                                 _I64, _I64, _I, _P, _I64, _P], _I),
+    "kbn_fp8_gemm_bf16a_workspace_bytes": ([_I64, _I64, _I64], _I64),
+    "kbn_fp8_gemm_bf16a_preferred": ([_I64, _I64, _I64], _I),
+    "kbn_fp8_gemm_bf16a": ([_P, _I64, _F, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P], _I),
     "kbn_fp8_gemm_nt_noalloc_scratch_bytes": ([], _I64),
     "kbn_fp8_gemm_nt_noalloc": ([_P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _P], _I),
     "kbn_fp8_grouped_gemm_nt_contiguous": (

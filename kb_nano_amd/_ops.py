@@ -234,6 +234,70 @@ def fp8_linear_forward(x: torch.Tensor, q_buf: torch.Tensor, s_buf: torch.Tensor
         check(rc, what)
 
 
+BF16A_MAX_M = 64   # rows the bf16-activation GEMM covers (its 64-row tiles)
+
+
+def fp8_gemm_bf16a(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, output: torch.Tensor,
+                   eps: float = QUANT_EPS) -> None:
+    """``output[M, N] = block-scaled quant(x) x weight^T`` for bf16 ``x [M, K]``
+    with M <= 64, the 1x128 UE8M0 activation quant done inside the GEMM
+    kernel (one launch, no fp8 copy of ``x``).  The codes and scales are the
+    ones ``per_token_group_quant_fp8`` produces, so the output equals that
+    quant followed by ``fp8_gemm_nt`` bit for bit.
+
+    The counterpart of the reference's small-M branch, which hands bf16
+    activations to a GEMM that quantizes them itself
+    (tasks/baseline/L1/fp8_linear.py:126-148 ``flashinfer_blockscale_gemm``,
+    taken at :398-417 for M < 32)."""
+    what = "fp8_gemm_bf16a"
+    idx = x.get_device()
+    if (idx not in _GFX950_DEVICES or idx != _cur_device() or weight.get_device() != idx
+            or weight_scale.get_device() != idx or output.get_device() != idx):
+        _dev_check(what, x, weight, weight_scale, output)
+    if x.dtype is not _BF16 or weight.dtype is not FP8 or weight_scale.dtype is not _F32 or output.dtype is not _BF16:
+        raise TypeError(f"{what}: expected bf16 x, fp8 weight, fp32 weight_scale, bf16 output")
+    if x.dim() != 2 or weight.dim() != 2 or weight_scale.dim() != 2:
+        raise ValueError(f"{what}: x, weight and weight_scale must be 2-D")
+    M, K = x.shape
+    N, K2 = weight.shape
+    KB, NB = -(-K // GROUP), -(-N // GROUP)
+    wssh = weight_scale.shape
+    if K2 != K or K % GROUP or tuple(output.shape) != (M, N) or wssh[0] < NB or wssh[1] < KB:
+        raise ValueError(f"{what}: shapes x {tuple(x.shape)}, W {tuple(weight.shape)}, sW {tuple(wssh)}, "
+                         f"out {tuple(output.shape)}")
+    if M > BF16A_MAX_M:
+        raise ValueError(f"{what}: M={M} > {BF16A_MAX_M}; quantize with per_token_group_quant_fp8 and use fp8_gemm_nt")
+    xs, ws_, wss, os_ = x.stride(), weight.stride(), weight_scale.stride(), output.stride()
+    if xs[1] != 1 or ws_[1] != 1 or os_[1] != 1 or wss[1] != 1:
+        raise ValueError(f"{what}: rows must be contiguous")
+    if M == 0 or N == 0:
+        return
+    L = lib()
+    key = (idx, "bf16a", M, N, K)
+    ws_bytes = _WS_CACHE.get(key)
+    if ws_bytes is None:
+        with torch.cuda.device(idx):
+            ws_bytes = _WS_CACHE[key] = int(L.kbn_fp8_gemm_bf16a_workspace_bytes(M, N, K))
+    st = _raw_stream(idx)
+    ws = _workspace(ws_bytes, idx, st, output.device) if ws_bytes else None
+    rc = L.kbn_fp8_gemm_bf16a(x.data_ptr(), xs[0], float(eps), weight.data_ptr(), ws_[0], weight_scale.data_ptr(),
+                              wss[0], output.data_ptr(), os_[0], M, N, K,
+                              ws.data_ptr() if ws is not None else None, ws_bytes, st)
+    if rc:
+        check(rc, what)
+
+
+def bf16a_preferred(M: int, N: int, K: int, idx: int) -> bool:
+    """Whether ``fp8_gemm_bf16a`` is expected to beat quant + ``fp8_gemm_nt``
+    for this shape on device idx (the library's plan-based rule); cached."""
+    key = (idx, "bf16a?", M, N, K)
+    r = _WS_CACHE.get(key)
+    if r is None:
+        with torch.cuda.device(idx):
+            r = _WS_CACHE[key] = bool(lib().kbn_fp8_gemm_bf16a_preferred(M, N, K))
+    return r
+
+
 _WS_CACHE: dict = {}
 _WS_BUFS: dict = {}
 
@@ -620,6 +684,13 @@ def _register():
                         "Tensor weight, Tensor weight_scale, Tensor! output) -> ()")
         _fp8_lib.impl("fp8_gemm_nt", lambda q, s, w, ws, o: fp8_gemm_nt(q, s, w, ws, o), "CUDA")
         _fp8_lib.impl("fp8_gemm_nt", _meta_noop, "Meta")
+    if not _has_op("kb_nano_fp8", "flashinfer_blockscale_gemm"):
+        # the reference's bf16-input small-M GEMM op (fp8_linear.py:126-153);
+        # here the gfx950 kernel that quantizes its activations itself
+        _fp8_lib.define("flashinfer_blockscale_gemm(Tensor input_bf16, Tensor weight_fp8, "
+                        "Tensor weight_scale, Tensor! output) -> ()")
+        _fp8_lib.impl("flashinfer_blockscale_gemm", lambda x, w, ws, o: fp8_gemm_bf16a(x, w, ws, o), "CUDA")
+        _fp8_lib.impl("flashinfer_blockscale_gemm", _meta_noop, "Meta")
     if not _has_op("kb_nano_fp8", "per_token_group_quant_fp8"):
         _fp8_lib.define("per_token_group_quant_fp8(Tensor input, Tensor! output_fp8, "
                         "Tensor! output_scale, bool column_major_scales=False) -> ()")

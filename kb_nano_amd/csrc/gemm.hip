@@ -30,7 +30,7 @@ namespace kbn {
 // parallel against 20.0 us split in two), and long K takes fewer, longer
 // splits than a traffic-only model picks.
 static void plan_tail(Schedule& s, int64_t M, int KBT) {
-    const int occ = gemm_occupancy(s.bm, s.bn, s.stages);
+    const int occ = gemm_occupancy(s.bm, s.bn, s.stages, s.fuse_a);
     const int cus = cu_count();
     const int64_t slots = (int64_t)occ * cus;
     s.dp_tiles = s.tiles;
@@ -211,6 +211,21 @@ static Schedule dense_schedule(int64_t M, int64_t N, int64_t K, int ue8m0, bool 
     return s;
 }
 
+// Tile plan of the GEMM over bf16 activations (M <= 64, quantized by the
+// kernel): the 64x128 weight-streaming tiles with 256-B A rows per stage,
+// 4 stages (136 KB) when the tiles do not fill the CUs, else 3 (102 KB);
+// one workgroup per CU either way.
+static Schedule bf16a_schedule(int64_t M, int64_t N, int64_t K, bool allow_split) {
+    Schedule s;
+    s.bm = 64; s.bn = 128; s.fuse_a = true;
+    s.tiles = ((M + 63) / 64) * ((N + 127) / 128);
+    s.stages = s.tiles > cu_count() ? 3 : 4;
+    s.dp_tiles = s.tiles;
+    s.kb_per_split = (int)(K / kGroup);
+    if (allow_split) plan_tail(s, M, (int)(K / kGroup));
+    return s;
+}
+
 template <bool kUe8m0>
 static int dispatch_dense(const GemmArgs& a, const Schedule& sc, int64_t K, hipStream_t st, const char* what) {
     if constexpr (kUe8m0) {
@@ -354,6 +369,65 @@ extern "C" int kbn_fp8_linear_forward(const void* x_bf16, int64_t M, int64_t K, 
         return rc;
     return gemm_nt_impl(what, q_fp8, ld_q, scale, s_stride_m, s_stride_g, W, ldw, sW, sW_ld, D_bf16, ldd, M, N, K,
                         scale_ue8m0, workspace, workspace_bytes, stream);
+}
+
+extern "C" int64_t kbn_fp8_gemm_bf16a_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || M > 64 || N <= 0 || K <= 0 || K % kGroup != 0 || N > 0x7FFFFFFFLL) return 0;
+    return bf16a_schedule(M, N, K, true).ws_bytes;
+}
+
+// Whether the bf16-activation GEMM is expected to beat quant + GEMM: its
+// in-kernel quant costs each workgroup about 0.1-0.3 us per K block, the
+// separate quant launch about 3-5 us per call (MI355X, M <= 64), so it is
+// taken when the plan spreads K over split workgroups of at most 16 blocks
+// each and the tiles fit one wave (Llama-70B o, 2048x2048-class shapes);
+// long K per workgroup (qkv 22, down 56 blocks) and more tiles than CUs
+// (gate_up) stay with quant + GEMM.
+extern "C" int kbn_fp8_gemm_bf16a_preferred(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || M > 64 || N <= 0 || K <= 0 || K % kGroup != 0 || N > 0x7FFFFFFFLL) return 0;
+    const Schedule s = bf16a_schedule(M, N, K, true);
+    return (s.tiles <= (int64_t)cu_count() && s.splits > 1 && s.kb_per_split <= 16) ? 1 : 0;
+}
+
+extern "C" int kbn_fp8_gemm_bf16a(const void* x_bf16, int64_t ld_x, float eps, const void* W, int64_t ldw,
+                                  const float* sW, int64_t sW_ld, void* D_bf16, int64_t ldd, int64_t M, int64_t N,
+                                  int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
+    const char* what = "fp8_gemm_bf16a";
+    KBN_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "%s: negative shape", what);
+    KBN_CHECK_ARG(M <= 64, "%s: M=%lld; the bf16-activation GEMM covers M <= 64 (quantize, then fp8_gemm_nt)", what,
+                  (long long)M);
+    KBN_CHECK_ARG(K % kGroup == 0, "%s: K=%lld must be a multiple of 128", what, (long long)K);
+    KBN_CHECK_ARG(N <= 0x7FFFFFFFLL && K <= 0x3FFFFFFFLL, "%s: shape too large", what);
+    if (M == 0 || N == 0) return 0;
+    KBN_CHECK_ARG(K > 0 && x_bf16 && W && sW && D_bf16, "%s: null pointer or empty K", what);
+    KBN_CHECK_ARG(ld_x >= K && ldw >= K && ldd >= N, "%s: leading dimension too small", what);
+    KBN_CHECK_ARG(aligned16(x_bf16) && ld_x % 8 == 0, "%s: activation rows must be 16-byte aligned", what);
+    KBN_CHECK_ARG(aligned16(W) && ldw % 16 == 0, "%s: weight rows must be 16-byte aligned", what);
+    KBN_CHECK_ARG(((reinterpret_cast<uintptr_t>(D_bf16) & 1u) == 0), "%s: D must be 2-byte aligned", what);
+    KBN_CHECK_ARG(ld_x * 2 * 64 + K * 2 < 0x7FFFFFFFLL && ldw * 256 + K < 0x7FFFFFFFLL && ldd * 2 * 256 < 0x7FFFFFFFLL,
+                  "%s: leading dimension too large", what);
+    KBN_CHECK_ARG(sW_ld >= K / kGroup, "%s: weight-scale row stride %lld < K/128", what, (long long)sW_ld);
+    KBN_CHECK_ARG((N + kGroup - 1) / kGroup * sW_ld * 4 < 0x7FFFFFFFLL, "%s: weight scales span >= 2 GiB", what);
+    GemmArgs a{};
+    a.X = (const uint16_t*)x_bf16; a.ldx = ld_x; a.eps = eps;
+    a.W = (const uint8_t*)W; a.ldw = ldw;
+    a.sW = sW; a.sW_ld = sW_ld;
+    a.D = (uint16_t*)D_bf16; a.ldd = ldd;
+    a.vec_store = (reinterpret_cast<uintptr_t>(D_bf16) % 16 == 0) && (ldd % 8 == 0);
+    a.M = (int)M; a.N = (int)N; a.K = (int)K; a.E = 1;
+    Schedule sc = bf16a_schedule(M, N, K, workspace != nullptr);
+    if (sc.splits > 1) {
+        if (workspace_bytes >= sc.ws_bytes) {
+            KBN_CHECK_ARG(aligned16(workspace), "%s: workspace must be 16-byte aligned", what);
+            a.P = (float*)workspace;
+            a.ws_bytes = workspace_bytes;
+        } else {
+            sc = bf16a_schedule(M, N, K, false);
+        }
+    }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (sc.stages == 4) return launch_gemm<64, 128, 4, true, false, 4, true>(a, sc, st, what);
+    return launch_gemm<64, 128, 3, true, false, 4, true>(a, sc, st, what);
 }
 
 extern "C" int64_t kbn_fp8_gemm_nt_noalloc_scratch_bytes(void) { return kScratchBytes; }

@@ -94,6 +94,11 @@ struct GemmArgs {
     int64_t D_bytes;             // bytes at D the scattered stores may write
     const float* row_weight;     // [num_valid] fp32 factors of the output rows, or nullptr
     int sa_sorted;               // sA already holds row R's scales at R (gathered by sorted_scale_gather_kernel)
+    // bf16 activations quantized by the kernel itself (1x128 groups, UE8M0):
+    // X [M, K] with row stride ldx elements, group absmax floor eps.
+    const uint16_t* X;
+    int64_t ldx;
+    float eps;
 };
 
 // Raw buffer descriptor (base, byte range) built from uniform values so it
@@ -305,6 +310,17 @@ __device__ __forceinline__ void splitk_sum_rows(const GemmArgs& a, int trel, int
     }
 }
 
+// LDS bytes of a tile configuration of four wavefronts (an A row of a stage
+// is 128 fp8 bytes, or 256 bf16 bytes when the kernel quantizes bf16
+// activations itself); configurations that fit twice into a CU's 160 KB run
+// two workgroups per CU.
+constexpr int gemm_lds_bytes(int bm, int bn, int stages, bool fuse_a = false) {
+    return stages * (bm * (fuse_a ? 2 * kRowB : kRowB) + bn * kRowB + 2048);
+}
+constexpr int gemm_occupancy(int bm, int bn, int stages, bool fuse_a = false) {
+    return gemm_lds_bytes(bm, bn, stages, fuse_a) <= 80 * 1024 ? 2 : 1;
+}
+
 // Block-scaled GEMM tile kernel: BM x BN output tile, four wavefronts in a
 // 2 x 2 grid, each owning a (BM/2) x (BN/2) block of 32x32 MFMA fragments.
 //
@@ -324,10 +340,25 @@ __device__ __forceinline__ void splitk_sum_rows(const GemmArgs& a, int trel, int
 //               of K half 0 (and the scales) of block kb+1.
 // So kStages-1 blocks are in flight while one is consumed, and no fragment
 // register set is ever copied.
-template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, bool kSplitK, int kWaves, bool kSorted = false>
-__global__ __launch_bounds__(64 * kWaves, (kStages * (BM + BN) * 128 + kStages * 512 * kWaves <= 80 * 1024) ? 2 : 1) void
+//
+// kFuseA: A arrives as bf16 (a.X) and is quantized by the kernel, 1x128
+// groups with UE8M0 scales exactly as the quant kernel does it
+// (quant.hip), so the product equals quant + GEMM bit for bit.  A stage
+// then holds the bf16 A rows (256 B each, 16-B chunk c of row r in slot
+// c ^ (r & 15), conflict-free for 16 consecutive rows); each wavefront reads
+// its fragment rows' 128 values of a block (two lanes per row), takes the
+// group absmax across the lane pair, and converts them to the fp8 fragments
+// of both K halves.
+template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, bool kSplitK, int kWaves, bool kSorted = false,
+          bool kFuseA = false>
+__global__ __launch_bounds__(64 * kWaves, (kStages * (BM * (kFuseA ? 2 : 1) + BN) * 128 + kStages * 512 * kWaves <=
+                                           80 * 1024)
+                                              ? 2
+                                              : 1) void
 gemm_bs_kernel(const GemmArgs a) {
     static_assert(!(kSorted && (kGrouped || kSplitK)), "the sorted-token layout is its own grouped mode");
+    static_assert(!kFuseA || (kUe8m0 && !kGrouped && !kSorted && BM == 64 && kWaves == 4),
+                  "in-kernel activation quant: UE8M0, dense, 64-row tiles of four wavefronts");
     static_assert(kWaves == 4 || kWaves == 8, "2x2 or 2x4 wavefronts");
     constexpr int WM = 2, WN = kWaves / 2;
     constexpr int TM = BM / WM, TN = BN / WN;   // wavefront tile
@@ -335,7 +366,8 @@ gemm_bs_kernel(const GemmArgs a) {
     static_assert(FM >= 1 && FN >= 1 && TM % 32 == 0 && TN % 32 == 0, "fragment tiling");
     static_assert(BM <= 64 * kWaves && BM % (16 * kWaves) == 0 && BN % (16 * kWaves) == 0, "DMA tiling");
     static_assert(128 % TN == 0 || TN % 128 == 0, "wave N tile must not straddle a scale block");
-    constexpr int kA = BM * kRowB, kB = BN * kRowB, kSA = kWaves * 256, kSW = kWaves * 256;
+    constexpr int kArow = kFuseA ? 2 * kRowB : kRowB;   // LDS bytes of one A row of a stage
+    constexpr int kA = BM * kArow, kB = BN * kRowB, kSA = kWaves * 256, kSW = kWaves * 256;
     constexpr int kStage = kA + kB + kSA + kSW;
     static_assert(kStages >= 2 && kStages * kStage <= 160 * 1024, "LDS budget");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStage];
@@ -387,8 +419,9 @@ gemm_bs_kernel(const GemmArgs a) {
         return (t >= 0 && t < a.num_valid) ? t : -1;
     };
 
-    const v4i dA = kSorted ? make_desc(a.A, a.A_bytes)
-                           : make_desc(a.A + (int64_t)m0 * a.lda, (int64_t)(a.M - m0 - 1) * a.lda + a.K);
+    const v4i dA = kFuseA  ? make_desc(a.X + (int64_t)m0 * a.ldx, ((int64_t)(a.M - m0 - 1) * a.ldx + a.K) * 2)
+                   : kSorted ? make_desc(a.A, a.A_bytes)
+                             : make_desc(a.A + (int64_t)m0 * a.lda, (int64_t)(a.M - m0 - 1) * a.lda + a.K);
     const v4i dW = make_desc(Wbase + (int64_t)n0 * a.ldw, (int64_t)(a.N - n0 - 1) * a.ldw + a.K);
     const v4i dSA = make_desc(a.sA, a.sA_bytes);
     const v4i dSW = make_desc(sWbase, (int64_t)NB * a.sW_ld * 4);
@@ -396,8 +429,11 @@ gemm_bs_kernel(const GemmArgs a) {
     // DMA lane mapping: one instruction = 8 rows x 128 B starting at row
     // r0 = 8 q; lane i fills slot i % 8 of row r0 + i / 8 with global chunk
     // (i % 8) ^ swz(r0 + i / 8) = (i % 8) ^ ((i >> 4) | 4 (q & 1)).
-    constexpr int kAInstr = BM / (8 * kWaves), kBInstr = BN / (8 * kWaves);   // 8-row DMAs per wave
+    // fused bf16 A: 4-row DMAs (16 lanes x 16 B per row), 4 per wave
+    constexpr int kAInstr = kFuseA ? BM * 2 * kRowB / (1024 * kWaves) : BM / (8 * kWaves);
+    constexpr int kBInstr = BN / (8 * kWaves);   // 8-row DMAs per wave
     static_assert(kAInstr % 2 == 0 && kBInstr % 2 == 0, "even instruction counts keep q & 1 == i & 1");
+    static_assert(!kFuseA || kAInstr == 4, "fused A: the swizzle below assumes 16 rows per wavefront");
     const int drow = lane >> 3;
     const int ch_e = ((lane & 7) ^ (lane >> 4)) << 4;
     const int ch_o = ((lane & 7) ^ ((lane >> 4) | 4)) << 4;
@@ -405,6 +441,16 @@ gemm_bs_kernel(const GemmArgs a) {
     const int a_o = a_e - ch_e + ch_o;
     const int w_e = (int)((wave * kBInstr * 8 + drow) * a.ldw) + ch_e + kb0 * kRowB;
     const int w_o = w_e - ch_e + ch_o;
+    // fused A: byte offset of this lane's 16-B chunk for instruction i: row
+    // 16 wave + 4 i + lane / 16, slot lane % 16 <- global chunk slot ^ (row & 15)
+    int xa_off[kFuseA ? kAInstr : 1];
+    if constexpr (kFuseA) {
+#pragma unroll
+        for (int i = 0; i < kAInstr; ++i) {
+            const int row = wave * 16 + 4 * i + (lane >> 4);
+            xa_off[i] = row * (int)(a.ldx * 2) + (((lane & 15) ^ (row & 15)) << 4) + kb0 * 2 * kRowB;
+        }
+    }
     // sorted layout: byte offset of each DMA row of this lane's A instructions
     // (gathered rows; padding reads zeros)
     int a_row[kSorted ? kAInstr : 1];
@@ -431,7 +477,8 @@ gemm_bs_kernel(const GemmArgs a) {
     const bool sw_live = (lane < (BN + 127) / 128) & (n0 / 128 + lane < NB);
     const int sw_kstep = sw_live ? 4 : 0;
     const int sw_off0 = sw_live ? (n0 / 128 + lane) * (int)a.sW_ld * 4 + kb0 * 4 : kOob;
-    constexpr int kDma = kAInstr + kBInstr + 2;  // DMA instructions per wave per stage
+    constexpr int kScaleDma = kFuseA ? 1 : 2;    // scale vectors per stage (no A scales when fused)
+    constexpr int kDma = kAInstr + kBInstr + kScaleDma;  // DMA instructions per wave per stage
     // Weight rows stream past L2 (non-temporal) where the weights dominate the
     // traffic: the 128-column dense tiles (chosen only for M <= 128) and the
     // grouped and sorted MoE tiles.  The large dense tiles keep the default,
@@ -445,18 +492,19 @@ gemm_bs_kernel(const GemmArgs a) {
     auto issue_one = [&](int s, bool live, int d) {
         const uint32_t base = lds0 + (s % kStages) * kStage;
         const int k0 = s * kRowB;
-        if (d == 0) {
+        if (!kFuseA && d == 0) {
             dma_b32(dSA, base + kA + kB + wave * 256, live ? sa_off0 + s * sa_kstep : kOob);
-        } else if (d == 1) {
+        } else if (d == kScaleDma - 1) {
             dma_b32(dSW, base + kA + kB + kSA + wave * 256, live ? sw_off0 + s * sw_kstep : kOob);
-        } else if (d < 2 + kAInstr) {
-            const int i = d - 2;
+        } else if (d < kScaleDma + kAInstr) {
+            const int i = d - kScaleDma;
             int off;
-            if constexpr (kSorted) off = a_row[i] + ((i & 1) ? ch_o : ch_e) + k0;
+            if constexpr (kFuseA) off = xa_off[i] + s * 2 * kRowB;
+            else if constexpr (kSorted) off = a_row[i] + ((i & 1) ? ch_o : ch_e) + k0;
             else off = ((i & 1) ? a_o : a_e) + (int)(i * 8 * a.lda) + k0;
             dma_b128(dA, base + (wave * kAInstr + i) * 1024, live ? off : kOob);
         } else {
-            const int i = d - 2 - kAInstr;
+            const int i = d - kScaleDma - kAInstr;
             const uint32_t dst = base + kA + (wave * kBInstr + i) * 1024;
             const int off = live ? ((i & 1) ? w_o : w_e) + (int)(i * 8 * a.ldw) + k0 : kOob;
             if constexpr (kWeightNt) dma_b128_nt(dW, dst, off);
@@ -482,8 +530,10 @@ gemm_bs_kernel(const GemmArgs a) {
     auto read_half = [&](const uint8_t* st, int kk, int q, v8i (&af)[FM], v8i (&bf)[FN]) {
         const int f = q >> 1, h = q & 1;
         const int c = 4 * kk + 2 * (lane >> 5) + h;
-        const uint8_t* tile = f < FM ? st + (wm * TM + f * 32) * kRowB : st + kA + (wn * TN + (f - FM) * 32) * kRowB;
-        const v4i v = *reinterpret_cast<const v4i*>(tile + frow + ((c ^ fs) << 4));
+        const uint8_t* tile = f < FM ? st + (wm * TM + f * 32) * kArow : st + kA + (wn * TN + (f - FM) * 32) * kRowB;
+        // fused A rows: 256-B stride, chunk c of row r in slot c ^ (r & 15) (fragments start at multiples of 16 rows)
+        const int off = (kFuseA && f < FM) ? (lane & 31) * kArow + ((c ^ (lane & 15)) << 4) : frow + ((c ^ fs) << 4);
+        const v4i v = *reinterpret_cast<const v4i*>(tile + off);
         if (f < FM) {
             if (h) af[f].hi = v; else af[f].lo = v;
         } else {
@@ -585,12 +635,85 @@ gemm_bs_kernel(const GemmArgs a) {
     constexpr int kT = FM * FN;           // MFMAs per sub-step
     constexpr int kR = 2 * (FM + FN);     // 16-B fragment reads per sub-step
 
+    // Fused A: this wavefront's 16 rows of a block (the rows its own DMAs
+    // brought in: 16 wave + i) quantized in place, four lanes per row and
+    // 32 values per lane: the group absmax (packed 16-bit max of the
+    // sign-cleared words, then over the lane quad), the UE8M0 scale and the
+    // codes exactly as the quant kernel derives them (its general path for a
+    // group with an infinity, a NaN or a subnormal scale); the 128 code bytes
+    // of row r take chunk slots c ^ (r & 15) of the row's 256 bytes, the
+    // scale goes to the stage's activation-scale slot.  Every lane's loads
+    // complete before the first write (the quad max consumes them all), and
+    // no other wavefront reads these rows before the next barrier.
+    auto quant_rows = [&](const uint8_t* st_c) {
+        if constexpr (kFuseA) {
+            typedef uint16_t u16v2 __attribute__((ext_vector_type(2)));
+            uint8_t* st = const_cast<uint8_t*>(st_c);
+            const int r = wave * 16 + (lane >> 2), j = lane & 3, sr = r & 15;
+            uint8_t* row = st + r * kArow;
+            u32x4 v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = *reinterpret_cast<const u32x4*>(row + (((4 * j + q) ^ sr) << 4));
+            u16v2 m{0, 0};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                m = __builtin_elementwise_max(m, __builtin_bit_cast(u16v2, v[q].x & 0x7FFF7FFFu));
+                m = __builtin_elementwise_max(m, __builtin_bit_cast(u16v2, v[q].y & 0x7FFF7FFFu));
+                m = __builtin_elementwise_max(m, __builtin_bit_cast(u16v2, v[q].z & 0x7FFF7FFFu));
+                m = __builtin_elementwise_max(m, __builtin_bit_cast(u16v2, v[q].w & 0x7FFF7FFFu));
+            }
+            auto quad_max = [](uint32_t x) {
+                uint32_t t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false);  // [1,0,3,2]
+                x = x > t ? x : t;
+                t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false);           // [2,3,0,1]
+                return x > t ? x : t;
+            };
+            const uint32_t abits = quad_max((uint32_t)(m.x > m.y ? m.x : m.y) << 16);
+            float sc = ue8m0_ceil_div448(fmaxf(__uint_as_float(abits), a.eps));
+            uint32_t c[8];
+            if (ue8m0_fast_path(abits, sc)) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    c[2 * q] = pack4_e4m3_bf16(v[q].x, v[q].y, sc);
+                    c[2 * q + 1] = pack4_e4m3_bf16(v[q].z, v[q].w, sc);
+                }
+            } else {   // uniform over the row's quad
+                float amax = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    amax = fmaxf(amax, fabsf(bf16lo(v[q].x)));
+                    amax = fmaxf(amax, fabsf(bf16hi(v[q].x)));
+                    amax = fmaxf(amax, fabsf(bf16lo(v[q].y)));
+                    amax = fmaxf(amax, fabsf(bf16hi(v[q].y)));
+                    amax = fmaxf(amax, fabsf(bf16lo(v[q].z)));
+                    amax = fmaxf(amax, fabsf(bf16hi(v[q].z)));
+                    amax = fmaxf(amax, fabsf(bf16lo(v[q].w)));
+                    amax = fmaxf(amax, fabsf(bf16hi(v[q].w)));
+                }
+                sc = ue8m0_ceil_div448(fmaxf(__uint_as_float(quad_max(__float_as_uint(amax))), a.eps));
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    c[2 * q] = pack4_e4m3_ue8m0_general(bf16lo(v[q].x), bf16hi(v[q].x), bf16lo(v[q].y),
+                                                        bf16hi(v[q].y), sc);
+                    c[2 * q + 1] = pack4_e4m3_ue8m0_general(bf16lo(v[q].z), bf16hi(v[q].z), bf16lo(v[q].w),
+                                                            bf16hi(v[q].w), sc);
+                }
+            }
+            *reinterpret_cast<u32x4*>(row + (((2 * j) ^ sr) << 4)) = u32x4{c[0], c[1], c[2], c[3]};
+            *reinterpret_cast<u32x4*>(row + (((2 * j + 1) ^ sr) << 4)) = u32x4{c[4], c[5], c[6], c[7]};
+            if (j == 0) reinterpret_cast<float*>(st + kA + kB)[r] = sc;
+        } else {
+            (void)st_c;
+        }
+    };
+
     // prologue: blocks 0 .. kStages-1 in flight, block 0 published
 #pragma unroll
     for (int s = 0; s < kStages; ++s)
 #pragma unroll
         for (int d = 0; d < kDma; ++d) issue_one(s, s < KB, d);
     wait_dma_n<(kStages - 1) * kDma>();
+    quant_rows(stage_ptr(0));   // fused A: block 0 (the loop quantizes block kb+1 in iteration kb)
     __syncthreads();
     read_scales(stage_ptr(0), sa, sw);
 #pragma unroll
@@ -608,6 +731,15 @@ gemm_bs_kernel(const GemmArgs a) {
 #pragma unroll
             for (int q = t * kR / kT; q < (t + 1) * kR / kT; ++q) read_half(cur, 1, q, fa1, fb1);
             __builtin_amdgcn_sched_barrier(0);
+        }
+
+        // fused A: block kb+1's rows of this wavefront, quantized in place as
+        // soon as they have landed (its own DMAs: the activation rows come
+        // from L2 ahead of the block's weights, which may still stream in);
+        // the hand-off below publishes the codes with the weights
+        if constexpr (kFuseA) {
+            wait_dma_n<(kStages - 2) * kDma + kBInstr>();
+            quant_rows(stage_ptr(kb + 1));
         }
 
         // ---- hand-off: publish block kb+1, free buffer kb for block kb+kStages
@@ -834,10 +966,6 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a) {
                                                         ((int)threadIdx.x % kRuns) * 4);
 }
 
-// LDS bytes of a tile configuration; configurations that fit twice into a
-// CU's 160 KB run two workgroups per CU.
-constexpr int gemm_lds_bytes(int bm, int bn, int stages) { return stages * (bm * kRowB + bn * kRowB + 2048); }
-constexpr int gemm_occupancy(int bm, int bn, int stages) { return gemm_lds_bytes(bm, bn, stages) <= 80 * 1024 ? 2 : 1; }
 
 // Launch plan of a dense GEMM.  Whole waves of tiles run data-parallel in
 // one launch; when the last wave would be partly empty, its tiles (the
@@ -850,6 +978,7 @@ struct Schedule {
     int splits = 1, kb_per_split = 0;  // the tail [dp_tiles, tiles)
     int64_t ws_bytes = 0;         // fp32 slabs of the tail
     bool fused = false;           // the split launch sums the slabs itself
+    bool fuse_a = false;          // bf16 activations quantized by the GEMM (LDS A rows of 256 B)
 };
 
 // Split-K tails of the 64-row tiles summed by the split launch itself (no
@@ -873,7 +1002,7 @@ unsigned* splitk_flags_for(hipStream_t st, int64_t tail_tiles);
 // accumulators per lane need the AGPRs.
 int launch_gemm_256(const GemmArgs& a, const Schedule& sc, int64_t K, hipStream_t st, const char* what);
 
-template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, int kWaves = 4>
+template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, int kWaves = 4, bool kFuseA = false>
 static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const char* what) {
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
@@ -887,14 +1016,14 @@ static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const cha
         a.kb_per_split = a.K / kRowB;
         const int64_t grid = kGrouped ? moe_dealt_grid(a.tiles_m, a.tiles_n) : dp;
         KBN_CHECK_ARG(grid <= 0x7FFFFFFFLL, "%s: too many tiles", what);
-        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped, false, kWaves>
+        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped, false, kWaves, false, kFuseA>
             <<<dim3((unsigned)grid), dim3(64 * kWaves), 0, st>>>(a);
         KBN_CHECK_LAUNCH(what);
     }
     if (dp < tiles) {
         // the plan must be for this tile shape, and its slabs must fit the workspace
-        KBN_CHECK_ARG(sc.bm == BM && sc.bn == BN && sc.tiles == tiles, "%s: split plan does not match the %dx%d tiles",
-                      what, BM, BN);
+        KBN_CHECK_ARG(sc.bm == BM && sc.bn == BN && sc.tiles == tiles && sc.fuse_a == kFuseA,
+                      "%s: split plan does not match the %dx%d tiles", what, BM, BN);
         const int64_t need = (int64_t)sc.splits * (tiles - dp) * BM * BN * 4;
         KBN_CHECK_ARG(need < 0x7FFFFFFFLL, "%s: split slabs span >= 2 GiB", what);
         KBN_CHECK_ARG(sc.splits >= 2 && sc.kb_per_split >= 1 && need <= a.ws_bytes,
@@ -913,7 +1042,7 @@ static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const cha
         // less).  More rows: that sum would run on one workgroup per tile at
         // the end of the launch, so the separate kernel spreads it instead.
         a.flags = (BM <= 64 && sc.fused) ? splitk_flags_for(st, tiles - dp) : nullptr;
-        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped && false, true, kWaves>
+        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped && false, true, kWaves, false, kFuseA>
             <<<dim3((unsigned)blocks), dim3(64 * kWaves), 0, st>>>(a);
         KBN_CHECK_LAUNCH(what);
         if (!a.flags) {

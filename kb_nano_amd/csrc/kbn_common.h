@@ -135,4 +135,43 @@ __device__ __forceinline__ uint32_t pack4_e4m3_scaled(float a, float b, float c,
     return __builtin_bit_cast(uint32_t, r);
 }
 
+// Four e4m3 codes of the bf16 pairs w0, w1 divided by the power of two sc,
+// by the gfx950 scaled conversion v_cvt_scalef32_pk_fp8_bf16: for every
+// finite bf16 input and every normal power-of-two sc it gives the codes of
+// v_cvt_pk_fp8_f32(x * (1/sc)) (round to nearest even; checked exhaustively
+// on the device), so no widening to fp32 and no multiply are needed.
+__device__ __forceinline__ uint32_t pack4_e4m3_bf16(uint32_t w0, uint32_t w1, float sc) {
+    typedef short s16x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    s16x2 r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(s16x2{0, 0}, __builtin_bit_cast(bf16x2, w0), sc, false);
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r, __builtin_bit_cast(bf16x2, w1), sc, true);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// UE8M0 quantization of a 1x128 group, shared by the quant kernels and the
+// GEMM that quantizes its bf16 activations itself, so both produce the same
+// codes and scales:
+//  * abits: the group's largest bf16 magnitude as fp32 bits (NaN patterns
+//    above infinity's); sc = ue8m0_ceil_div448(max(that, eps));
+//  * fast path (finite absmax, normal sc): codes by the scaled conversion;
+//  * otherwise the general path: the absmax recomputed ignoring NaN (as the
+//    reference's max does), and the codes below.
+__device__ __forceinline__ bool ue8m0_fast_path(uint32_t abits, float sc) {
+    return abits < 0x7F800000u && (__float_as_uint(sc) >> 23) - 1u < 254u;
+}
+// General-path codes of four values under a UE8M0 scale: an infinite scale
+// (a group holding an infinity) maps finite values to +-0 (codes 0x00 /
+// 0x80, x / inf) and the rest to the NaN code; otherwise x times the exact
+// reciprocal of the power of two, by the hardware conversion.
+__device__ __forceinline__ uint32_t pack4_e4m3_ue8m0_general(float a, float b, float c, float d, float sc) {
+    if (sc == __builtin_inff()) {
+        auto code = [](float v) -> uint32_t {
+            return (fabsf(v) < __builtin_inff()) ? (__float_as_uint(v) >> 24 & 0x80u) : 0xFFu;
+        };
+        return code(a) | code(b) << 8 | code(c) << 16 | code(d) << 24;
+    }
+    const float inv = pow2_recip(sc);
+    return pack4_e4m3(a * inv, b * inv, c * inv, d * inv);
+}
+
 }  // namespace kbn

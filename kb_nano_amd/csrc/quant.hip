@@ -115,17 +115,6 @@ __device__ __forceinline__ uint32_t absmax8_bits(const uint32_t (&w)[4]) {
     return (lo > hi ? lo : hi) << 16;
 }
 
-// Four e4m3 codes of the bf16 pairs w0, w1 divided by the power of two sc,
-// by the gfx950 scaled conversion v_cvt_scalef32_pk_fp8_bf16: for every
-// finite bf16 input and every normal power-of-two sc it gives the codes of
-// v_cvt_pk_fp8_f32(x * (1/sc)) (round to nearest even; checked exhaustively
-// on the device), so no widening to fp32 and no multiply are needed.
-__device__ __forceinline__ uint32_t pack4_e4m3_bf16(uint32_t w0, uint32_t w1, float sc) {
-    s16x2 r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(s16x2{0, 0}, __builtin_bit_cast(bf16x2, w0), sc, false);
-    r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r, __builtin_bit_cast(bf16x2, w1), sc, true);
-    return __builtin_bit_cast(uint32_t, r);
-}
-
 // Quantize the 8 bf16 values owned by this lane (four packed words; 16
 // lanes per group); returns the group scale (valid in every lane of the
 // group).
@@ -146,7 +135,7 @@ __device__ __forceinline__ float quant8_store(const uint32_t (&w)[4], float eps,
         const uint32_t abits = row16_max_u32(absmax8_bits(w));
         const float sc = ue8m0_ceil_div448(fmaxf(__uint_as_float(abits), eps));
         // finite absmax and a normal scale (a subnormal one needs eps < 2^-118)
-        if (abits < 0x7F800000u && (__float_as_uint(sc) >> 23) - 1u < 254u) {
+        if (ue8m0_fast_path(abits, sc)) {
             const u32x2 o{pack4_e4m3_bf16(w[0], w[1], sc), pack4_e4m3_bf16(w[2], w[3], sc)};
             if constexpr (kNtStore) __builtin_nontemporal_store(o, reinterpret_cast<u32x2*>(qptr + sub * 8));
             else *reinterpret_cast<u32x2*>(qptr + sub * 8) = o;
@@ -178,18 +167,8 @@ __device__ __forceinline__ float quant8_store(const uint32_t (&w)[4], float eps,
     if (kUe8m0) {
         // an infinite absmax gives an infinite scale: x / inf is +-0 for
         // finite x (code 0x00 / 0x80) and NaN otherwise, as in the reference
-        if (sc == __builtin_inff()) {
-            uint32_t c[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                c[i] = (fabsf(v[i]) < __builtin_inff()) ? (__float_as_uint(v[i]) >> 24 & 0x80u) : 0xFFu;
-            lo = c[0] | c[1] << 8 | c[2] << 16 | c[3] << 24;
-            hi = c[4] | c[5] << 8 | c[6] << 16 | c[7] << 24;
-        } else {
-            const float inv = pow2_recip(sc);
-            lo = pack4_e4m3(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
-            hi = pack4_e4m3(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
-        }
+        lo = pack4_e4m3_ue8m0_general(v[0], v[1], v[2], v[3], sc);
+        hi = pack4_e4m3_ue8m0_general(v[4], v[5], v[6], v[7], sc);
     } else {
         lo = pack4_e4m3(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
         hi = pack4_e4m3(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);

@@ -11,11 +11,15 @@ Reference interface mirrored here:
   * ``Fp8Linear`` (``BLOCK_SIZE``, ``_FLASHINFER_M_THRESHOLD``,
     ``_a_buf/_s_buf/_o_buf/_pf``, ``_ensure_buffers``, ``forward``)   (:335-450)
   * ``postprocess_fp8_weights[_batched]``                            (:453-554)
-  * ops ``torch.ops.kb_nano_fp8.{fp8_gemm_nt, per_token_group_quant_fp8}`` (:89-178)
+  * ops ``torch.ops.kb_nano_fp8.{fp8_gemm_nt, per_token_group_quant_fp8,
+    flashinfer_blockscale_gemm}`` (:89-178)
 
-The reference sends M < 32 to FlashInfer's Hopper-only swapAB kernel
-(:398-417); on gfx950 that branch does not exist and small M is handled
-inside ``fp8_gemm_nt`` by the GEMM's own small-M tile configuration.
+The reference sends M < 32 to FlashInfer's Hopper-only swapAB kernel, which
+takes bf16 activations and quantizes them itself (:398-417).  Its gfx950
+counterpart is ``_ops.fp8_gemm_bf16a`` (op ``flashinfer_blockscale_gemm``):
+the block-scaled GEMM quantizes its activations in-kernel, bit-identical to
+the quant launch followed by ``fp8_gemm_nt``.  ``Fp8Linear`` takes it for
+M <= 64 where the library's plan says one launch beats two.
 """
 from __future__ import annotations
 
@@ -78,8 +82,9 @@ class _Fp8PrefillBufs:
 
 
 def _maybe_get_flashinfer_fp8_gemm():
-    """The reference's Hopper-only small-M kernel (:55-82); never present on
-    gfx950, where ``fp8_gemm_nt`` covers every M."""
+    """The reference's Hopper-only small-M kernel (:55-82); FlashInfer is
+    never present on gfx950.  Its role, a bf16-input GEMM for small M, is
+    ``_ops.fp8_gemm_bf16a``, which ``Fp8Linear.forward`` selects itself."""
     return None
 
 
@@ -88,9 +93,11 @@ class Fp8Linear(nn.Module):
     scales [ceil(N/128), ceil(K/128)], bf16 output [..., N].
 
     ``forward`` quantizes the input 1x128 with UE8M0 scales into column-major
-    scale storage and runs the block-scaled GEMM; with buffers installed the
-    result is a view into the reused output buffer, exactly as the reference
-    returns ``_o_buf[:M]`` / ``_pf.o[:M]``."""
+    scale storage and runs the block-scaled GEMM, or, for M <= 64 where it is
+    faster, runs the GEMM that quantizes its bf16 input itself (the same
+    output bits; the fp8 buffers are then not written); with buffers
+    installed the result is a view into the reused output buffer, exactly as
+    the reference returns ``_o_buf[:M]`` / ``_pf.o[:M]``."""
 
     BLOCK_SIZE = GROUP
     _FLASHINFER_M_THRESHOLD = 32
@@ -123,6 +130,19 @@ class Fp8Linear(nn.Module):
             output = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
             torch.ops.kb_nano_fp8.per_token_group_quant_fp8(x2, q_input, input_scale, True)
             torch.ops.kb_nano_fp8.fp8_gemm_nt(q_input, input_scale, weight_fp8, weight_scale_inv, output)
+        elif M <= _ops.BF16A_MAX_M and is_e8m0_used() and _ops.bf16a_preferred(M, N, K, dev.index):
+            # small M (the reference's bf16-input branch, :398-417): one
+            # launch of the GEMM that quantizes its bf16 activations itself,
+            # the same codes and scales as the quant launch would write, where
+            # the library's plan says it is the faster of the two
+            if self._o_buf is not None and M <= self._o_buf.shape[0]:
+                o_buf = self._o_buf
+            elif self._pf is not None and M <= self._pf.o.shape[0]:
+                o_buf = self._pf.o
+            else:
+                o_buf = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+            output = o_buf if o_buf.shape[0] == M else o_buf[:M]
+            _ops.fp8_gemm_bf16a(x2, weight_fp8, weight_scale_inv, output)
         else:
             # eager: both launches through one library call; the installed
             # decode / prefill buffers (scales included: any row stride works)

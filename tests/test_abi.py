@@ -121,6 +121,48 @@ def test_gemm_ws_rejects_bad_shapes():
     assert "multiple of 128" in _err()
 
 
+def test_bf16a_gemm_rejects_bad_shapes_and_plans_like_the_dense_gemm():
+    """The bf16-activation GEMM covers M <= 64 and K in whole 128-blocks;
+    its split plan is the 64x128 tiles' (one fp32 slab per split and tail
+    tile), asked for only where the dense GEMM's plan splits too."""
+    from kb_nano_amd._lib import lib
+    L = lib()
+    p = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    assert L.kbn_fp8_gemm_bf16a(p, 256, 1e-10, p, 256, p, 2, p, 128, 65, 128, 256, None, 0, None) == 1
+    assert "M <= 64" in _err()
+    assert L.kbn_fp8_gemm_bf16a(p, 256, 1e-10, p, 256, p, 2, p, 128, 8, 128, 200, None, 0, None) == 1
+    assert "multiple of 128" in _err()
+    assert L.kbn_fp8_gemm_bf16a(ctypes.c_void_p(8), 256, 1e-10, p, 256, p, 2, p, 128, 8, 128, 256, None, 0,
+                                None) == 1
+    assert "aligned" in _err()
+    assert L.kbn_fp8_gemm_bf16a(None, 256, 1e-10, None, 256, None, 2, None, 128, 0, 128, 256, None, 0, None) == 0
+    assert L.kbn_fp8_gemm_bf16a_workspace_bytes(65, 8192, 8192) == 0
+    assert L.kbn_fp8_gemm_bf16a_workspace_bytes(8, 8192, 100) == 0
+    assert L.kbn_fp8_gemm_bf16a_workspace_bytes(8, 12288, 1536) == 0      # 12 K blocks stay data-parallel
+    for M, N, K in ((1, 10240, 8192), (64, 8192, 28672), (8, 8192, 8192)):
+        n = L.kbn_fp8_gemm_bf16a_workspace_bytes(M, N, K)
+        assert n > 0 and n % (64 * 128 * 4) == 0, (M, N, K, n)
+
+
+def test_bf16a_routing_rule():
+    """Fp8Linear takes the bf16-activation GEMM where its plan splits K into
+    workgroups of at most 16 blocks within one wave of tiles (measured faster
+    than quant + GEMM on MI355X: cfg1, Llama-70B o at every M), and stays
+    with quant + GEMM for long K per workgroup (qkv, down), more tiles than
+    CUs (gate_up), unsplit plans and M > 64."""
+    from kb_nano_amd._lib import lib
+    L = lib()
+    if torch.cuda.device_count() > 0 and torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the plan depends on the device's CU count; pinned for 256 CUs")
+    yes = [(64, 2048, 2048), (1, 2048, 2048), (1, 8192, 8192), (64, 8192, 8192), (32, 7168, 2048)]
+    no = [(1, 10240, 8192), (32, 10240, 8192), (1, 8192, 28672), (1, 57344, 8192), (64, 7168, 2048),
+          (65, 2048, 2048), (8, 2048, 200)]
+    for M, N, K in yes:
+        assert L.kbn_fp8_gemm_bf16a_preferred(M, N, K) == 1, (M, N, K)
+    for M, N, K in no:
+        assert L.kbn_fp8_gemm_bf16a_preferred(M, N, K) == 0, (M, N, K)
+
+
 def test_grouped_rejects_unaligned_m_sum():
     from kb_nano_amd._lib import lib
     p = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
@@ -148,6 +190,9 @@ def test_ops_registered_with_reference_schemas():
     s = str(torch.ops.kb_nano_fp8.fp8_gemm_nt.default._schema)
     assert "fp8_gemm_nt(Tensor q_input, Tensor input_scale, Tensor weight, Tensor weight_scale, Tensor(" in s
     assert "!" in s.split("weight_scale,")[1]  # output is declared mutated
+    s = str(torch.ops.kb_nano_fp8.flashinfer_blockscale_gemm.default._schema)
+    assert "flashinfer_blockscale_gemm(Tensor input_bf16, Tensor weight_fp8, Tensor weight_scale, Tensor(" in s
+    assert "!" in s.split("weight_scale,")[1]
     s = str(torch.ops.kb_nano_fp8.per_token_group_quant_fp8.default._schema)
     assert "bool column_major_scales=False" in s
     s = str(torch.ops.kb_nano_fp8_moe.m_grouped_gemm_nt_contiguous.default._schema)
