@@ -34,6 +34,7 @@ QUANT_EPS = 1e-10  # tasks/baseline/L1/fp8_linear.py:44
 # device/stream objects cost about 2 us.
 _raw_stream = torch._C._cuda_getCurrentRawStream
 _cur_device = torch._C._cuda_getDevice
+_capturing = torch._C._cuda_isCurrentStreamCapturing
 _GFX950_DEVICES: set = set()
 _BF16 = torch.bfloat16
 _F32 = torch.float32
@@ -182,7 +183,7 @@ def fp8_gemm_nt(q_input: torch.Tensor, input_scale: torch.Tensor, weight: torch.
     # concurrent streams never share one
     ws_bytes = _gemm_workspace_bytes(L, idx, M, N, K, ue8m0)
     st = _raw_stream(idx)
-    ws = _workspace(ws_bytes, idx, st, output.device) if ws_bytes else None
+    ws = _workspace(ws_bytes, idx, st, output) if ws_bytes else None
     rc = L.kbn_fp8_gemm_nt_ws(
         q_input.data_ptr(), qs[0], input_scale.data_ptr(), ss[0], ss[1], weight.data_ptr(), ws_[0],
         weight_scale.data_ptr(), sws_[0], output.data_ptr(), os_[0], M, N, K, 1 if ue8m0 else 0,
@@ -225,7 +226,7 @@ def fp8_linear_forward(x: torch.Tensor, q_buf: torch.Tensor, s_buf: torch.Tensor
     L = lib()
     ws_bytes = _gemm_workspace_bytes(L, idx, M, N, K, ue8m0)
     st = _raw_stream(idx)
-    ws = _workspace(ws_bytes, idx, st, out_buf.device) if ws_bytes else None
+    ws = _workspace(ws_bytes, idx, st, out_buf) if ws_bytes else None
     rc = L.kbn_fp8_linear_forward(
         x.data_ptr(), M, K, xs[0], q_buf.data_ptr(), qs[0], s_buf.data_ptr(), ss[0], ss[1], QUANT_EPS, 1,
         weight.data_ptr(), ws_[0], weight_scale.data_ptr(), wss[0], out_buf.data_ptr(), os_[0], N,
@@ -256,15 +257,14 @@ def fp8_gemm_bf16a(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Te
         _dev_check(what, x, weight, weight_scale, output)
     if x.dtype is not _BF16 or weight.dtype is not FP8 or weight_scale.dtype is not _F32 or output.dtype is not _BF16:
         raise TypeError(f"{what}: expected bf16 x, fp8 weight, fp32 weight_scale, bf16 output")
-    if x.dim() != 2 or weight.dim() != 2 or weight_scale.dim() != 2:
-        raise ValueError(f"{what}: x, weight and weight_scale must be 2-D")
-    M, K = x.shape
-    N, K2 = weight.shape
-    KB, NB = -(-K // GROUP), -(-N // GROUP)
-    wssh = weight_scale.shape
-    if K2 != K or K % GROUP or tuple(output.shape) != (M, N) or wssh[0] < NB or wssh[1] < KB:
-        raise ValueError(f"{what}: shapes x {tuple(x.shape)}, W {tuple(weight.shape)}, sW {tuple(wssh)}, "
-                         f"out {tuple(output.shape)}")
+    xsh, wsh, wssh, osh = x.shape, weight.shape, weight_scale.shape, output.shape
+    if len(xsh) != 2 or len(wsh) != 2 or len(wssh) != 2 or len(osh) != 2:
+        raise ValueError(f"{what}: x, weight, weight_scale and output must be 2-D")
+    M, K = xsh
+    N = wsh[0]
+    if (wsh[1] != K or K % GROUP or osh[0] != M or osh[1] != N or wssh[0] * GROUP < N
+            or wssh[1] * GROUP < K):
+        raise ValueError(f"{what}: shapes x {tuple(xsh)}, W {tuple(wsh)}, sW {tuple(wssh)}, out {tuple(osh)}")
     if M > BF16A_MAX_M:
         raise ValueError(f"{what}: M={M} > {BF16A_MAX_M}; quantize with per_token_group_quant_fp8 and use fp8_gemm_nt")
     xs, ws_, wss, os_ = x.stride(), weight.stride(), weight_scale.stride(), output.stride()
@@ -279,7 +279,7 @@ def fp8_gemm_bf16a(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Te
         with torch.cuda.device(idx):
             ws_bytes = _WS_CACHE[key] = int(L.kbn_fp8_gemm_bf16a_workspace_bytes(M, N, K))
     st = _raw_stream(idx)
-    ws = _workspace(ws_bytes, idx, st, output.device) if ws_bytes else None
+    ws = _workspace(ws_bytes, idx, st, output) if ws_bytes else None
     rc = L.kbn_fp8_gemm_bf16a(x.data_ptr(), xs[0], float(eps), weight.data_ptr(), ws_[0], weight_scale.data_ptr(),
                               wss[0], output.data_ptr(), os_[0], M, N, K,
                               ws.data_ptr() if ws is not None else None, ws_bytes, st)
@@ -302,20 +302,21 @@ _WS_CACHE: dict = {}
 _WS_BUFS: dict = {}
 
 
-def _workspace(nbytes: int, idx: int, stream: int, device) -> torch.Tensor:
+def _workspace(nbytes: int, idx: int, stream: int, like: torch.Tensor) -> torch.Tensor:
     """Scratch for one launch on ``stream``.  Eager launches on a stream reuse
     one buffer per (device, stream), grown as needed: launches on a stream
     run in order, so a buffer is free again when the next launch on that
     stream reads it, and a replaced buffer goes back to the caching allocator,
     which hands it out again only in that stream's order.  Under graph capture
     every launch takes its own buffer from the capture's memory pool, as
-    before (a graph keeps what it was captured with)."""
-    if torch.cuda.is_current_stream_capturing():
-        return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    before (a graph keeps what it was captured with).  ``like`` is a tensor
+    on the device (its device object is only built when allocating)."""
+    if _capturing():
+        return torch.empty(nbytes, dtype=torch.uint8, device=like.device)
     key = (idx, stream)
     buf = _WS_BUFS.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=like.device)
         _WS_BUFS[key] = buf
     return buf
 

@@ -118,19 +118,20 @@ class Fp8Linear(nn.Module):
     def forward(self, input_bf16: torch.Tensor, weight_fp8: torch.Tensor,
                 weight_scale_inv: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
         N, K = weight_fp8.shape
-        x2 = input_bf16.reshape(-1, K)
+        in_shape = input_bf16.shape
+        flat = len(in_shape) == 2 and in_shape[1] == K
+        x2 = input_bf16 if flat else input_bf16.reshape(-1, K)
         M = x2.shape[0]
         G = (K + self.BLOCK_SIZE - 1) // self.BLOCK_SIZE
-        dev = x2.device
 
         if torch.compiler.is_compiling():
             # opaque ops for the compiler (the reference's op boundary)
-            q_input = torch.empty(M, K, dtype=FP8, device=dev)
-            input_scale = _alloc_colmajor_scale(M, G, dev)
-            output = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+            q_input = torch.empty(M, K, dtype=FP8, device=x2.device)
+            input_scale = _alloc_colmajor_scale(M, G, x2.device)
+            output = torch.empty(M, N, dtype=torch.bfloat16, device=x2.device)
             torch.ops.kb_nano_fp8.per_token_group_quant_fp8(x2, q_input, input_scale, True)
             torch.ops.kb_nano_fp8.fp8_gemm_nt(q_input, input_scale, weight_fp8, weight_scale_inv, output)
-        elif M <= _ops.BF16A_MAX_M and is_e8m0_used() and _ops.bf16a_preferred(M, N, K, dev.index):
+        elif M <= _ops.BF16A_MAX_M and is_e8m0_used() and _ops.bf16a_preferred(M, N, K, x2.get_device()):
             # small M (the reference's bf16-input branch, :398-417): one
             # launch of the GEMM that quantizes its bf16 activations itself,
             # the same codes and scales as the quant launch would write, where
@@ -140,7 +141,7 @@ class Fp8Linear(nn.Module):
             elif self._pf is not None and M <= self._pf.o.shape[0]:
                 o_buf = self._pf.o
             else:
-                o_buf = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+                o_buf = torch.empty(M, N, dtype=torch.bfloat16, device=x2.device)
             output = o_buf if o_buf.shape[0] == M else o_buf[:M]
             _ops.fp8_gemm_bf16a(x2, weight_fp8, weight_scale_inv, output)
         else:
@@ -152,15 +153,15 @@ class Fp8Linear(nn.Module):
             elif self._pf is not None and M <= self._pf.a.shape[0]:
                 q_buf, s_buf, o_buf = self._pf.a, self._pf.s, self._pf.o
             else:
-                q_buf = torch.empty(M, K, dtype=FP8, device=dev)
-                s_buf = _alloc_colmajor_scale(M, G, dev)
-                o_buf = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+                q_buf = torch.empty(M, K, dtype=FP8, device=x2.device)
+                s_buf = _alloc_colmajor_scale(M, G, x2.device)
+                o_buf = torch.empty(M, N, dtype=torch.bfloat16, device=x2.device)
             _ops.fp8_linear_forward(x2, q_buf, s_buf, weight_fp8, weight_scale_inv, o_buf)
             output = o_buf if o_buf.shape[0] == M else o_buf[:M]
 
         if bias is not None:
             output = output + bias
-        return output.view(*input_bf16.shape[:-1], N)
+        return output if flat else output.view(*in_shape[:-1], N)
 
 
 # ---------------------------------------------------------------------------
