@@ -212,12 +212,12 @@ static Schedule dense_schedule(int64_t M, int64_t N, int64_t K, int ue8m0, bool 
 }
 
 // Tile plan of the GEMM over bf16 activations (M <= 64, quantized by the
-// kernel): the 64x128 weight-streaming tiles with 256-B A rows per stage,
-// 4 stages (136 KB) when the tiles do not fill the CUs, else 3 (102 KB);
-// one workgroup per CU either way.
+// kernel): the 64x128 weight-streaming tiles with 16, 32 or 64 bf16 A rows
+// of 256 B per stage (as M needs), 4 stages when the tiles do not fill the
+// CUs, else 3 (two workgroups per CU up to 32 rows: 66 / 78 KB).
 static Schedule bf16a_schedule(int64_t M, int64_t N, int64_t K, bool allow_split) {
     Schedule s;
-    s.bm = 64; s.bn = 128; s.fuse_a = true;
+    s.bm = 64; s.bn = 128; s.fuse_a = M <= 16 ? 1 : M <= 32 ? 2 : 4;
     s.tiles = ((M + 63) / 64) * ((N + 127) / 128);
     s.stages = s.tiles > cu_count() ? 3 : 4;
     s.dp_tiles = s.tiles;
@@ -376,15 +376,19 @@ extern "C" int64_t kbn_fp8_gemm_bf16a_workspace_bytes(int64_t M, int64_t N, int6
     return bf16a_schedule(M, N, K, true).ws_bytes;
 }
 
-// Whether the bf16-activation GEMM is expected to beat quant + GEMM: its
-// in-kernel quant costs each workgroup about 0.1-0.3 us per K block, the
-// separate quant launch about 3-5 us per call (MI355X, M <= 64), so it is
-// taken when the plan spreads K over split workgroups of at most 16 blocks
-// each and the tiles fit one wave (Llama-70B o, 2048x2048-class shapes);
-// long K per workgroup (qkv 22, down 56 blocks) and more tiles than CUs
-// (gate_up) stay with quant + GEMM.
+// Whether the bf16-activation GEMM is expected to beat quant + GEMM (the
+// separate quant launch costs 3-5 us per call on MI355X).  Up to 32 rows the
+// in-kernel quant of the 16 or 32 loaded rows costs each workgroup well under
+// that (measured on every Llama-70B decode shape and 2048/7168 x 2048: 0.5-4.7
+// us faster, gate_up at 32 rows even).  With 64 rows (16 per wavefront) it
+// costs about 0.1-0.3 us per K block, so it is taken only when the plan
+// splits K into workgroups of at most 16 blocks within one wave of tiles
+// (2048 x 2048, o); long K per workgroup (qkv 22, down 56 blocks), more
+// tiles than CUs (gate_up: its 102 KB stage set drops to one workgroup per
+// CU) and unsplit plans stay with quant + GEMM.
 extern "C" int kbn_fp8_gemm_bf16a_preferred(int64_t M, int64_t N, int64_t K) {
     if (M <= 0 || M > 64 || N <= 0 || K <= 0 || K % kGroup != 0 || N > 0x7FFFFFFFLL) return 0;
+    if (M <= 32) return 1;
     const Schedule s = bf16a_schedule(M, N, K, true);
     return (s.tiles <= (int64_t)cu_count() && s.splits > 1 && s.kb_per_split <= 16) ? 1 : 0;
 }
@@ -426,8 +430,17 @@ extern "C" int kbn_fp8_gemm_bf16a(const void* x_bf16, int64_t ld_x, float eps, c
         }
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (sc.stages == 4) return launch_gemm<64, 128, 4, true, false, 4, true>(a, sc, st, what);
-    return launch_gemm<64, 128, 3, true, false, 4, true>(a, sc, st, what);
+    // rows of four each wavefront loads and quantizes: just enough for M
+    if (sc.fuse_a == 1) {
+        if (sc.stages == 4) return launch_gemm<64, 128, 4, true, false, 4, 1>(a, sc, st, what);
+        return launch_gemm<64, 128, 3, true, false, 4, 1>(a, sc, st, what);
+    }
+    if (sc.fuse_a == 2) {
+        if (sc.stages == 4) return launch_gemm<64, 128, 4, true, false, 4, 2>(a, sc, st, what);
+        return launch_gemm<64, 128, 3, true, false, 4, 2>(a, sc, st, what);
+    }
+    if (sc.stages == 4) return launch_gemm<64, 128, 4, true, false, 4, 4>(a, sc, st, what);
+    return launch_gemm<64, 128, 3, true, false, 4, 4>(a, sc, st, what);
 }
 
 extern "C" int64_t kbn_fp8_gemm_nt_noalloc_scratch_bytes(void) { return kScratchBytes; }

@@ -310,14 +310,16 @@ __device__ __forceinline__ void splitk_sum_rows(const GemmArgs& a, int trel, int
     }
 }
 
-// LDS bytes of a tile configuration of four wavefronts (an A row of a stage
-// is 128 fp8 bytes, or 256 bf16 bytes when the kernel quantizes bf16
-// activations itself); configurations that fit twice into a CU's 160 KB run
+// LDS bytes of a tile configuration of four wavefronts: a stage holds BM A
+// rows of 128 fp8 bytes, or, when the kernel quantizes bf16 activations
+// itself (fuse_a = rows of four per wavefront, 1, 2 or 4), 16 fuse_a bf16
+// rows of 256 bytes; configurations that fit twice into a CU's 160 KB run
 // two workgroups per CU.
-constexpr int gemm_lds_bytes(int bm, int bn, int stages, bool fuse_a = false) {
-    return stages * (bm * (fuse_a ? 2 * kRowB : kRowB) + bn * kRowB + 2048);
+constexpr int gemm_a_stage_bytes(int bm, int fuse_a) { return fuse_a ? 16 * fuse_a * 2 * kRowB : bm * kRowB; }
+constexpr int gemm_lds_bytes(int bm, int bn, int stages, int fuse_a = 0) {
+    return stages * (gemm_a_stage_bytes(bm, fuse_a) + bn * kRowB + 2048);
 }
-constexpr int gemm_occupancy(int bm, int bn, int stages, bool fuse_a = false) {
+constexpr int gemm_occupancy(int bm, int bn, int stages, int fuse_a = 0) {
     return gemm_lds_bytes(bm, bn, stages, fuse_a) <= 80 * 1024 ? 2 : 1;
 }
 
@@ -341,24 +343,29 @@ constexpr int gemm_occupancy(int bm, int bn, int stages, bool fuse_a = false) {
 // So kStages-1 blocks are in flight while one is consumed, and no fragment
 // register set is ever copied.
 //
-// kFuseA: A arrives as bf16 (a.X) and is quantized by the kernel, 1x128
-// groups with UE8M0 scales exactly as the quant kernel does it
-// (quant.hip), so the product equals quant + GEMM bit for bit.  A stage
-// then holds the bf16 A rows (256 B each, 16-B chunk c of row r in slot
-// c ^ (r & 15), conflict-free for 16 consecutive rows); each wavefront reads
-// its fragment rows' 128 values of a block (two lanes per row), takes the
-// group absmax across the lane pair, and converts them to the fp8 fragments
-// of both K halves.
+// kFuseA (1, 2 or 4; 0 = off): A arrives as bf16 (a.X) and is quantized
+// by the kernel, 1x128 groups with UE8M0 scales exactly as the quant kernel
+// does it (quant.hip), so the product equals quant + GEMM bit for bit.  A
+// stage then holds 16 kFuseA bf16 A rows of 256 B (the caller keeps
+// M <= 16 kFuseA; the tile's rows past those are never loaded, and what the
+// MFMAs make of them is never stored).  Tile row r sits at LDS row
+// p(r) = (r % 4) 4 kFuseA + r / 4 (wavefront w's DMAs bring rows w, w + 4,
+// w + 8, ... into LDS rows 4 kFuseA w, +1, ...), and its 16-B chunk c in slot
+// c ^ (r & 15), so 16 consecutive tile rows read conflict-free.  Each
+// wavefront quantizes the 4 kFuseA rows its own DMAs brought, in place,
+// with 16 / kFuseA lanes per row.
 template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, bool kSplitK, int kWaves, bool kSorted = false,
-          bool kFuseA = false>
-__global__ __launch_bounds__(64 * kWaves, (kStages * (BM * (kFuseA ? 2 : 1) + BN) * 128 + kStages * 512 * kWaves <=
+          int kFuseA = 0>
+__global__ __launch_bounds__(64 * kWaves, (kStages * (gemm_a_stage_bytes(BM, kFuseA) + BN * 128) +
+                                               kStages * 512 * kWaves <=
                                            80 * 1024)
                                               ? 2
                                               : 1) void
 gemm_bs_kernel(const GemmArgs a) {
     static_assert(!(kSorted && (kGrouped || kSplitK)), "the sorted-token layout is its own grouped mode");
-    static_assert(!kFuseA || (kUe8m0 && !kGrouped && !kSorted && BM == 64 && kWaves == 4),
-                  "in-kernel activation quant: UE8M0, dense, 64-row tiles of four wavefronts");
+    static_assert(!kFuseA || (kUe8m0 && !kGrouped && !kSorted && BM == 64 && kWaves == 4 &&
+                              (kFuseA == 1 || kFuseA == 2 || kFuseA == 4)),
+                  "in-kernel activation quant: UE8M0, dense, 64-row tiles of four wavefronts, 16/32/64 rows");
     static_assert(kWaves == 4 || kWaves == 8, "2x2 or 2x4 wavefronts");
     constexpr int WM = 2, WN = kWaves / 2;
     constexpr int TM = BM / WM, TN = BN / WN;   // wavefront tile
@@ -367,7 +374,8 @@ gemm_bs_kernel(const GemmArgs a) {
     static_assert(BM <= 64 * kWaves && BM % (16 * kWaves) == 0 && BN % (16 * kWaves) == 0, "DMA tiling");
     static_assert(128 % TN == 0 || TN % 128 == 0, "wave N tile must not straddle a scale block");
     constexpr int kArow = kFuseA ? 2 * kRowB : kRowB;   // LDS bytes of one A row of a stage
-    constexpr int kA = BM * kArow, kB = BN * kRowB, kSA = kWaves * 256, kSW = kWaves * 256;
+    constexpr int kA = gemm_a_stage_bytes(BM, kFuseA), kB = BN * kRowB, kSA = kWaves * 256, kSW = kWaves * 256;
+    constexpr int kAW = 4 * (kFuseA ? kFuseA : 1);     // fused A: LDS rows per wavefront
     constexpr int kStage = kA + kB + kSA + kSW;
     static_assert(kStages >= 2 && kStages * kStage <= 160 * 1024, "LDS budget");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStage];
@@ -429,11 +437,10 @@ gemm_bs_kernel(const GemmArgs a) {
     // DMA lane mapping: one instruction = 8 rows x 128 B starting at row
     // r0 = 8 q; lane i fills slot i % 8 of row r0 + i / 8 with global chunk
     // (i % 8) ^ swz(r0 + i / 8) = (i % 8) ^ ((i >> 4) | 4 (q & 1)).
-    // fused bf16 A: 4-row DMAs (16 lanes x 16 B per row), 4 per wave
-    constexpr int kAInstr = kFuseA ? BM * 2 * kRowB / (1024 * kWaves) : BM / (8 * kWaves);
+    // fused bf16 A: kFuseA 4-row DMAs (16 lanes x 16 B per row) per wave
+    constexpr int kAInstr = kFuseA ? kFuseA : BM / (8 * kWaves);
     constexpr int kBInstr = BN / (8 * kWaves);   // 8-row DMAs per wave
-    static_assert(kAInstr % 2 == 0 && kBInstr % 2 == 0, "even instruction counts keep q & 1 == i & 1");
-    static_assert(!kFuseA || kAInstr == 4, "fused A: the swizzle below assumes 16 rows per wavefront");
+    static_assert((kFuseA || kAInstr % 2 == 0) && kBInstr % 2 == 0, "even instruction counts keep q & 1 == i & 1");
     const int drow = lane >> 3;
     const int ch_e = ((lane & 7) ^ (lane >> 4)) << 4;
     const int ch_o = ((lane & 7) ^ ((lane >> 4) | 4)) << 4;
@@ -441,13 +448,14 @@ gemm_bs_kernel(const GemmArgs a) {
     const int a_o = a_e - ch_e + ch_o;
     const int w_e = (int)((wave * kBInstr * 8 + drow) * a.ldw) + ch_e + kb0 * kRowB;
     const int w_o = w_e - ch_e + ch_o;
-    // fused A: byte offset of this lane's 16-B chunk for instruction i: row
-    // 16 wave + 4 i + lane / 16, slot lane % 16 <- global chunk slot ^ (row & 15)
+    // fused A: instruction i of wavefront w fills LDS rows 4 kFuseA w + 4 i + lane / 16
+    // with tile row r = w + 16 i + 4 (lane / 16); slot lane % 16 <- global chunk
+    // slot ^ (r & 15); this lane's byte offset of its chunk in X
     int xa_off[kFuseA ? kAInstr : 1];
     if constexpr (kFuseA) {
 #pragma unroll
         for (int i = 0; i < kAInstr; ++i) {
-            const int row = wave * 16 + 4 * i + (lane >> 4);
+            const int row = wave + 16 * i + 4 * (lane >> 4);
             xa_off[i] = row * (int)(a.ldx * 2) + (((lane & 15) ^ (row & 15)) << 4) + kb0 * 2 * kRowB;
         }
     }
@@ -531,8 +539,17 @@ gemm_bs_kernel(const GemmArgs a) {
         const int f = q >> 1, h = q & 1;
         const int c = 4 * kk + 2 * (lane >> 5) + h;
         const uint8_t* tile = f < FM ? st + (wm * TM + f * 32) * kArow : st + kA + (wn * TN + (f - FM) * 32) * kRowB;
-        // fused A rows: 256-B stride, chunk c of row r in slot c ^ (r & 15) (fragments start at multiples of 16 rows)
-        const int off = (kFuseA && f < FM) ? (lane & 31) * kArow + ((c ^ (lane & 15)) << 4) : frow + ((c ^ fs) << 4);
+        // fused A rows: tile row r at LDS row (r % 4) kAW + r / 4 (256 B each),
+        // chunk c in slot c ^ (r & 15); rows past 4 kAW (never stored) alias
+        // loaded ones so every read stays inside the stage's A rows
+        int off;
+        if (kFuseA && f < FM) {
+            const int r = wm * TM + f * 32 + (lane & 31);
+            off = ((r & 3) * kAW + ((r >> 2) & (kAW - 1))) * kArow + ((c ^ (r & 15)) << 4) -
+                  (int)(tile - st);
+        } else {
+            off = frow + ((c ^ fs) << 4);
+        }
         const v4i v = *reinterpret_cast<const v4i*>(tile + off);
         if (f < FM) {
             if (h) af[f].hi = v; else af[f].lo = v;
@@ -635,52 +652,66 @@ gemm_bs_kernel(const GemmArgs a) {
     constexpr int kT = FM * FN;           // MFMAs per sub-step
     constexpr int kR = 2 * (FM + FN);     // 16-B fragment reads per sub-step
 
-    // Fused A: this wavefront's 16 rows of a block (the rows its own DMAs
-    // brought in: 16 wave + i) quantized in place, four lanes per row and
-    // 32 values per lane: the group absmax (packed 16-bit max of the
-    // sign-cleared words, then over the lane quad), the UE8M0 scale and the
-    // codes exactly as the quant kernel derives them (its general path for a
-    // group with an infinity, a NaN or a subnormal scale); the 128 code bytes
-    // of row r take chunk slots c ^ (r & 15) of the row's 256 bytes, the
-    // scale goes to the stage's activation-scale slot.  Every lane's loads
-    // complete before the first write (the quad max consumes them all), and
-    // no other wavefront reads these rows before the next barrier.
+    // Fused A: the 4 kFuseA rows of a block this wavefront's own DMAs
+    // brought (tile rows w, w + 4, ...), quantized in place, 16 / kFuseA lanes
+    // per row and 8 kFuseA values per lane: the group absmax (packed 16-bit
+    // max of the sign-cleared words, then over the row's lanes by DPP), the
+    // UE8M0 scale and the codes exactly as the quant kernel derives them (its
+    // general path for a group with an infinity, a NaN or a subnormal scale);
+    // fp8 chunk c of row r takes slot c ^ (r & 15) of the row's 256 bytes, the
+    // scale the stage's activation-scale slot.  Every lane's loads complete
+    // before the first write (the DPP max consumes them all), and no other
+    // wavefront reads these rows before the next barrier.
     auto quant_rows = [&](const uint8_t* st_c) {
         if constexpr (kFuseA) {
             typedef uint16_t u16v2 __attribute__((ext_vector_type(2)));
+            constexpr int kQ = kFuseA;            // 16-B bf16 chunks per lane
+            constexpr int kLanes = 16 / kQ;       // lanes per row
             uint8_t* st = const_cast<uint8_t*>(st_c);
-            const int r = wave * 16 + (lane >> 2), j = lane & 3, sr = r & 15;
-            uint8_t* row = st + r * kArow;
-            u32x4 v[4];
+            const int pl = lane / kLanes;         // row of this wave: LDS row 16 w + pl
+            const int r = wave + 4 * pl, sr = r & 15;
+            const int c0 = (lane % kLanes) * kQ;  // first bf16 chunk of the lane
+            uint8_t* row = st + (kAW * wave + pl) * kArow;
+            u32x4 v[kQ];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) v[q] = *reinterpret_cast<const u32x4*>(row + (((4 * j + q) ^ sr) << 4));
+            for (int q = 0; q < kQ; ++q) v[q] = *reinterpret_cast<const u32x4*>(row + (((c0 + q) ^ sr) << 4));
             u16v2 m{0, 0};
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < kQ; ++q) {
                 m = __builtin_elementwise_max(m, __builtin_bit_cast(u16v2, v[q].x & 0x7FFF7FFFu));
                 m = __builtin_elementwise_max(m, __builtin_bit_cast(u16v2, v[q].y & 0x7FFF7FFFu));
                 m = __builtin_elementwise_max(m, __builtin_bit_cast(u16v2, v[q].z & 0x7FFF7FFFu));
                 m = __builtin_elementwise_max(m, __builtin_bit_cast(u16v2, v[q].w & 0x7FFF7FFFu));
             }
-            auto quad_max = [](uint32_t x) {
-                uint32_t t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false);  // [1,0,3,2]
-                x = x > t ? x : t;
-                t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false);           // [2,3,0,1]
-                return x > t ? x : t;
+            // max over the row's kLanes consecutive lanes (operands are non-negative float bits)
+            auto row_max = [](uint32_t x) {
+                if constexpr (kLanes == 16) {
+                    return row16_max_u32(x);
+                } else {
+                    uint32_t t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false);  // [1,0,3,2]
+                    x = x > t ? x : t;
+                    t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false);  // [2,3,0,1]
+                    x = x > t ? x : t;
+                    if constexpr (kLanes == 8) {
+                        t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xF, 0xF, false);  // row_half_mirror
+                        x = x > t ? x : t;
+                    }
+                    return x;
+                }
             };
-            const uint32_t abits = quad_max((uint32_t)(m.x > m.y ? m.x : m.y) << 16);
+            const uint32_t abits = row_max((uint32_t)(m.x > m.y ? m.x : m.y) << 16);
             float sc = ue8m0_ceil_div448(fmaxf(__uint_as_float(abits), a.eps));
-            uint32_t c[8];
+            uint32_t c[2 * kQ];
             if (ue8m0_fast_path(abits, sc)) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
+                for (int q = 0; q < kQ; ++q) {
                     c[2 * q] = pack4_e4m3_bf16(v[q].x, v[q].y, sc);
                     c[2 * q + 1] = pack4_e4m3_bf16(v[q].z, v[q].w, sc);
                 }
-            } else {   // uniform over the row's quad
+            } else {   // uniform over the row's lanes
                 float amax = 0.0f;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
+                for (int q = 0; q < kQ; ++q) {
                     amax = fmaxf(amax, fabsf(bf16lo(v[q].x)));
                     amax = fmaxf(amax, fabsf(bf16hi(v[q].x)));
                     amax = fmaxf(amax, fabsf(bf16lo(v[q].y)));
@@ -690,18 +721,25 @@ gemm_bs_kernel(const GemmArgs a) {
                     amax = fmaxf(amax, fabsf(bf16lo(v[q].w)));
                     amax = fmaxf(amax, fabsf(bf16hi(v[q].w)));
                 }
-                sc = ue8m0_ceil_div448(fmaxf(__uint_as_float(quad_max(__float_as_uint(amax))), a.eps));
+                sc = ue8m0_ceil_div448(fmaxf(__uint_as_float(row_max(__float_as_uint(amax))), a.eps));
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
+                for (int q = 0; q < kQ; ++q) {
                     c[2 * q] = pack4_e4m3_ue8m0_general(bf16lo(v[q].x), bf16hi(v[q].x), bf16lo(v[q].y),
                                                         bf16hi(v[q].y), sc);
                     c[2 * q + 1] = pack4_e4m3_ue8m0_general(bf16lo(v[q].z), bf16hi(v[q].z), bf16lo(v[q].w),
                                                             bf16hi(v[q].w), sc);
                 }
             }
-            *reinterpret_cast<u32x4*>(row + (((2 * j) ^ sr) << 4)) = u32x4{c[0], c[1], c[2], c[3]};
-            *reinterpret_cast<u32x4*>(row + (((2 * j + 1) ^ sr) << 4)) = u32x4{c[4], c[5], c[6], c[7]};
-            if (j == 0) reinterpret_cast<float*>(st + kA + kB)[r] = sc;
+            // codes of bf16 chunk c0 + q are fp8 bytes [8 (c0 + q), +8): chunk (c0 + q) / 2, half (c0 + q) % 2
+            if constexpr (kQ == 1) {
+                *reinterpret_cast<uint2*>(row + (((c0 >> 1) ^ sr) << 4) + 8 * (c0 & 1)) = make_uint2(c[0], c[1]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < kQ; q += 2)
+                    *reinterpret_cast<u32x4*>(row + ((((c0 + q) >> 1) ^ sr) << 4)) =
+                        u32x4{c[2 * q], c[2 * q + 1], c[2 * q + 2], c[2 * q + 3]};
+            }
+            if (lane % kLanes == 0) reinterpret_cast<float*>(st + kA + kB)[r] = sc;
         } else {
             (void)st_c;
         }
@@ -978,7 +1016,7 @@ struct Schedule {
     int splits = 1, kb_per_split = 0;  // the tail [dp_tiles, tiles)
     int64_t ws_bytes = 0;         // fp32 slabs of the tail
     bool fused = false;           // the split launch sums the slabs itself
-    bool fuse_a = false;          // bf16 activations quantized by the GEMM (LDS A rows of 256 B)
+    int fuse_a = 0;               // bf16 activations quantized by the GEMM: rows of four per wavefront (1, 2, 4)
 };
 
 // Split-K tails of the 64-row tiles summed by the split launch itself (no
@@ -1002,7 +1040,7 @@ unsigned* splitk_flags_for(hipStream_t st, int64_t tail_tiles);
 // accumulators per lane need the AGPRs.
 int launch_gemm_256(const GemmArgs& a, const Schedule& sc, int64_t K, hipStream_t st, const char* what);
 
-template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, int kWaves = 4, bool kFuseA = false>
+template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, int kWaves = 4, int kFuseA = 0>
 static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const char* what) {
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;

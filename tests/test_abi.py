@@ -145,18 +145,19 @@ def test_bf16a_gemm_rejects_bad_shapes_and_plans_like_the_dense_gemm():
 
 
 def test_bf16a_routing_rule():
-    """Fp8Linear takes the bf16-activation GEMM where its plan splits K into
-    workgroups of at most 16 blocks within one wave of tiles (measured faster
-    than quant + GEMM on MI355X: cfg1, Llama-70B o at every M), and stays
-    with quant + GEMM for long K per workgroup (qkv, down), more tiles than
-    CUs (gate_up), unsplit plans and M > 64."""
+    """Fp8Linear takes the bf16-activation GEMM for every shape up to 32 rows
+    (measured faster than quant + GEMM on MI355X on all Llama-70B decode
+    shapes), and at 33-64 rows only where its plan splits K into workgroups
+    of at most 16 blocks within one wave of tiles (2048 x 2048, o); long K per
+    workgroup (qkv, down), more tiles than CUs (gate_up), unsplit plans and
+    M > 64 stay with quant + GEMM."""
     from kb_nano_amd._lib import lib
     L = lib()
     if torch.cuda.device_count() > 0 and torch.cuda.get_device_properties(0).multi_processor_count != 256:
         pytest.skip("the plan depends on the device's CU count; pinned for 256 CUs")
-    yes = [(64, 2048, 2048), (1, 2048, 2048), (1, 8192, 8192), (64, 8192, 8192), (32, 7168, 2048)]
-    no = [(1, 10240, 8192), (32, 10240, 8192), (1, 8192, 28672), (1, 57344, 8192), (64, 7168, 2048),
-          (65, 2048, 2048), (8, 2048, 200)]
+    yes = [(1, 10240, 8192), (32, 57344, 8192), (16, 8192, 28672), (64, 2048, 2048), (64, 8192, 8192)]
+    no = [(64, 10240, 8192), (64, 8192, 28672), (64, 57344, 8192), (64, 7168, 2048), (65, 2048, 2048),
+          (8, 2048, 200)]
     for M, N, K in yes:
         assert L.kbn_fp8_gemm_bf16a_preferred(M, N, K) == 1, (M, N, K)
     for M, N, K in no:
