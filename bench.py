@@ -255,7 +255,7 @@ def bench_linear(steps, warmup, dev):
     for name, M, N, K, seed in cases:
         if (N, K) not in weights:
             w, sw = synthetic.dense_weight(N, K, seed=seed, device=dev)
-            n = _copies_for(N * K, 1) if N * K > 64 * 2 ** 20 else 1
+            n = _copies_for(N * K, 1) if N * K >= 32 * 2 ** 20 else 1
             weights[(N, K)] = [(w.clone(), sw.clone()) for _ in range(n)]
             del w, sw
         ws = weights[(N, K)]
