@@ -87,7 +87,8 @@ int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int64_t sA_stri
  * would leave CUs idle (small M, or few N tiles) split K across workgroups,
  * write fp32 partial sums into `workspace` and sum them in a fixed order (so
  * results are deterministic and equal for any split count up to fp32
- * summation order): for M <= 32 the last workgroup of each tile does it in
+ * summation order): for few rows (M <= 32; up to 64 with short, shallow
+ * splits) the last workgroup of each tile does it in
  * the same launch, using per-tile arrival counters the library keeps in a
  * static device array per stream (per capturing stream under capture,
  * streams forked into one capture included); otherwise, or

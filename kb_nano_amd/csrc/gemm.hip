@@ -48,7 +48,7 @@ static void plan_tail(Schedule& s, int64_t M, int KBT) {
         const int ss = (KBT + kbps - 1) / kbps;
         const int64_t wgs = rem * ss;
         if (wgs > slots) break;
-        const bool fused = fused_split_sum(s.bm, M, ss);
+        const bool fused = fused_split_sum(s.bm, M, ss, kbps);
         const double fixed = fused ? 2.0 : 3.0, per_split = fused ? 0.4 : 0.2;
         const double cost = (kbps + fill) * t_block + fixed + per_split * ss + per_mb * slab_mb * ss * rem;
         if (cost < best - 1e-9) {

@@ -946,7 +946,7 @@ gemm_bs_kernel(const GemmArgs a) {
 
     if constexpr (kSplitK) {
         epilogue_partial();
-        // the fused sum is only planned for the 64-row tiles (M <= 48)
+        // the fused sum is only planned for the 64-row tiles (fused_split_sum)
         if constexpr (BM <= 64) if (a.flags) {
             // Fused reduction: every wavefront's (device-coherent) slab stores
             // have completed before its workgroup counts itself in; the
@@ -1021,15 +1021,18 @@ struct Schedule {
 
 // Split-K tails of the 64-row tiles summed by the split launch itself (no
 // reduction launch, about 3 us less host time per call): up to 32 rows
-// always, up to 48 rows when a tile has at most 4 splits.  The summing
-// workgroup reads its tile's slabs alone, so more rows or deeper splits
-// measure slower than the separate reduction spread over 8-row strips
-// (64 rows: 1024 x 28672 15.1 -> 17.1 us, 8192 x 28672 44.1 -> 46.3 us;
-// 40-48 rows, 3-4 splits: 10240 x 8192 21.0 -> 19.9 us, 8192 x 8192
-// 18.2 -> 17.2 us).
-constexpr int kFusedReduceRows = 32, kFusedShallowRows = 48, kFusedShallowSplits = 4;
-constexpr bool fused_split_sum(int bm, int64_t M, int splits) {
-    return bm <= 64 && (M <= kFusedReduceRows || (M <= kFusedShallowRows && splits <= kFusedShallowSplits));
+// always, up to 48 rows when a tile has at most 4 splits, up to 64 rows when
+// it also has at most 24 K blocks per split.  The summing workgroup reads
+// its tile's slabs alone, so more rows, deeper splits or long splits (whose
+// workgroups finish far apart) measure slower than the separate reduction
+// spread over 8-row strips (64 rows: 1024 x 28672 15.1 -> 17.1 us,
+// 8192 x 28672 44.1 -> 46.3 us; 40-64 rows with 3-4 splits of at most 22
+// blocks: 10240 x 8192 21.9 -> 21.0 us at 49 rows, 8192 x 8192 19.9 -> 18.5
+// us at 49 rows and 20.2 -> 19.9 us at 64, 2048 x 2048 10.9 -> 10.3 us).
+constexpr int kFusedReduceRows = 32, kFusedShallowRows = 48, kFusedShallowSplits = 4, kFusedShortKb = 24;
+constexpr bool fused_split_sum(int bm, int64_t M, int splits, int kb_per_split) {
+    return bm <= 64 && (M <= kFusedReduceRows || (M <= kFusedShallowRows && splits <= kFusedShallowSplits) ||
+                        (M <= 64 && splits <= kFusedShallowSplits && kb_per_split <= kFusedShortKb));
 }
 // Arrival counters of the fused split-K reduction for one launch on `st`, or
 // nullptr (then the separate reduction kernel runs); defined in gemm.hip.
