@@ -66,6 +66,19 @@ int kbn_silu_mul_quant_fp8(const void* in_bf16, int64_t M, int64_t N_half, int64
                            float eps, int use_ue8m0, void* stream);
 
 /*
+ * kbn_silu_mul_quant_fp8 over the rows whose id is not negative: rows r with
+ * row_ids[r] < 0 are neither read nor written (int32 row_ids[M], device
+ * memory).  No counterpart in the reference: FusedExperts (fused_experts.py:
+ * 246-283) runs SiLU*Mul+quant over all M_sum rows of the contiguous layout,
+ * whose padding rows (expert id -1) GEMM1 never wrote and GEMM2 never reads;
+ * with the expert ids as row ids those rows cost no traffic.
+ */
+int kbn_silu_mul_quant_fp8_rows(const void* in_bf16, int64_t M, int64_t N_half, int64_t ld_in,
+                                void* q_fp8, int64_t ld_q, float* scale,
+                                int64_t s_stride_m, int64_t s_stride_g,
+                                float eps, int use_ue8m0, const int32_t* row_ids, void* stream);
+
+/*
  * Block-scaled FP8 GEMM, "NT" (both operands K-contiguous).
  * Replaces op kb_nano_fp8::fp8_gemm_nt -> deep_gemm.fp8_gemm_nt
  * (tasks/baseline/L1/fp8_linear.py:89-118).

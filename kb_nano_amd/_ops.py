@@ -117,9 +117,11 @@ def per_token_group_quant_fp8(x: torch.Tensor, out_fp8: torch.Tensor, out_scale:
 
 
 def silu_mul_quant_fp8(inp: torch.Tensor, out_fp8: torch.Tensor, out_scale: torch.Tensor,
-                       use_ue8m0: bool = True, eps: float = QUANT_EPS) -> None:
+                       use_ue8m0: bool = True, eps: float = QUANT_EPS, row_ids: torch.Tensor | None = None) -> None:
     """y = bf16(silu(gate) * up) for ``inp = [gate | up]`` (bf16 [M, 2N']),
-    quantized 1x128 into ``out_fp8 [M,N']`` and ``out_scale [M, N'/128]``."""
+    quantized 1x128 into ``out_fp8 [M,N']`` and ``out_scale [M, N'/128]``.
+    With ``row_ids`` (int32 [M], e.g. the contiguous MoE layout's expert ids),
+    rows whose id is negative are neither read nor written."""
     what = "silu_mul_quant_fp8"
     idx = inp.get_device()
     if (idx not in _GFX950_DEVICES or idx != _cur_device() or out_fp8.get_device() != idx
@@ -136,6 +138,16 @@ def silu_mul_quant_fp8(inp: torch.Tensor, out_fp8: torch.Tensor, out_scale: torc
     xs, qs, ss = inp.stride(), out_fp8.stride(), out_scale.stride()
     if xs[1] != 1 or qs[1] != 1:
         raise ValueError(f"{what}: input and output rows must be contiguous")
+    if row_ids is not None:
+        if (row_ids.get_device() != idx or row_ids.dtype is not torch.int32 or row_ids.dim() != 1
+                or row_ids.shape[0] < M or (M > 1 and row_ids.stride(0) != 1)):
+            raise ValueError(f"{what}: row_ids must be a contiguous int32 vector of at least M={M} on the input's device")
+        rc = lib().kbn_silu_mul_quant_fp8_rows(
+            inp.data_ptr(), M, Nh, xs[0], out_fp8.data_ptr(), qs[0], out_scale.data_ptr(), ss[0], ss[1],
+            float(eps), 1 if use_ue8m0 else 0, row_ids.data_ptr(), _raw_stream(idx))
+        if rc:
+            check(rc, what)
+        return
     rc = lib().kbn_silu_mul_quant_fp8(
         inp.data_ptr(), M, Nh, xs[0], out_fp8.data_ptr(), qs[0], out_scale.data_ptr(), ss[0], ss[1],
         float(eps), 1 if use_ue8m0 else 0, _raw_stream(idx))

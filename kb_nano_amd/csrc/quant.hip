@@ -72,6 +72,10 @@ struct QuantArgs {
     int rows_per_xcd;       // contiguous rows owned by one XCD (multiple of kLineRows)
     int step_q, step_r;     // per-pass stride inside an XCD's rows, as (rows, groups)
     float eps;
+    // optional per-row ids (nullptr: every row): rows whose id is negative
+    // (the padding rows of the contiguous MoE layout) are neither read nor
+    // written
+    const int32_t* row_ids;
 };
 
 // Position of a lane's group in the (row, group) space.
@@ -184,7 +188,9 @@ __device__ __forceinline__ float quant8_store(const uint32_t (&w)[4], float eps,
 // workgroups walk the flattened (row, group) space so that one pass covers a
 // contiguous range, each wavefront reading kUnroll consecutive blocks of 4
 // groups (1 KB of bf16 per operand and block) before any arithmetic.
-template <bool kSilu, bool kUe8m0>
+// kRows: rows whose a.row_ids entry is negative are skipped (no loads, no
+// stores); the ids are read one pass ahead.
+template <bool kSilu, bool kUe8m0, bool kRows = false>
 __global__ __launch_bounds__(kThreads) void group_quant_kernel(const QuantArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t lut[kSilu ? 65536 : 8];
     if constexpr (kSilu) {  // stage the bf16 SiLU table: 8192 x 16 B
@@ -201,6 +207,17 @@ __global__ __launch_bounds__(kThreads) void group_quant_kernel(const QuantArgs a
     constexpr int kUnroll = kUnrollOf<kSilu>;
     const int64_t t0 = ((int64_t)local * (kThreads / 64) + wave) * (4 * kUnroll) + (lane >> 4);
     GroupCursor c{row_begin + (int)(t0 / a.G), (int)(t0 % a.G)};
+    // kRows: the row ids of the groups of the next pass, loaded one pass
+    // ahead (an id below zero skips the group: no loads, no stores)
+    int rid[kRows ? kUnroll : 1];
+    if constexpr (kRows) {
+        GroupCursor cn = c;
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            rid[u] = cn.row < row_end ? a.row_ids[cn.row] : -1;
+            cn.step4(a.G);
+        }
+    }
     while (c.row < row_end) {
         GroupCursor cu[kUnroll];
         cu[0] = c;
@@ -209,18 +226,33 @@ __global__ __launch_bounds__(kThreads) void group_quant_kernel(const QuantArgs a
             cu[u] = cu[u - 1];
             cu[u].step4(a.G);
         }
+        bool skip[kRows ? kUnroll : 1];   // kRows: this pass's groups of skipped rows
+        if constexpr (kRows) {
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) skip[u] = rid[u] < 0;
+        }
         u32x4 xa[kUnroll], xb[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u)
-            if (cu[u].row < row_end) {
+            if (cu[u].row < row_end && !(kRows && skip[kRows ? u : 0])) {
                 const uint16_t* p = a.x + (int64_t)cu[u].row * a.ld_x + (int64_t)cu[u].g * kGroup + sub * 8;
                 xa[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
                 if constexpr (kSilu) xb[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + a.up_off));
             }
         c.advance(a.step_q, a.step_r, a.G);
+        if constexpr (kRows) {
+            GroupCursor cn = c;
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                rid[u] = cn.row < row_end ? a.row_ids[cn.row] : -1;
+                cn.step4(a.G);
+            }
+        }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             if (cu[u].row >= row_end) break;  // uniform over the group's 16 lanes; rows grow with u
+            if constexpr (kRows)
+                if (skip[u]) continue;        // a skipped row (uniform over the group's lanes)
             uint32_t w[4];
             if constexpr (kSilu) {
                 w[0] = silu_mul_pair(lut, xa[u].x, xb[u].x);
@@ -309,6 +341,27 @@ extern "C" int kbn_silu_mul_quant_fp8(const void* in_bf16, int64_t M, int64_t N_
         group_quant_kernel<true, true><<<blocks, kThreads, 0, st>>>(a);
     else
         group_quant_kernel<true, false><<<blocks, kThreads, 0, st>>>(a);
+    KBN_CHECK_LAUNCH(what);
+    return 0;
+}
+
+extern "C" int kbn_silu_mul_quant_fp8_rows(const void* in_bf16, int64_t M, int64_t N_half, int64_t ld_in,
+                                           void* q_fp8, int64_t ld_q, float* scale, int64_t s_stride_m,
+                                           int64_t s_stride_g, float eps, int use_ue8m0, const int32_t* row_ids,
+                                           void* stream) {
+    const char* what = "silu_mul_quant_fp8_rows";
+    if (int rc = check_quant_args(what, in_bf16, M, N_half, ld_in, q_fp8, ld_q, scale)) return rc;
+    if (M == 0 || N_half == 0) return 0;
+    KBN_CHECK_ARG(ld_in >= 2 * N_half, "%s: input row stride smaller than 2*N/2", what);
+    KBN_CHECK_ARG(row_ids, "%s: null row ids", what);
+    QuantArgs a{(const uint16_t*)in_bf16, ld_in, N_half, (uint8_t*)q_fp8, ld_q, scale, s_stride_m, s_stride_g,
+                (int)M, (int)(N_half / kGroup), 0, 0, 0, eps, row_ids};
+    const int blocks = plan(a, 1, kUnrollOf<true>);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (use_ue8m0)
+        group_quant_kernel<true, true, true><<<blocks, kThreads, 0, st>>>(a);
+    else
+        group_quant_kernel<true, false, true><<<blocks, kThreads, 0, st>>>(a);
     KBN_CHECK_LAUNCH(what);
     return 0;
 }

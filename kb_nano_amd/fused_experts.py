@@ -27,6 +27,7 @@ import math
 import torch
 import torch.nn as nn
 
+from . import _ops
 from .fp8_linear import PerTokenGroupQuantFp8
 from .moe_grouped_gemm import _valid_deep_gemm, m_grouped_fp8_gemm_nt_contiguous
 from .moe_layout import _compute_aligned_M, _deepgemm_permute, _deepgemm_unpermute_and_reduce
@@ -154,7 +155,17 @@ class FusedExperts(nn.Module):
         m_grouped_fp8_gemm_nt_contiguous((a1_perm, a1_scale_perm), (w13, w13_scale), mm1_out, expert_ids)
 
         quant_out = self._get_dg_workspace(2, (M_sum, N), dev, torch.float8_e4m3fn)
-        a2_fp8, a2_scale = self.silu_mul_quant_fp8(mm1_out, output=quant_out)
+        if type(self.silu_mul_quant_fp8) is SiluMulQuantFp8 and not torch.compiler.is_compiling():
+            # this package's module: the same launch over the rows with an
+            # expert id only (padding rows hold nothing GEMM1 wrote and GEMM2
+            # never reads; half of config 4's rows), scales column-major as
+            # the module makes them
+            a2_fp8 = quant_out
+            a2_scale = torch.empty_strided((M_sum, N // _FP8_GROUP_SIZE), (1, M_sum), dtype=torch.float32,
+                                           device=dev)
+            _ops.silu_mul_quant_fp8(mm1_out, a2_fp8, a2_scale, True, 1e-10, row_ids=expert_ids)
+        else:   # a swapped-in module (or the compiler's trace) keeps the reference's call
+            a2_fp8, a2_scale = self.silu_mul_quant_fp8(mm1_out, output=quant_out)
 
         mm2_out = self._get_dg_workspace(1, (M_sum, K), dev, hidden_states.dtype)
         m_grouped_fp8_gemm_nt_contiguous((a2_fp8, a2_scale), (w2, w2_scale), mm2_out, expert_ids)

@@ -49,6 +49,13 @@ def test_quant_rejects_ragged_k_without_device():
     assert rc == 1 and "multiple of 128" in _err()
 
 
+def test_silu_rows_rejects_null_row_ids():
+    from kb_nano_amd._lib import lib
+    p = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    assert lib().kbn_silu_mul_quant_fp8_rows(p, 128, 256, 512, p, 256, p, 1, 128, 1e-10, 1, None, None) == 1
+    assert "row ids" in _err()
+
+
 def test_silu_rejects_ragged_n():
     from kb_nano_amd._lib import lib
     rc = lib().kbn_silu_mul_quant_fp8(None, 8, 100, 200, None, 100, None, 1, 1, 1e-10, 1, None)

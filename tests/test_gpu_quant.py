@@ -161,6 +161,33 @@ def test_silu_mul_quant_module(gpu_device):
         SiluMulQuantFp8()(x[:100])   # M % 128 != 0, as the reference asserts
 
 
+@pytest.mark.parametrize("M,Nh", [(384, 512), (4096, 2048)])
+def test_silu_mul_quant_skips_rows_with_negative_ids(gpu_device, M, Nh):
+    """Row ids (the contiguous MoE layout's expert ids, as FusedExperts
+    passes them): rows whose id is negative are neither read nor written
+    (their codes and scales keep a sentinel); every other row is bit-exact
+    against the oracle."""
+    from kb_nano_amd import _ops
+    x = seeded_bf16((M, 2 * Nh), seed=M + 3, outlier_frac=1e-3)
+    g = torch.Generator().manual_seed(M)
+    ids = torch.randint(0, 256, (M,), generator=g, dtype=torch.int32)
+    ids[torch.rand(M, generator=g) < 0.45] = -1
+    ids[:3] = -1   # a run at the start, and the last row too
+    ids[-1] = -1
+    keep = (ids >= 0).numpy()
+    qo, so = oracle.silu_mul_quant(bf16_bits(x))
+    xd, idd = x.to(gpu_device), ids.to(gpu_device)
+    q = torch.full((M, Nh), 0x55, dtype=torch.uint8, device=gpu_device).view(torch.float8_e4m3fn)
+    s = torch.full((Nh // 128, M), -3.0, device=gpu_device).t()
+    _ops.silu_mul_quant_fp8(xd, q, s, row_ids=idd)
+    torch.cuda.synchronize()
+    qc, sc = fp8_codes(q), s.cpu().numpy()
+    assert np.array_equal(qc[keep], qo[keep])
+    assert np.array_equal(sc[keep], so[keep])
+    assert (qc[~keep] == 0x55).all(), "a skipped row was written"
+    assert (sc[~keep] == -3.0).all(), "a skipped row's scales were written"
+
+
 def test_silu_mul_quant_cfg2_full(gpu_device):
     """BASELINE config 2 at full size: [8192, 36864] bf16 with 0.1% x50
     outliers, checked bit-exact against the oracle on every row."""
