@@ -54,7 +54,8 @@ constexpr int kThreads = 1024;       // 16 wavefronts
 // 4-group blocks per wavefront per pass (per operand): the SiLU kernel runs
 // one workgroup per CU (its LDS table), so it takes more blocks per pass to
 // keep as many bytes in flight (measured at cfg2: 4 -> 129 us, 2 -> 132 us,
-// 5..8 -> 136-140 us; the quant kernel is best at 2).
+// 5..8 -> 136-140 us; the quant kernel is best at 2).  The row-skipping
+// mode is best at 4 as well (cfg4 layout: 88 us against 90-92 us at 6 and 8).
 template <bool kSilu>
 constexpr int kUnrollOf = kSilu ? 4 : 2;
 constexpr int kXcds = 8;             // MI355X: workgroups are dealt round-robin to 8 XCDs
@@ -189,7 +190,10 @@ __device__ __forceinline__ float quant8_store(const uint32_t (&w)[4], float eps,
 // contiguous range, each wavefront reading kUnroll consecutive blocks of 4
 // groups (1 KB of bf16 per operand and block) before any arithmetic.
 // kRows: rows whose a.row_ids entry is negative are skipped (no loads, no
-// stores); the ids are read one pass ahead.
+// stores); the ids are read one pass ahead.  The rows are then dealt to the
+// XCDs in blocks of 32 (block b to XCD b % 8) instead of contiguous slices:
+// skipped rows cluster (an expert segment's padding, the layout's unused
+// tail), and contiguous slices would leave whole XCDs without work.
 template <bool kSilu, bool kUe8m0, bool kRows = false>
 __global__ __launch_bounds__(kThreads) void group_quant_kernel(const QuantArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t lut[kSilu ? 65536 : 8];
@@ -202,8 +206,11 @@ __global__ __launch_bounds__(kThreads) void group_quant_kernel(const QuantArgs a
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane & 15;
     const int xcd = blockIdx.x % kXcds, local = blockIdx.x / kXcds;
-    const int row_begin = xcd * a.rows_per_xcd;
-    const int row_end = min(a.M, row_begin + a.rows_per_xcd);
+    // kRows: the cursor walks XCD-local rows [0, rows_per_xcd); local row lr
+    // is global row ((lr / 32) * 8 + xcd) * 32 + lr % 32, valid below a.M
+    const int row_begin = kRows ? 0 : xcd * a.rows_per_xcd;
+    const int row_end = kRows ? a.rows_per_xcd : min(a.M, row_begin + a.rows_per_xcd);
+    auto grow = [&](int lr) { return kRows ? (((lr >> 5) * kXcds + xcd) << 5) + (lr & 31) : lr; };
     constexpr int kUnroll = kUnrollOf<kSilu>;
     const int64_t t0 = ((int64_t)local * (kThreads / 64) + wave) * (4 * kUnroll) + (lane >> 4);
     GroupCursor c{row_begin + (int)(t0 / a.G), (int)(t0 % a.G)};
@@ -214,7 +221,8 @@ __global__ __launch_bounds__(kThreads) void group_quant_kernel(const QuantArgs a
         GroupCursor cn = c;
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            rid[u] = cn.row < row_end ? a.row_ids[cn.row] : -1;
+            const int r = grow(cn.row);
+            rid[u] = cn.row < row_end && r < a.M ? a.row_ids[r] : -1;
             cn.step4(a.G);
         }
     }
@@ -235,7 +243,7 @@ __global__ __launch_bounds__(kThreads) void group_quant_kernel(const QuantArgs a
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u)
             if (cu[u].row < row_end && !(kRows && skip[kRows ? u : 0])) {
-                const uint16_t* p = a.x + (int64_t)cu[u].row * a.ld_x + (int64_t)cu[u].g * kGroup + sub * 8;
+                const uint16_t* p = a.x + (int64_t)grow(cu[u].row) * a.ld_x + (int64_t)cu[u].g * kGroup + sub * 8;
                 xa[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
                 if constexpr (kSilu) xb[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + a.up_off));
             }
@@ -244,7 +252,8 @@ __global__ __launch_bounds__(kThreads) void group_quant_kernel(const QuantArgs a
             GroupCursor cn = c;
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) {
-                rid[u] = cn.row < row_end ? a.row_ids[cn.row] : -1;
+                const int r = grow(cn.row);
+                rid[u] = cn.row < row_end && r < a.M ? a.row_ids[r] : -1;
                 cn.step4(a.G);
             }
         }
@@ -262,8 +271,9 @@ __global__ __launch_bounds__(kThreads) void group_quant_kernel(const QuantArgs a
             } else {
                 w[0] = xa[u].x; w[1] = xa[u].y; w[2] = xa[u].z; w[3] = xa[u].w;
             }
-            const float sc = quant8_store<kUe8m0, kSilu>(w, a.eps, sub, a.q + (int64_t)cu[u].row * a.ld_q + (int64_t)cu[u].g * kGroup);
-            if (sub == 0) a.s[(int64_t)cu[u].row * a.s_sm + (int64_t)cu[u].g * a.s_sg] = sc;
+            const int64_t r = grow(cu[u].row);
+            const float sc = quant8_store<kUe8m0, kSilu>(w, a.eps, sub, a.q + r * a.ld_q + (int64_t)cu[u].g * kGroup);
+            if (sub == 0) a.s[r * a.s_sm + (int64_t)cu[u].g * a.s_sg] = sc;
         }
     }
 }

@@ -161,12 +161,13 @@ def test_silu_mul_quant_module(gpu_device):
         SiluMulQuantFp8()(x[:100])   # M % 128 != 0, as the reference asserts
 
 
-@pytest.mark.parametrize("M,Nh", [(384, 512), (4096, 2048)])
-def test_silu_mul_quant_skips_rows_with_negative_ids(gpu_device, M, Nh):
+@pytest.mark.parametrize("M,Nh,tail", [(384, 512, 0.0), (1000, 384, 0.3), (4096, 2048, 0.25)])
+def test_silu_mul_quant_skips_rows_with_negative_ids(gpu_device, M, Nh, tail):
     """Row ids (the contiguous MoE layout's expert ids, as FusedExperts
     passes them): rows whose id is negative are neither read nor written
     (their codes and scales keep a sentinel); every other row is bit-exact
-    against the oracle."""
+    against the oracle.  Ragged M (not a multiple of the 32-row blocks the
+    rows are dealt in) and a skipped tail, as the layout's unused rows."""
     from kb_nano_amd import _ops
     x = seeded_bf16((M, 2 * Nh), seed=M + 3, outlier_frac=1e-3)
     g = torch.Generator().manual_seed(M)
@@ -174,6 +175,7 @@ def test_silu_mul_quant_skips_rows_with_negative_ids(gpu_device, M, Nh):
     ids[torch.rand(M, generator=g) < 0.45] = -1
     ids[:3] = -1   # a run at the start, and the last row too
     ids[-1] = -1
+    ids[M - int(tail * M):] = -1
     keep = (ids >= 0).numpy()
     qo, so = oracle.silu_mul_quant(bf16_bits(x))
     xd, idd = x.to(gpu_device), ids.to(gpu_device)
