@@ -14,6 +14,12 @@
 
 namespace kbn {
 
+// Contiguous-layout grouped GEMMs read their padding rows as zeros up to this K.
+#ifndef KBN_PAD_ZERO_MAX_K
+#define KBN_PAD_ZERO_MAX_K 2048
+#endif
+constexpr int64_t kPadZeroMaxK = KBN_PAD_ZERO_MAX_K;
+
 // Only tails whose split workgroups fit in one wave are split (more waves
 // never measured faster, and the allocation-free entry point's scratch is
 // sized for one wave).  Cost model in microseconds, fitted to sweeps of the
@@ -477,6 +483,11 @@ extern "C" int kbn_fp8_grouped_gemm_nt_contiguous(const void* A, int64_t lda, co
     a.expert_ids = expert_ids;
     KBN_CHECK_ARG(E <= 0x7FFFFFFFLL, "%s: too many experts", what);
     a.M = (int)M_sum; a.N = (int)N; a.K = (int)K; a.E = (int)E;
+    // Padding rows read as zeros for short K only: at cfg4 the down GEMM
+    // (K = 2048) gains, while over gate_up's K = 7168 an expert's nearly
+    // empty second row tile runs ahead of its first and the two stop sharing
+    // the expert's weight panel in L2.
+    a.a_pad_zero = K <= kPadZeroMaxK;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     Schedule sc;   // grouped: data-parallel, one workgroup per 128-row block x N tile
     if (scale_ue8m0) return launch_gemm<128, 256, 3, true, true>(a, sc, st, what);

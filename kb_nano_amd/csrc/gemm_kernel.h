@@ -94,6 +94,9 @@ struct GemmArgs {
     int64_t D_bytes;             // bytes at D the scattered stores may write
     const float* row_weight;     // [num_valid] fp32 factors of the output rows, or nullptr
     int sa_sorted;               // sA already holds row R's scales at R (gathered by sorted_scale_gather_kernel)
+    // Grouped: A rows of a tile that belong to no expert or another one (the
+    // layout's padding) are read as zeros instead of fetched.
+    int a_pad_zero;
     // bf16 activations quantized by the kernel itself (1x128 groups, UE8M0):
     // X [M, K] with row stride ldx elements, group absmax floor eps.
     const uint16_t* X;
@@ -459,6 +462,19 @@ gemm_bs_kernel(const GemmArgs a) {
             xa_off[i] = row * (int)(a.ldx * 2) + (((lane & 15) ^ (row & 15)) << 4) + kb0 * 2 * kRowB;
         }
     }
+    // grouped with a.a_pad_zero: bit i set when the row of this lane's A
+    // instruction i is not one of the tile expert's rows (its DMA reads zeros;
+    // those rows are never stored)
+    uint32_t a_dead = 0;
+    if constexpr (kGrouped) {
+        if (a.a_pad_zero) {
+#pragma unroll
+            for (int i = 0; i < kAInstr; ++i) {
+                const int r = m0 + wave * kAInstr * 8 + i * 8 + drow;
+                if (r >= a.M || a.expert_ids[r] != expert) a_dead |= 1u << i;
+            }
+        }
+    }
     // sorted layout: byte offset of each DMA row of this lane's A instructions
     // (gathered rows; padding reads zeros)
     int a_row[kSorted ? kAInstr : 1];
@@ -510,7 +526,7 @@ gemm_bs_kernel(const GemmArgs a) {
             if constexpr (kFuseA) off = xa_off[i] + s * 2 * kRowB;
             else if constexpr (kSorted) off = a_row[i] + ((i & 1) ? ch_o : ch_e) + k0;
             else off = ((i & 1) ? a_o : a_e) + (int)(i * 8 * a.lda) + k0;
-            dma_b128(dA, base + (wave * kAInstr + i) * 1024, live ? off : kOob);
+            dma_b128(dA, base + (wave * kAInstr + i) * 1024, live && !((a_dead >> i) & 1u) ? off : kOob);
         } else {
             const int i = d - kScaleDma - kAInstr;
             const uint32_t dst = base + kA + (wave * kBInstr + i) * 1024;
