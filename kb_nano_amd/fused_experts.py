@@ -157,8 +157,9 @@ class FusedExperts(nn.Module):
         quant_out = self._get_dg_workspace(2, (M_sum, N), dev, torch.float8_e4m3fn)
         if type(self.silu_mul_quant_fp8) is SiluMulQuantFp8 and not torch.compiler.is_compiling():
             # this package's module: the same launch over the rows with an
-            # expert id only (padding rows hold nothing GEMM1 wrote and GEMM2
-            # never reads; half of config 4's rows), scales column-major as
+            # expert id only (padding rows hold nothing GEMM1 wrote, and
+            # GEMM2 neither stores their output rows nor lets them touch
+            # another row; half of config 4's rows), scales column-major as
             # the module makes them
             a2_fp8 = quant_out
             a2_scale = torch.empty_strided((M_sum, N // _FP8_GROUP_SIZE), (1, M_sum), dtype=torch.float32,
