@@ -280,6 +280,35 @@ def test_grouped_gemm_free_function_colmajor_scales(gpu_device):
     assert_gemm_close(C[torch.from_numpy(valid).to(dev)], ref[valid], "grouped free fn")
 
 
+@pytest.mark.parametrize("K", [1024, 2560])
+@pytest.mark.parametrize("ue8m0", [True, False])
+def test_grouped_gemm_padding_garbage_is_isolated(gpu_device, K, ue8m0):
+    """Padding rows (id -1) may hold anything: FusedExperts leaves them
+    unwritten.  NaN codes and infinite or NaN scales there change no bit of
+    the output, whether the kernel reads those rows as zeros (K <= 2048) or
+    fetches them (longer K); padding output rows stay unwritten."""
+    from kb_nano_amd import _ops
+    E, N = 5, 256
+    ids, qa, sa, qb, sb, M_sum = _grouped_case(E, N, K, M_tok=80, topk=2, seed=21, dev=gpu_device)
+    dev = gpu_device
+    pad = ids < 0
+    assert pad.any()
+    qa2, sa2 = qa.copy(), sa.copy()
+    qa2[pad] = 0x7F                       # e4m3 NaN
+    sa2[pad] = np.float32(np.inf)
+    sa2[np.ix_(pad, np.arange(0, K // 128, 2))] = np.float32(np.nan)
+    B, sB, idt = to_fp8(qb, dev), torch.from_numpy(sb).to(dev), torch.from_numpy(ids).to(dev)
+    outs = []
+    for q_, s_ in ((qa, sa), (qa2, sa2)):
+        C = torch.full((M_sum, N), 7.0, dtype=torch.bfloat16, device=dev)
+        _ops.m_grouped_gemm_nt_contiguous(to_fp8(q_, dev), torch.from_numpy(s_).to(dev), B, sB, C, idt,
+                                          disable_ue8m0_cast=not ue8m0)
+        outs.append(C)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    assert torch.all(outs[1][torch.from_numpy(pad).to(dev)] == 7.0)
+
+
 # ------------------------------------------------- FP32 scale contract
 # disable_ue8m0_cast: the scales' exponents go to the MFMA, their
 # significands are carried per row and the running sum is rescaled when they
