@@ -162,3 +162,20 @@ def test_bf16a_rejects_large_m(gpu_device):
     sW = torch.ones(1, 2, device=gpu_device)
     with pytest.raises(ValueError, match="M=65"):
         _ops.fp8_gemm_bf16a(x, W, sW, torch.empty(65, 128, dtype=torch.bfloat16, device=gpu_device))
+
+
+def test_bf16a_random_shapes(gpu_device):
+    """24 seeded random shapes (M 1..64, ragged N, K up to 16384: data-
+    parallel, split with the sum in the split launch or in the separate
+    reduction), each bit-identical to quant + GEMM."""
+    rng = np.random.default_rng(2024)
+    for case in range(24):
+        M = int(rng.integers(1, 65))
+        N = int(rng.integers(1, 4097))
+        K = 128 * int(rng.integers(1, 129))
+        x = seeded_bf16((M, K), seed=case, outlier_frac=1e-3).to(gpu_device)
+        W, sW = _weights(N, K, seed=case + 100, dev=gpu_device)
+        ref = _quant_then_gemm(x, W, sW)
+        got = _fused(x, W, sW)
+        torch.cuda.synchronize()
+        _assert_same_bits(got, ref, f"case {case}: bf16a {M}x{N}x{K}")
