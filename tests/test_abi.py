@@ -279,9 +279,9 @@ def test_moe_permute_workspace_query():
     assert L.kbn_moe_permute_workspace_bytes(-1, 8) == -1
     # no pairs: counts and offsets only
     assert L.kbn_moe_permute_workspace_bytes(0, 256) == 1024 + 1040
-    # cfg4: 32 chunks x 256 experts of histograms, a rank per pair, counts, offsets
-    assert L.kbn_moe_permute_workspace_bytes(32768, 256) == 32 * 256 * 4 + 32768 * 4 + 1024 + 1040
-    # chunks grow past 256 x 1024 pairs so the scan stays short
+    # cfg4: 64 chunks x 256 experts of histograms, a rank per pair, counts, offsets
+    assert L.kbn_moe_permute_workspace_bytes(32768, 256) == 64 * 256 * 4 + 32768 * 4 + 1024 + 1040
+    # chunks grow past 256 x 512 pairs so the scan stays short
     n = 1 << 20
     assert L.kbn_moe_permute_workspace_bytes(n, 64) == 256 * 64 * 4 + n * 4 + 256 + 272
 
