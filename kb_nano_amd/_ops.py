@@ -299,6 +299,35 @@ def fp8_gemm_bf16a(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Te
         check(rc, what)
 
 
+def flashinfer_blockscale_gemm(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+                               output: torch.Tensor) -> None:
+    """Implementation of the op ``kb_nano_fp8::flashinfer_blockscale_gemm``
+    (reference tasks/baseline/L1/fp8_linear.py:126-153): bf16 activations
+    ``x [M, K]``, fp8 weight ``[N, K]`` with fp32 block scales, bf16
+    ``output [M, N]``, any M.  The reference op uses the weight scales as
+    given; here the scale contract of the GEMM ops decides, as for
+    ``fp8_gemm_nt``:
+
+    * UE8M0 (``is_e8m0_used()``) and M <= 64: ``fp8_gemm_bf16a``, one launch
+      that quantizes the activations itself;
+    * otherwise (scales used as given, or more rows than that kernel's
+      64-row tiles): the 1x128 quant of ``x`` into fresh buffers (UE8M0 scales
+      only under that contract), then ``fp8_gemm_nt`` under the same
+      contract, so non-power-of-two weight scales are never rounded unless
+      the contract says so."""
+    ue8m0 = is_e8m0_used()
+    if x.dim() == 2 and ue8m0 and x.shape[0] <= BF16A_MAX_M:
+        fp8_gemm_bf16a(x, weight, weight_scale, output)
+        return
+    if x.dim() != 2:
+        raise ValueError(f"flashinfer_blockscale_gemm: x must be 2-D, got {tuple(x.shape)}")
+    M, K = x.shape
+    q = torch.empty(M, K, dtype=FP8, device=x.device)
+    s = torch.empty_strided((M, -(-K // GROUP)), (1, max(M, 1)), dtype=torch.float32, device=x.device)
+    per_token_group_quant_fp8(x if x.is_contiguous() else x.contiguous(), q, s, use_ue8m0=ue8m0)
+    fp8_gemm_nt(q, s, weight, weight_scale, output, use_ue8m0=ue8m0)
+
+
 def bf16a_preferred(M: int, N: int, K: int, idx: int) -> bool:
     """Whether ``fp8_gemm_bf16a`` is expected to beat quant + ``fp8_gemm_nt``
     for this shape on device idx (the library's plan-based rule); cached."""
@@ -331,6 +360,22 @@ def _workspace(nbytes: int, idx: int, stream: int, like: torch.Tensor) -> torch.
         buf = torch.empty(nbytes, dtype=torch.uint8, device=like.device)
         _WS_BUFS[key] = buf
     return buf
+
+
+def release_workspaces(device: int | None = None) -> int:
+    """Drop the eager split-K workspaces ``_workspace`` keeps per (device,
+    stream), all of them or those of one device index; returns how many were
+    dropped.  A buffer goes back to torch's caching allocator once no launch
+    still uses it (stream-ordered), so a following ``torch.cuda.empty_cache()``
+    can return it to the device.  Call it when streams are retired (each
+    buffer grows to the largest split plan run on its stream, up to 64 MiB)
+    or before measuring free memory; the next eager split launch on a stream
+    allocates afresh.  Graph-captured launches hold their own buffers and
+    are not affected."""
+    keys = [k for k in _WS_BUFS if device is None or k[0] == device]
+    for k in keys:
+        del _WS_BUFS[k]
+    return len(keys)
 
 
 def _gemm_workspace_bytes(L, idx: int, M, N, K, ue8m0) -> int:
@@ -698,11 +743,13 @@ def _register():
         _fp8_lib.impl("fp8_gemm_nt", lambda q, s, w, ws, o: fp8_gemm_nt(q, s, w, ws, o), "CUDA")
         _fp8_lib.impl("fp8_gemm_nt", _meta_noop, "Meta")
     if not _has_op("kb_nano_fp8", "flashinfer_blockscale_gemm"):
-        # the reference's bf16-input small-M GEMM op (fp8_linear.py:126-153);
-        # here the gfx950 kernel that quantizes its activations itself
+        # the reference's bf16-input GEMM op (fp8_linear.py:126-153): the
+        # gfx950 kernel that quantizes its activations itself where the scale
+        # contract and M allow, else quant + fp8_gemm_nt
         _fp8_lib.define("flashinfer_blockscale_gemm(Tensor input_bf16, Tensor weight_fp8, "
                         "Tensor weight_scale, Tensor! output) -> ()")
-        _fp8_lib.impl("flashinfer_blockscale_gemm", lambda x, w, ws, o: fp8_gemm_bf16a(x, w, ws, o), "CUDA")
+        _fp8_lib.impl("flashinfer_blockscale_gemm", lambda x, w, ws, o: flashinfer_blockscale_gemm(x, w, ws, o),
+                      "CUDA")
         _fp8_lib.impl("flashinfer_blockscale_gemm", _meta_noop, "Meta")
     if not _has_op("kb_nano_fp8", "per_token_group_quant_fp8"):
         _fp8_lib.define("per_token_group_quant_fp8(Tensor input, Tensor! output_fp8, "

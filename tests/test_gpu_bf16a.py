@@ -104,14 +104,19 @@ LLAMA70B = [("qkv", 10240, 8192), ("o", 8192, 8192), ("gate_up", 57344, 8192), (
 @pytest.mark.parametrize("name,N,K", LLAMA70B)
 def test_bf16a_cfg5_full_size(gpu_device, name, N, K):
     """Config 5 (Llama-3.1-70B decode shapes, BASELINE recipe weights) at
-    every M: bit-identical to quant + GEMM."""
+    every M: bit-identical to quant + GEMM, both outputs (prefilled with NaN)
+    entirely written, so a tile both paths skipped cannot pass as equal (the
+    oracle comparison at every tile is test_fp8_linear_cfg5_every_tile)."""
     from kb_nano_amd import synthetic
+    from tests._util import assert_all_written
     W, sW = _weights(N, K, seed=4, dev=gpu_device)
     for M in (1, 8, 32, 64):
         x = synthetic.bf16_normal((M, K), seed=40 + M).to(gpu_device)
         ref = _quant_then_gemm(x, W, sW)
         got = _fused(x, W, sW)
         torch.cuda.synchronize()
+        assert_all_written(ref, f"cfg5 {name} M={M} quant + GEMM")
+        assert_all_written(got, f"cfg5 {name} M={M} bf16a")
         _assert_same_bits(got, ref, f"cfg5 {name} M={M}")
 
 
@@ -179,3 +184,45 @@ def test_bf16a_random_shapes(gpu_device):
         got = _fused(x, W, sW)
         torch.cuda.synchronize()
         _assert_same_bits(got, ref, f"case {case}: bf16a {M}x{N}x{K}")
+
+
+def test_bf16a_op_honours_scale_contract(gpu_device, monkeypatch):
+    """The registered op (reference fp8_linear.py:126-153) under the FP32
+    contract (VLLM_USE_DEEP_GEMM_E8M0=0) with non-power-of-two weight scales
+    uses them as given: equal bit for bit to quant (fp32 scales) + fp8_gemm_nt
+    under that contract, within tolerance of the oracle with the unrounded
+    scales, and not equal to the UE8M0 result.  Under UE8M0 with M = 100
+    (past the fused kernel's 64 rows) it runs quant + GEMM."""
+    from kb_nano_amd import _ops
+    from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
+    M, N, K = 16, 1024, 2048
+    x = seeded_bf16((M, K), seed=31)
+    W, sW = _weights(N, K, seed=32, dev=gpu_device)
+    sW = sW * 1.37
+    xd = x.to(gpu_device)
+    monkeypatch.setattr(_ops, "is_e8m0_used", lambda: False)
+    out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu_device)
+    torch.ops.kb_nano_fp8.flashinfer_blockscale_gemm(xd, W, sW, out)
+    q = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=gpu_device)
+    s = _alloc_colmajor_scale(M, K // 128, gpu_device)
+    _ops.per_token_group_quant_fp8(xd, q, s, use_ue8m0=False)
+    ref = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu_device)
+    _ops.fp8_gemm_nt(q, s, W, sW, ref, use_ue8m0=False)
+    torch.cuda.synchronize()
+    _assert_same_bits(out, ref, "FP32 contract op")
+    qa, sa = oracle.quant_group128(bf16_bits(x), use_ue8m0=False)
+    assert_gemm_close(out, oracle.gemm_nt_sample(qa, sa, fp8_codes(W), sW.cpu().numpy(), ue8m0=False),
+                      "FP32 contract op vs oracle")
+    rounded = _fused(xd, W, sW)
+    torch.cuda.synchronize()
+    assert int((rounded.view(torch.int16) != out.view(torch.int16)).sum()) > N, "contract had no effect"
+
+    monkeypatch.setattr(_ops, "is_e8m0_used", lambda: True)
+    M2 = 100
+    x2 = seeded_bf16((M2, K), seed=33).to(gpu_device)
+    sW2 = sW / 1.37
+    out2 = torch.full((M2, N), float("nan"), dtype=torch.bfloat16, device=gpu_device)
+    torch.ops.kb_nano_fp8.flashinfer_blockscale_gemm(x2, W, sW2, out2)
+    ref2 = _quant_then_gemm(x2, W, sW2)
+    torch.cuda.synchronize()
+    _assert_same_bits(out2, ref2, "UE8M0 op at M=100")

@@ -173,11 +173,18 @@ def test_fused_experts_cfg4_full_size(gpu_device, cfg4):
 @pytest.mark.parametrize("name,N,K", [(n, N, K) for n, N, K in
                                       [("qkv", 10240, 8192), ("o", 8192, 8192), ("gate_up", 57344, 8192),
                                        ("down", 8192, 28672)]])
-def test_fp8_linear_cfg5_full_size(gpu_device, name, N, K):
-    """Fp8Linear.forward (1x128 quant into column-major scales, then the
-    block-scaled GEMM with its split-K workspace) at every config-5 (shape,
-    M) pair, against oracle quant + oracle GEMM on sampled columns."""
-    from kb_nano_amd import Fp8Linear, synthetic
+def test_fp8_linear_cfg5_every_tile(gpu_device, name, N, K):
+    """Config 5 at every (shape, M) through the three entry points a decode
+    step can take: fp8_gemm_nt on the quantized input (with its split-K
+    workspace), Fp8Linear.forward into installed buffers (quant + GEMM, or,
+    where the plan prefers it, the GEMM over bf16 activations), and the
+    bf16-activation GEMM itself.  Each output is prefilled with NaN and must
+    come back entirely written and finite, and each is compared with oracle
+    quant + oracle GEMM at a point inside every 64x128 block (every tile of
+    every plan, split tails included) plus the edge rows and columns."""
+    from kb_nano_amd import Fp8Linear, _ops, synthetic
+    from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
+    from tests._util import assert_all_written, tile_cover
     dev = gpu_device
     print(f"cfg5 {name} N={N} K={K}: drawing the weight", flush=True)
     W, sW = synthetic.dense_weight(N, K, seed=4, device=dev)
@@ -186,10 +193,27 @@ def test_fp8_linear_cfg5_full_size(gpu_device, name, N, K):
     for M in (1, 8, 32, 64):
         print(f"cfg5 {name} M={M}", flush=True)
         x = synthetic.bf16_normal((M, K), seed=40 + M)
-        y = Fp8Linear()(x.to(dev), W, sW)
-        torch.cuda.synchronize()
-        assert y.shape == (M, N) and bool(torch.isfinite(y).all()), f"{name} M={M}"
+        xd = x.to(dev)
+        rows, cols = tile_cover(M, N, rng)
         qa, sa = oracle.quant_group128(bf16_bits(x))
-        cols = _cols(N, rng)
-        ref = oracle.gemm_nt_sample(qa, sa, qw, sw, cols=cols, ue8m0=True)
-        assert_gemm_close(y[:, torch.from_numpy(cols).to(dev)], ref, f"cfg5 {name} M={M}")
+        ref = oracle.gemm_nt_sample(qa, sa, qw, sw, rows=rows, cols=cols, ue8m0=True)
+        rt, ct = torch.from_numpy(rows).to(dev), torch.from_numpy(cols).to(dev)
+
+        q = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=dev)
+        s = _alloc_colmajor_scale(M, K // 128, dev)
+        _ops.per_token_group_quant_fp8(xd, q, s)
+        D = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+        _ops.fp8_gemm_nt(q, s, W, sW, D, use_ue8m0=True)
+
+        lin = Fp8Linear()
+        lin._ensure_buffers(M, K, N, dev)
+        lin._o_buf.fill_(float("nan"))
+        y = lin(xd, W, sW)
+
+        Dx = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+        _ops.fp8_gemm_bf16a(xd, W, sW, Dx)
+        torch.cuda.synchronize()
+        assert y.shape == (M, N) and y.data_ptr() == lin._o_buf.data_ptr()
+        for out, path in ((D, "fp8_gemm_nt"), (y, "Fp8Linear"), (Dx, "fp8_gemm_bf16a")):
+            assert_all_written(out, f"cfg5 {name} M={M} {path}")
+            assert_gemm_close(out[rt][:, ct], ref, f"cfg5 {name} M={M} {path} ({len(rows)} x {len(cols)} points)")

@@ -81,30 +81,34 @@ def test_gemm_single_k_block_special_case(gpu_device):
 @pytest.mark.parametrize("name,N,K", [("q_b_proj", 24576, 1536), ("gate_up", 36864, 7168),
                                       ("down_proj", 7168, 18432), ("o_proj", 7168, 16384)])
 @pytest.mark.parametrize("M", [128, 4096])
-def test_gemm_dsv3_shapes_sampled(gpu_device, name, N, K, M):
+def test_gemm_dsv3_every_tile(gpu_device, name, N, K, M):
     """BASELINE config 3 at full size, inputs drawn on the CPU by the BASELINE
-    recipe (seed 2 for the weights, 20 for the activations); the oracle is
-    evaluated on 48 sampled rows x 96 sampled columns (including the
-    first/last row and column)."""
+    recipe (seed 2 for the weights, 20 for the activations).  The output is
+    prefilled with NaN and must come back entirely written and finite; the
+    oracle is evaluated on a row set x column set that puts a point inside
+    every 64x128 block of the output (so inside every tile of every plan,
+    split-tail tiles included) plus the first and last rows and columns of
+    the edge tiles."""
     from kb_nano_amd import _ops, synthetic
     from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
+    from tests._util import assert_all_written, tile_cover
+    print(f"cfg3 {name} M={M}", flush=True)
     a = synthetic.bf16_normal((M, K), seed=20).to(gpu_device)
     A = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=gpu_device)
     sA = _alloc_colmajor_scale(M, K // 128, gpu_device)
     _ops.per_token_group_quant_fp8(a, A, sA)
     W, sW = synthetic.dense_weight(N, K, seed=2, device=gpu_device)
-    D = torch.empty(M, N, dtype=torch.bfloat16, device=gpu_device)
+    D = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu_device)
     _ops.fp8_gemm_nt(A, sA, W, sW, D, use_ue8m0=True)
     torch.cuda.synchronize()
-    rng = np.random.default_rng(M + N)
-    rows = np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, 46)]))
-    cols = np.unique(np.concatenate([[0, N - 1], rng.integers(0, N, 94)]))
+    assert_all_written(D, f"{name} M={M}")
+    rows, cols = tile_cover(M, N, np.random.default_rng(M + N))
     qa = fp8_codes(A[torch.from_numpy(rows).to(gpu_device)])
     sa = sA[torch.from_numpy(rows).to(gpu_device)].cpu().numpy()
     qw = fp8_codes(W)
     ref = oracle.gemm_nt_sample(qa, sa, qw, sW.cpu().numpy(), cols=cols)
     got = D[torch.from_numpy(rows).to(gpu_device)][:, torch.from_numpy(cols).to(gpu_device)]
-    assert_gemm_close(got, ref, f"{name} M={M}")
+    assert_gemm_close(got, ref, f"{name} M={M} ({len(rows)} x {len(cols)} points)")
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 7168, 18432), (8, 8192, 8192), (64, 1024, 28672), (100, 7168, 16384),
