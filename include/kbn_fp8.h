@@ -368,6 +368,31 @@ int kbn_fp8_block_requant(const void* w_in, int in_f32, const float* s_in, int64
                           int64_t s_out_e, int64_t s_out_ld, int use_ue8m0, float eps, void* stream);
 
 /*
+ * Split-K arrival counters (no counterpart in the reference; DeepGEMM has no
+ * split-K).  The small-M split launches of the 64-row tiles sum their fp32
+ * slabs themselves, counting arrivals in a region of a library-held device
+ * array: one region per eager stream and per (capture, stream) pair, kept
+ * for the life of the process (a captured graph replays with its region).
+ * When a device's regions are all taken, later launches on new streams or
+ * captures run the separate reduction kernel instead: same results, one
+ * launch more; the first such launch also prints one line on stderr.
+ *   regions_used   regions in use on the busiest device
+ *   regions_total  regions per device (1024)
+ *   fallbacks      split launches that found no free region
+ * Any pointer may be NULL.  Host bookkeeping only: callable without a GPU.
+ */
+int kbn_splitk_counter_stats(int64_t* regions_used, int64_t* regions_total, int64_t* fallbacks);
+
+/*
+ * Test hook (no counterpart in the reference): the region bookkeeping above
+ * on a private table, without a GPU.  n_keys distinct eager streams of one
+ * device ask for a region, then the first asks again: out_region[i] gets
+ * stream i's region (-1: none left), out_region[n_keys] the repeated
+ * stream's; *out_fallbacks the table's fallback count.  1 <= n_keys <= 4096.
+ */
+int kbn_debug_splitk_regions(int64_t n_keys, int32_t* out_region, int64_t* out_fallbacks);
+
+/*
  * Test hook (no counterpart in the reference): the kernels' bf16 SiLU
  * applied elementwise to n bf16 bit patterns, for exhaustive checking.
  */

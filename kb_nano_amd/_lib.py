@@ -49,6 +49,8 @@ SIGNATURES = {
     "kbn_fp8_fused_moe_gemm_workspace_bytes": ([_I64, _I64], _I64),
     "kbn_moe_sum": ([_P, _I64, _I64, _I64, _I64, _P, _I64, _P], _I),
     "kbn_fp8_block_requant": ([_P, _I, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I, _F, _P], _I),
+    "kbn_splitk_counter_stats": ([_P, _P, _P], _I),
+    "kbn_debug_splitk_regions": ([_I64, _P, _P], _I),
     "kbn_debug_silu_bf16": ([_P, _P, _I64, _P], _I),
 }
 

@@ -378,6 +378,22 @@ def release_workspaces(device: int | None = None) -> int:
     return len(keys)
 
 
+def splitk_counter_stats() -> dict:
+    """State of the split-K arrival-counter regions (``kbn_splitk_counter_stats``):
+    ``regions_used`` on the busiest device, ``regions_total`` per device and
+    ``fallbacks``, the small-M split launches that ran the separate reduction
+    kernel because every region was taken (one region per eager stream and
+    per captured stream, held for the life of the process).  A non-zero
+    ``fallbacks`` means results as usual but one launch more per such call:
+    an engine that re-captures graphs many times should reuse its graphs
+    instead."""
+    import ctypes
+    used, total, fb = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    check(lib().kbn_splitk_counter_stats(ctypes.byref(used), ctypes.byref(total), ctypes.byref(fb)),
+          "splitk_counter_stats")
+    return {"regions_used": used.value, "regions_total": total.value, "fallbacks": fb.value}
+
+
 def _gemm_workspace_bytes(L, idx: int, M, N, K, ue8m0) -> int:
     """Split-K workspace of a shape on device idx (the plan depends on the
     device's CU count); cached per (device, shape)."""

@@ -8,6 +8,7 @@
 #include "gemm_kernel.h"
 
 #include <algorithm>
+#include <cstdio>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -79,17 +80,44 @@ static void plan_tail(Schedule& s, int64_t M, int KBT) {
 // and eager streams get distinct regions, so concurrent launches never share
 // a counter.  Every launch leaves its counters at zero.  When the regions are
 // used up (or the array's address cannot be had), launches fall back to the
-// separate reduction kernel.
-constexpr int kFlagRegion = 1024;   // tail tiles per launch; a tail is below 2 x CUs tiles
-constexpr int kFlagRegions = 512;
+// separate reduction kernel: the results are the same, each such call costs
+// one more launch (about 3 us of host time).  The fallbacks are counted
+// (kbn_splitk_counter_stats) and the first one is reported once on stderr.
+// A tail of the 64-row tiles (the only ones whose split launch sums its own
+// slabs) has fewer tiles than two workgroups per CU, i.e. at most 512 on a
+// 256-CU device; larger tails never take a region.
+constexpr int kFlagRegion = 512;    // tail tiles per launch
+constexpr int kFlagRegions = 1024;
 constexpr int kFlagDevices = 64;
 __device__ __attribute__((aligned(256))) unsigned g_splitk_flags[kFlagRegions * kFlagRegion];
 
+// Which region each (device, capture id + 1 or 0 for eager launches, stream)
+// key holds.  Host bookkeeping only (no HIP calls), so the CPU tests can
+// drive a private instance through kbn_debug_splitk_regions.
+struct FlagRegionTable {
+    std::map<std::tuple<int, uint64_t, uint64_t>, int> region;
+    int used[kFlagDevices] = {};
+    int64_t fallbacks = 0;
+    // The key's region, a new one if it has none, or -1 (counted) when the
+    // device's regions are all taken.
+    int acquire(int dev, uint64_t cap_key, uint64_t stream) {
+        const auto key = std::make_tuple(dev, cap_key, stream);
+        auto it = region.find(key);
+        if (it != region.end()) return it->second;
+        if (used[dev] >= kFlagRegions) {
+            ++fallbacks;
+            return -1;
+        }
+        region.emplace(key, used[dev]);
+        return used[dev]++;
+    }
+};
+
+static std::mutex g_flag_mu;
+static FlagRegionTable g_flag_table;
+
 unsigned* splitk_flags_for(hipStream_t st, int64_t tail_tiles) {
-    static std::mutex mu;
     static unsigned* base[kFlagDevices] = {};
-    static int used[kFlagDevices] = {};
-    static std::map<std::tuple<int, uint64_t, uint64_t>, int> region;  // (device, capture id or 0, stream)
     if (tail_tiles > kFlagRegion) return nullptr;
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kFlagDevices) return nullptr;
@@ -98,7 +126,7 @@ unsigned* splitk_flags_for(hipStream_t st, int64_t tail_tiles) {
     if (hipStreamGetCaptureInfo(st, &cs, &cid) != hipSuccess) return nullptr;
     if (cs != hipStreamCaptureStatusNone && cs != hipStreamCaptureStatusActive) return nullptr;
     const bool cap = cs == hipStreamCaptureStatusActive;
-    std::lock_guard<std::mutex> lock(mu);
+    std::lock_guard<std::mutex> lock(g_flag_mu);
     if (!base[dev]) {
         if (cap) return nullptr;   // resolved on the first eager launch, not inside a capture
         void* p = nullptr;
@@ -109,14 +137,50 @@ unsigned* splitk_flags_for(hipStream_t st, int64_t tail_tiles) {
         base[dev] = static_cast<unsigned*>(p);
     }
     // eager launches key on 0, captured ones on capture id + 1
-    const auto key = std::make_tuple(dev, cap ? (uint64_t)cid + 1 : (uint64_t)0, (uint64_t)(uintptr_t)st);
-    auto it = region.find(key);
-    if (it == region.end()) {
-        if (used[dev] >= kFlagRegions) return nullptr;
-        it = region.emplace(key, used[dev]++).first;
+    const int r = g_flag_table.acquire(dev, cap ? (uint64_t)cid + 1 : (uint64_t)0, (uint64_t)(uintptr_t)st);
+    if (r < 0) {
+        if (g_flag_table.fallbacks == 1)
+            std::fprintf(stderr,
+                         "kb_nano_amd: all %d split-K counter regions of device %d are taken (one per eager stream "
+                         "and per captured stream); later small-M split launches on new streams or captures use "
+                         "the separate reduction kernel (same results, one launch more)\n",
+                         kFlagRegions, dev);
+        return nullptr;
     }
-    return base[dev] + (int64_t)it->second * kFlagRegion;
+    return base[dev] + (int64_t)r * kFlagRegion;
 }
+
+}  // namespace kbn
+
+// Regions in use on the busiest device, regions per device, and split
+// launches that took the separate reduction because no region was free.
+extern "C" int kbn_splitk_counter_stats(int64_t* regions_used, int64_t* regions_total, int64_t* fallbacks) {
+    using namespace kbn;
+    std::lock_guard<std::mutex> lock(g_flag_mu);
+    int most = 0;
+    for (int d = 0; d < kFlagDevices; ++d) most = std::max(most, g_flag_table.used[d]);
+    if (regions_used) *regions_used = most;
+    if (regions_total) *regions_total = kFlagRegions;
+    if (fallbacks) *fallbacks = g_flag_table.fallbacks;
+    return 0;
+}
+
+// Test hook: n_keys distinct eager streams on device 0 of a fresh region
+// table, then the first key again; out_region[i] gets key i's region (-1:
+// none left) and out_region[n_keys] the repeated key's; *out_fallbacks the
+// table's fallback count.  No HIP calls.
+extern "C" int kbn_debug_splitk_regions(int64_t n_keys, int32_t* out_region, int64_t* out_fallbacks) {
+    using namespace kbn;
+    KBN_CHECK_ARG(n_keys >= 1 && n_keys <= 4 * kFlagRegions && out_region && out_fallbacks,
+                  "debug_splitk_regions: bad arguments");
+    FlagRegionTable t;
+    for (int64_t i = 0; i < n_keys; ++i) out_region[i] = t.acquire(0, 0, 0x1000 + 8 * (uint64_t)i);
+    out_region[n_keys] = t.acquire(0, 0, 0x1000);
+    *out_fallbacks = t.fallbacks;
+    return 0;
+}
+
+namespace kbn {
 
 // Sorted-token layout: the activation scales of every row R below the padded
 // total, gathered into column-major [KB, EM] order (row R of block kb at
@@ -285,16 +349,35 @@ static void* scratch_ptr(const char* what) {
     return ptr[dev];
 }
 
-static int gemm_nt_impl(const char* what, const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
-                        int64_t sA_stride_k, const void* W, int64_t ldw, const float* sW, int64_t sW_ld, void* D_bf16,
-                        int64_t ldd, int64_t M, int64_t N, int64_t K, int scale_ue8m0, void* workspace,
-                        int64_t workspace_bytes, void* stream, bool use_scratch = false) {
+// The checks launch_gemm makes before each launch, made ahead of any launch
+// (kbn_fp8_linear_forward validates its GEMM before it enqueues the quant).
+static int check_plan(const GemmArgs& a, const Schedule& sc, const char* what) {
+    const int64_t tiles = (((int64_t)a.M + sc.bm - 1) / sc.bm) * (((int64_t)a.N + sc.bn - 1) / sc.bn);
+    KBN_CHECK_ARG(tiles == sc.tiles && tiles <= 0x7FFFFFFFLL, "%s: too many tiles", what);
+    if (a.P && sc.splits > 1 && sc.dp_tiles < tiles) {
+        const int64_t need = (int64_t)sc.splits * (tiles - sc.dp_tiles) * sc.bm * sc.bn * 4;
+        KBN_CHECK_ARG(need < 0x7FFFFFFFLL && need <= a.ws_bytes && aligned16(a.P),
+                      "%s: workspace of %lld bytes is smaller than the %lld the split plan writes", what,
+                      (long long)a.ws_bytes, (long long)need);
+        KBN_CHECK_ARG((int64_t)sc.splits * sc.kb_per_split >= a.K / kRowB &&
+                          (int64_t)(sc.splits - 1) * sc.kb_per_split < a.K / kRowB,
+                      "%s: split plan does not cover K in %d non-empty splits", what, sc.splits);
+    }
+    return 0;
+}
+
+// Arguments, tile plan and workspace of a dense GEMM, all validated; nothing
+// is launched.  gemm_nt_launch then enqueues it.
+static int gemm_nt_prepare(const char* what, const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
+                           int64_t sA_stride_k, const void* W, int64_t ldw, const float* sW, int64_t sW_ld,
+                           void* D_bf16, int64_t ldd, int64_t M, int64_t N, int64_t K, int scale_ue8m0,
+                           void* workspace, int64_t workspace_bytes, bool use_scratch, GemmArgs& a, Schedule& sc) {
     if (int rc = check_common(what, A, lda, W, ldw, D_bf16, ldd, M, N, K)) return rc;
+    a = GemmArgs{};
     if (M == 0 || N == 0) return 0;
     KBN_CHECK_ARG(K > 0, "%s: K must be positive", what);
     KBN_CHECK_ARG(sA && sW, "%s: null scale pointer", what);
     KBN_CHECK_ARG(sW_ld >= K / kGroup, "%s: weight-scale row stride %lld < K/128", what, (long long)sW_ld);
-    GemmArgs a{};
     a.A = (const uint8_t*)A; a.lda = lda;
     if (int rc = check_scale_ranges(what, M, K, sA_stride_m, sA_stride_k, (N + kGroup - 1) / kGroup, sW_ld))
         return rc;
@@ -306,7 +389,7 @@ static int gemm_nt_impl(const char* what, const void* A, int64_t lda, const floa
     a.vec_store = (reinterpret_cast<uintptr_t>(D_bf16) % 16 == 0) && (ldd % 8 == 0);
     a.expert_ids = nullptr;
     a.M = (int)M; a.N = (int)N; a.K = (int)K; a.E = 1;
-    Schedule sc = dense_schedule(M, N, K, scale_ue8m0, workspace != nullptr || use_scratch);
+    sc = dense_schedule(M, N, K, scale_ue8m0, workspace != nullptr || use_scratch);
     if (use_scratch && sc.splits > 1) {
         KBN_CHECK_ARG(sc.ws_bytes <= kScratchBytes,
                       "%s: the split plan of M=%lld N=%lld K=%lld needs %lld bytes of scratch, more than the %lld "
@@ -325,8 +408,25 @@ static int gemm_nt_impl(const char* what, const void* A, int64_t lda, const floa
             sc = dense_schedule(M, N, K, scale_ue8m0, false);
         }
     }
+    return check_plan(a, sc, what);
+}
+
+static int gemm_nt_launch(const GemmArgs& a, const Schedule& sc, int scale_ue8m0, void* stream, const char* what) {
+    if (a.M == 0 || a.N == 0) return 0;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    return scale_ue8m0 ? dispatch_dense<true>(a, sc, K, st, what) : dispatch_dense<false>(a, sc, K, st, what);
+    return scale_ue8m0 ? dispatch_dense<true>(a, sc, a.K, st, what) : dispatch_dense<false>(a, sc, a.K, st, what);
+}
+
+static int gemm_nt_impl(const char* what, const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
+                        int64_t sA_stride_k, const void* W, int64_t ldw, const float* sW, int64_t sW_ld, void* D_bf16,
+                        int64_t ldd, int64_t M, int64_t N, int64_t K, int scale_ue8m0, void* workspace,
+                        int64_t workspace_bytes, void* stream, bool use_scratch = false) {
+    GemmArgs a;
+    Schedule sc;
+    if (int rc = gemm_nt_prepare(what, A, lda, sA, sA_stride_m, sA_stride_k, W, ldw, sW, sW_ld, D_bf16, ldd, M, N, K,
+                                 scale_ue8m0, workspace, workspace_bytes, use_scratch, a, sc))
+        return rc;
+    return gemm_nt_launch(a, sc, scale_ue8m0, stream, what);
 }
 
 extern "C" int kbn_fp8_gemm_nt(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
@@ -370,11 +470,15 @@ extern "C" int kbn_fp8_linear_forward(const void* x_bf16, int64_t M, int64_t K, 
     KBN_CHECK_ARG(M <= 0x3FFFFFFFLL, "%s: shape too large", what);
     KBN_CHECK_ARG(sW_ld >= K / kGroup, "%s: weight-scale row stride %lld < K/128", what, (long long)sW_ld);
     if (int rc = check_scale_ranges(what, M, K, s_stride_m, s_stride_g, (N + kGroup - 1) / kGroup, sW_ld)) return rc;
+    GemmArgs a;
+    Schedule sc;
+    if (int rc = gemm_nt_prepare(what, q_fp8, ld_q, scale, s_stride_m, s_stride_g, W, ldw, sW, sW_ld, D_bf16, ldd, M,
+                                 N, K, scale_ue8m0, workspace, workspace_bytes, false, a, sc))
+        return rc;
     if (int rc = kbn_per_token_group_quant_fp8(x_bf16, M, K, ld_x, q_fp8, ld_q, scale, s_stride_m, s_stride_g, eps,
                                                quant_ue8m0, stream))
         return rc;
-    return gemm_nt_impl(what, q_fp8, ld_q, scale, s_stride_m, s_stride_g, W, ldw, sW, sW_ld, D_bf16, ldd, M, N, K,
-                        scale_ue8m0, workspace, workspace_bytes, stream);
+    return gemm_nt_launch(a, sc, scale_ue8m0, stream, what);
 }
 
 extern "C" int64_t kbn_fp8_gemm_bf16a_workspace_bytes(int64_t M, int64_t N, int64_t K) {

@@ -462,3 +462,68 @@ def test_gemm_noalloc_validates_before_touching_a_device():
     assert "multiple of 128" in _err()
     assert L.kbn_fp8_gemm_nt_noalloc(None, 128, None, 1, 1, None, 128, None, 1, None, 128, 0, 128, 128, 1,
                                      None) == 0
+
+
+def test_splitk_counter_regions_exhaust_and_fall_back():
+    """The region table behind the fused split-K sums (no GPU): every new
+    stream takes the next region until all 1024 are taken, later streams get
+    none and are counted as fallbacks (their launches take the separate
+    reduction kernel), and a stream that holds a region keeps it."""
+    import numpy as np
+    from kb_nano_amd._lib import lib
+    L = lib()
+    used, total, fb = ctypes.c_int64(-1), ctypes.c_int64(-1), ctypes.c_int64(-1)
+    assert L.kbn_splitk_counter_stats(ctypes.byref(used), ctypes.byref(total), ctypes.byref(fb)) == 0
+    assert total.value == 1024 and used.value >= 0 and fb.value >= 0
+    for n in (1, 1023, 1024, 1030):
+        out = np.full(n + 1, -7, dtype=np.int32)
+        nfb = ctypes.c_int64(-1)
+        assert L.kbn_debug_splitk_regions(n, out.ctypes.data, ctypes.byref(nfb)) == 0, _err()
+        k = min(n, 1024)
+        assert np.array_equal(out[:k], np.arange(k)), n
+        assert np.all(out[k:n] == -1), n
+        assert out[n] == 0, "a stream keeps its region"
+        assert nfb.value == n - k
+    assert L.kbn_debug_splitk_regions(0, None, None) == 1
+    from kb_nano_amd import _ops
+    st = _ops.splitk_counter_stats()
+    assert st["regions_total"] == 1024 and st["fallbacks"] == fb.value
+
+
+def test_fused_experts_direct_silu_call_respects_hooks():
+    """The experts layer launches its SiLU*Mul+quant kernel directly only
+    when no forward hook would see the reference's module call."""
+    from torch import nn
+
+    from kb_nano_amd.fused_experts import _direct_call_ok
+    from kb_nano_amd.silu_mul_quant_fp8 import SiluMulQuantFp8
+    m = SiluMulQuantFp8()
+    assert _direct_call_ok(m)
+    h = m.register_forward_hook(lambda *a: None)
+    assert not _direct_call_ok(m)
+    h.remove()
+    h = m.register_forward_pre_hook(lambda *a: None)
+    assert not _direct_call_ok(m)
+    h.remove()
+    h = nn.modules.module.register_module_forward_hook(lambda *a: None)
+    assert not _direct_call_ok(m)
+    h.remove()
+    assert _direct_call_ok(m)
+
+    class Other(SiluMulQuantFp8):
+        pass
+    assert not _direct_call_ok(Other())
+
+
+def test_release_workspaces_drops_cached_buffers():
+    from kb_nano_amd import _ops
+    saved = dict(_ops._WS_BUFS)
+    try:
+        _ops._WS_BUFS.clear()
+        _ops._WS_BUFS[(0, 1)] = torch.empty(4, dtype=torch.uint8)
+        _ops._WS_BUFS[(1, 1)] = torch.empty(4, dtype=torch.uint8)
+        assert _ops.release_workspaces(device=1) == 1 and list(_ops._WS_BUFS) == [(0, 1)]
+        assert _ops.release_workspaces() == 1 and not _ops._WS_BUFS
+    finally:
+        _ops._WS_BUFS.clear()
+        _ops._WS_BUFS.update(saved)

@@ -26,6 +26,58 @@ def _call(L, fn, A, sA, W, sW, D, M, N, K, ws=None):
     assert rc == 0, L.kbn_last_error().decode()
 
 
+def _inputs(M, N, K, dev, seed):
+    from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
+    qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=seed)
+    A = to_fp8(qa, dev)
+    sA = _alloc_colmajor_scale(M, K // 128, dev)
+    sA.copy_(torch.from_numpy(sa))
+    return qa, sa, qw, sw, A, sA, to_fp8(qw, dev), torch.from_numpy(sw).to(dev)
+
+
+def test_gemm_noalloc_under_graph_capture(gpu_device):
+    """Collected first in this file, so in a fresh process (and after the
+    other test files, which never call this entry point) the scratch address
+    is looked up inside the capture.  Two split plans (summed in the split
+    launch, M = 8; by the separate reduction, M = 64) captured into one graph
+    and replayed four times with eager work in between: every replay equals
+    the workspace entry point's eager result bit for bit."""
+    from kb_nano_amd._lib import lib
+    L = lib()
+    cases = []
+    for M, N, K in ((8, 8192, 8192), (64, 10240, 8192)):
+        qa, sa, qw, sw, A, sA, W, sW = _inputs(M, N, K, gpu_device, seed=M + 11)
+        ws = torch.empty(L.kbn_fp8_gemm_nt_workspace_bytes(M, N, K, 1), dtype=torch.uint8, device=gpu_device)
+        ref = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu_device)
+        _call(L, L.kbn_fp8_gemm_nt_ws, A, sA, W, sW, ref, M, N, K, ws)
+        out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu_device)
+        cases.append((M, N, K, A, sA, W, sW, ref, out))
+    torch.cuda.synchronize()
+    print("noalloc GEMM: capturing two split plans", flush=True)
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            for M, N, K, A, sA, W, sW, ref, out in cases:
+                _call(L, L.kbn_fp8_gemm_nt_noalloc, A, sA, W, sW, out, M, N, K)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        for c in cases:
+            c[8].fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for M, N, K, A, sA, W, sW, ref, out in cases:
+            assert np.array_equal(bf16_bits(out), bf16_bits(ref)), f"replay {rep}: noalloc graph != ws at M={M}"
+        # eager calls of the same entry point between replays share the scratch
+        M, N, K, A, sA, W, sW, ref, _ = cases[1]
+        tmp = torch.empty(M, N, dtype=torch.bfloat16, device=gpu_device)
+        _call(L, L.kbn_fp8_gemm_nt_noalloc, A, sA, W, sW, tmp, M, N, K)
+        torch.cuda.synchronize()
+        assert np.array_equal(bf16_bits(tmp), bf16_bits(ref)), f"eager noalloc after replay {rep}"
+
+
 def test_gemm_noalloc_matches_workspace_entry_point(gpu_device):
     from kb_nano_amd._lib import lib
     from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
