@@ -89,13 +89,6 @@ def _quant_weight(w, torch):
     return _block_requant(w, use_ue8m0=True, eps=1e-10)
 
 
-def _rand_weight(N, K, gen, dev, torch):
-    w = torch.randn(N, K, generator=gen, device=dev) * 0.02
-    q, s = _quant_weight(w, torch)
-    del w
-    return q, s
-
-
 def _quant_act(a, torch):
     from kb_nano_amd import _ops
     from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
@@ -119,16 +112,99 @@ def bench_silu(steps, warmup, dev):
     s = torch.empty(Nh // 128, M, dtype=torch.float32, device=dev).t()
     nbytes = M * 2 * Nh * 2 + M * Nh + 4 * M * (Nh // 128)
     ms = _events_time_ms(lambda i: _ops.silu_mul_quant_fp8(x, q, s), steps, warmup, min_window_ms=0.0)
-    return {"ms": ms, "bytes": nbytes, "gbs": nbytes / (ms * 1e-3) / 1e9}
+    return {"ms": ms, "bytes": nbytes, "gbs": nbytes / (ms * 1e-3) / 1e9, "_bufs": (x, q, s)}
+
+
+def _bench_lib():
+    import ctypes
+
+    from kb_nano_amd._build import BENCH_LIB_PATH
+    if not os.path.exists(BENCH_LIB_PATH):
+        raise RuntimeError(f"{BENCH_LIB_PATH} missing: run __graft_entry__.build() first")
+    L = ctypes.CDLL(BENCH_LIB_PATH)
+    P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    L.kbnb_linear_read.argtypes = [P, I64, P, I, P]
+    L.kbnb_linear_mix.argtypes = [P, I64, P, I, P]
+    L.kbnb_group_pattern.argtypes = [I, P, I64, I64, I64, I64, P, I64, P, I64, I64, P]
+    L.kbnb_row_pattern.argtypes = [I, P, I64, I64, I64, I64, P, I64, P, I64, I64, I, P]
+    return L
+
+
+def bench_stream_ceiling(steps, warmup, dev, silu_bufs, silu_ms):
+    """What the same bytes move at on this box without the arithmetic
+    (libkbn_bench.so, bench_csrc/stream_probe.hip), beside the quant rows:
+      linear_read      the config-2 input (604 MB) read once, linear
+      linear_mix_4to1  that input read and a quarter of it written (151 MB), linear
+      silu_pattern     config 2's loads and stores exactly as the SiLU*Mul+quant
+                       kernel issues them (same grid, XCD slices and walk), the
+                       codes a fold of the loaded words
+      silu_rows_1wg / _2wg  the same bytes with whole rows streamed per workgroup
+                       (one or two 768-lane workgroups per CU)
+      quant_pattern    the 1x128 quant kernel's pattern at 4096 x 18432, rotated
+                       over the same copies as its row
+    GB/s count config 2's (or the quant row's) algorithmic bytes, so each is
+    directly the ceiling of the product kernel's figure."""
+    import torch
+    L = _bench_lib()
+    x, q, s = silu_bufs
+    M, N2 = x.shape
+    Nh = N2 // 2
+    G = Nh // 128
+    st = torch.cuda.current_stream().cuda_stream
+    grid = 2 * torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    algo = M * N2 * 2 + M * Nh + 4 * M * G
+
+    def run(fn):
+        def call(i):
+            rc = fn()
+            if rc:
+                raise RuntimeError(f"stream probe rejected its arguments ({rc})")
+        return _events_time_ms(call, steps, warmup, min_window_ms=0.0)
+
+    res = {"cfg2_algorithmic_bytes": algo}
+    in_bytes = x.numel() * 2
+    ms = run(lambda: L.kbnb_linear_read(x.data_ptr(), in_bytes, sink.data_ptr(), grid, st))
+    res["linear_read"] = {"bytes": in_bytes, "us": ms * 1e3, "GB/s": in_bytes / ms / 1e6}
+    ms = run(lambda: L.kbnb_linear_mix(x.data_ptr(), in_bytes, q.data_ptr(), grid, st))
+    mix = in_bytes + in_bytes // 4
+    res["linear_mix_4to1"] = {"bytes": mix, "us": ms * 1e3, "GB/s": mix / ms / 1e6}
+    ms = run(lambda: L.kbnb_group_pattern(1, x.data_ptr(), M, G, N2, Nh, q.data_ptr(), Nh, s.data_ptr(), 1, M, st))
+    res["silu_pattern"] = {"us": ms * 1e3, "GB/s": algo / ms / 1e6, "frac_hbm": algo / ms / 1e6 / HBM_PEAK_GBS,
+                           "kernel_over_pattern": silu_ms / ms}
+    for per_cu in (1, 2):
+        ms = run(lambda: L.kbnb_row_pattern(1, x.data_ptr(), M, G, N2, Nh, q.data_ptr(), Nh, s.data_ptr(), 1, M,
+                                            per_cu, st))
+        res[f"silu_rows_{per_cu}wg"] = {"us": ms * 1e3, "GB/s": algo / ms / 1e6,
+                                        "frac_hbm": algo / ms / 1e6 / HBM_PEAK_GBS}
+    Mq, Kq = 4096, 18432
+    qbytes = Mq * Kq * 3 + 4 * Mq * (Kq // 128)
+    n = _copies_for(qbytes, 2)
+    xq = [x.view(-1)[:Mq * Kq].view(Mq, Kq).clone() for _ in range(n)]
+    qq = [torch.empty(Mq, Kq, dtype=torch.float8_e4m3fn, device=dev) for _ in range(n)]
+    sq = [torch.empty(Kq // 128, Mq, device=dev).t() for _ in range(n)]
+
+    def qcall(i):
+        rc = L.kbnb_group_pattern(0, xq[i % n].data_ptr(), Mq, Kq // 128, Kq, 0, qq[i % n].data_ptr(), Kq,
+                                  sq[i % n].data_ptr(), 1, Mq, st)
+        if rc:
+            raise RuntimeError(f"stream probe rejected its arguments ({rc})")
+    ms = _events_time_ms(qcall, steps, warmup)
+    res["quant_pattern_4096x18432"] = {"us": ms * 1e3, "GB/s": qbytes / ms / 1e6,
+                                       "frac_hbm": qbytes / ms / 1e6 / HBM_PEAK_GBS, "rotated_copies": n}
+    del xq, qq, sq
+    torch.cuda.empty_cache()
+    return res
 
 
 def bench_quant(steps, warmup, dev, M=4096, K=18432):
     import torch
     from kb_nano_amd import _ops
+    from kb_nano_amd import synthetic
     nbytes = M * K * 2 + M * K + 4 * M * (K // 128)
     n = _copies_for(nbytes, 2)
-    gen = torch.Generator(device=dev).manual_seed(3)
-    xs = [torch.randn(M, K, generator=gen, device=dev).bfloat16() for _ in range(n)]
+    x0 = synthetic.bf16_normal((M, K), seed=3).to(dev)       # BASELINE recipe: CPU generator, bf16 copied over
+    xs = [x0] + [x0.clone() for _ in range(n - 1)]
     qs = [torch.empty(M, K, dtype=torch.float8_e4m3fn, device=dev) for _ in range(n)]
     ss = [torch.empty(K // 128, M, device=dev).t() for _ in range(n)]
     ms = _events_time_ms(lambda i: _ops.per_token_group_quant_fp8(xs[i % n], qs[i % n], ss[i % n]), steps, warmup)
@@ -142,17 +218,22 @@ def bench_norm(steps, warmup, dev, H=7168):
     and the scales (the weight vector stays in L2)."""
     import torch
     from kb_nano_amd import _ops
+    from kb_nano_amd import synthetic
     out = []
-    gen = torch.Generator(device=dev).manual_seed(11)
-    w = torch.randn(H, generator=gen, device=dev).bfloat16()
+    w = synthetic.bf16_normal((H,), seed=11).to(dev)           # BASELINE recipe: CPU generators
     G = -(-H // 128)
     for M in (4096, 128):
         for add in (False, True):
             per_row = H * (2 + 1) + 4 * G + (3 * 2 * H if add else 0)   # fused: reads r, writes r and x
             nbytes = M * per_row
             n = _copies_for(nbytes, 2)
-            xs = [torch.randn(M, H, generator=gen, device=dev).bfloat16() for _ in range(n)]
-            rs = [torch.randn(M, H, generator=gen, device=dev).bfloat16() for _ in range(n)] if add else None
+            x0 = synthetic.bf16_normal((M, H), seed=12).to(dev)
+            xs = [x0] + [x0.clone() for _ in range(n - 1)]
+            if add:
+                r0 = synthetic.bf16_normal((M, H), seed=13).to(dev)
+                rs = [r0] + [r0.clone() for _ in range(n - 1)]
+            else:
+                rs = None
             qs = [torch.empty(M, H, dtype=torch.float8_e4m3fn, device=dev) for _ in range(n)]
             ss = [torch.empty(G, M, device=dev).t() for _ in range(n)]
             fn = (lambda i: _ops.rmsnorm_fp8_quant(qs[i % n], ss[i % n], xs[i % n], w, 1e-6, residual=rs[i % n])) \
@@ -170,12 +251,8 @@ def bench_requant(steps, warmup, dev, E=32, N=4096, K=7168):
     gate_up shape, E experts in one launch): algorithmic bytes = the fp8
     codes read and written plus the block scales read and written."""
     import torch
-    from kb_nano_amd import postprocess_fp8_weights_batched
-    gen = torch.Generator(device=dev).manual_seed(13)
-    W = torch.empty(E, N, K, dtype=torch.float8_e4m3fn, device=dev)
-    sW = torch.empty(E, N // 128, K // 128, device=dev)
-    for e in range(E):
-        W[e], sW[e] = _rand_weight(N, K, gen, dev, torch)
+    from kb_nano_amd import postprocess_fp8_weights_batched, synthetic
+    W, sW = synthetic.expert_weights(E, N, K, seed=13, device=dev)   # BASELINE recipe: CPU generators
     nbytes = 2 * E * N * K + 8 * E * (N // 128) * (K // 128)
     ms = _events_time_ms(lambda i: postprocess_fp8_weights_batched(W, sW), steps, warmup)
     gbs = nbytes / (ms * 1e-3) / 1e9
@@ -184,34 +261,52 @@ def bench_requant(steps, warmup, dev, E=32, N=4096, K=7168):
     return {"E": E, "N": N, "K": K, "us": ms * 1e3, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
 
 
-def _gemm_case(name, M, N, K, steps, warmup, dev, seed, act_seed):
+def _gemm_case(name, M, N, K, steps, warmup, dev, seed, act_seed, vendor=False):
     """One dense GEMM shape, inputs by the BASELINE recipe (CPU generators:
-    the weight from `seed`, the activations from `act_seed`); HBM-bound
-    shapes rotate over copies of the weight that exceed the Infinity Cache."""
+    the weight from `seed`, the activations from `act_seed`).  Every shape
+    rotates over copies of its inputs (weight and activations) that together
+    exceed twice the Infinity Cache, so no call finds its operands left in
+    the MALL by the previous one.  With `vendor`, the same fp8 codes also go
+    through hipBLASLt's fp8 GEMM (torch._scaled_mm, per-tensor scales of 1:
+    no block scales) on the same rotation, as a same-box reference point."""
     import torch
     from kb_nano_amd import _ops, synthetic
     w_bytes = N * K + 4 * (-(-N // 128)) * (K // 128)
     a_bytes = M * K + 4 * M * (K // 128)
     nbytes = w_bytes + a_bytes + 2 * M * N
-    n = _copies_for(nbytes) if M <= 256 else 1
+    n = _copies_for(w_bytes + a_bytes)
     w0, s0 = synthetic.dense_weight(N, K, seed=seed, device=dev)
     Ws = [(w0, s0)] + [(w0.clone(), s0.clone()) for _ in range(n - 1)]
     del w0, s0
-    A, sA = _quant_act(synthetic.bf16_normal((M, K), seed=act_seed).to(dev), torch)
+    A0, sA0 = _quant_act(synthetic.bf16_normal((M, K), seed=act_seed).to(dev), torch)
+    As = [(A0, sA0)] + [(A0.clone(), sA0.clone()) for _ in range(n - 1)]
+    del A0, sA0
     D = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-    ms = _events_time_ms(lambda i: _ops.fp8_gemm_nt(A, sA, Ws[i % n][0], Ws[i % n][1], D, use_ue8m0=True),
+    ms = _events_time_ms(lambda i: _ops.fp8_gemm_nt(As[i % n][0], As[i % n][1], Ws[i % n][0], Ws[i % n][1], D,
+                                                    use_ue8m0=True),
                          steps, warmup, min_warm_ms=WARM_MS)
     flop = 2.0 * M * N * K
     t = ms * 1e-3
     tflops = flop / t / 1e12
     gbs = nbytes / t / 1e9
     roof = max(flop / (FP8_PEAK_TFLOPS * 1e12), nbytes / (HBM_PEAK_GBS * 1e9))
-    del Ws, A, sA, D
+    row = {"name": name, "M": M, "N": N, "K": K, "us": ms * 1e3, "TFLOPS": tflops,
+           "frac_mfma": tflops / FP8_PEAK_TFLOPS, "GB/s": gbs, "frac_roof": roof / t,
+           "bound": "mfma" if flop / (FP8_PEAK_TFLOPS * 1e12) > nbytes / (HBM_PEAK_GBS * 1e9) else "hbm",
+           "rotated_copies": n}
+    if vendor:
+        one = torch.ones((), dtype=torch.float32, device=dev)
+        try:
+            vms = _events_time_ms(lambda i: torch._scaled_mm(As[i % n][0], Ws[i % n][0].t(), scale_a=one, scale_b=one,
+                                                             out_dtype=torch.bfloat16),
+                                  steps, warmup, min_warm_ms=WARM_MS)
+            row["vendor_hipblaslt_per_tensor"] = {"us": vms * 1e3, "TFLOPS": flop / (vms * 1e-3) / 1e12,
+                                                  "frac_mfma": flop / (vms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS}
+        except (RuntimeError, TypeError) as e:   # reported, not fatal: the row is a reference point
+            row["vendor_hipblaslt_per_tensor"] = {"error": str(e)[:200]}
+    del Ws, As, D
     torch.cuda.empty_cache()
-    return {"name": name, "M": M, "N": N, "K": K, "us": ms * 1e3, "TFLOPS": tflops,
-            "frac_mfma": tflops / FP8_PEAK_TFLOPS, "GB/s": gbs, "frac_roof": roof / t,
-            "bound": "mfma" if flop / (FP8_PEAK_TFLOPS * 1e12) > nbytes / (HBM_PEAK_GBS * 1e9) else "hbm",
-            "rotated_copies": n}
+    return row
 
 
 DSV3 = [("q_b_proj", 24576, 1536), ("gate_up", 36864, 7168), ("down_proj", 7168, 18432), ("o_proj", 7168, 16384)]
@@ -222,7 +317,7 @@ def bench_dsv3(steps, warmup, dev):
     out = []
     for M in (4096, 128):
         for name, N, K in DSV3:
-            out.append(_gemm_case(name, M, N, K, steps, warmup, dev, seed=2, act_seed=20))
+            out.append(_gemm_case(name, M, N, K, steps, warmup, dev, seed=2, act_seed=20, vendor=M == 4096))
     return out
 
 
@@ -234,6 +329,26 @@ def bench_decode(steps, warmup, dev):
     return out
 
 
+def _runner_median_us(module, *inputs, warmup=10, runs=100):
+    """kb_nano's kernel-runner timing (bench/kernels/runner.py:160-193): under
+    no_grad, `warmup` calls, a synchronize, then per call perf_counter around
+    forward + torch.cuda.synchronize(); the median (element len // 2 of the
+    sorted times), in microseconds."""
+    import torch
+    with torch.no_grad():
+        for _ in range(warmup):
+            module(*inputs)
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            module(*inputs)
+            torch.cuda.synchronize()
+            times.append((time.perf_counter() - t0) * 1e6)
+    times.sort()
+    return times[len(times) // 2]
+
+
 def bench_linear(steps, warmup, dev):
     """Fp8Linear.forward end to end (1x128 quant + block-scaled GEMM, or for
     small M the GEMM that quantizes its bf16 input itself where that is
@@ -243,6 +358,10 @@ def bench_linear(steps, warmup, dev):
       eager_us       GPU time per call of back-to-back eager calls (events)
       eager_host_us  host time per eager call (launch path, no synchronisation)
       graph_us       time per call replayed from a captured HIP graph
+      runner_median_us  the reference runner's own measure (runner.py:160-193):
+                     a fresh module (no installed buffers) under no_grad, one
+                     weight, perf_counter around each forward plus a device
+                     synchronize, median of 100 calls after 10 warm-up calls
     The config-5 weights (84 / 67 MB) rotate over copies that exceed the 256 MB
     Infinity Cache; the output buffers are installed so a graph's output
     stays put (the reference's decode buffers)."""
@@ -287,8 +406,9 @@ def bench_linear(steps, warmup, dev):
                 lins[i % n](x, *ws[i % n])
         ms_graph = _events_time_ms(lambda i: g.replay(), max(2, steps // 2), warmup) / per_graph
         del g
+        runner_us = _runner_median_us(Fp8Linear(), x, *ws[0])
         out.append({"case": name, "M": M, "N": N, "K": K, "eager_us": ms_eager * 1e3, "eager_host_us": host_us,
-                    "graph_us": ms_graph * 1e3, "rotated_copies": n})
+                    "graph_us": ms_graph * 1e3, "runner_median_us": runner_us, "rotated_copies": n})
     del weights
     torch.cuda.empty_cache()
     return out
@@ -594,7 +714,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default="all",
-                    help="comma list of extra sections: quant,norm,requant,linear,dsv3,moe,moe_sorted,decode (default all; 'none' = headline only)")
+                    help="comma list of extra sections: stream,quant,norm,requant,linear,dsv3,moe,moe_sorted,decode "
+                         "(default all; 'none' = headline only)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three 1 GiB device copies (reference for rocprofv3 byte counters)")
@@ -617,15 +738,22 @@ def main():
     from kb_nano_amd._lib import require_gfx950
     require_gfx950(0)
 
-    sections = {"quant", "norm", "requant", "linear", "dsv3", "moe", "moe_sorted", "decode"} if args.only == "all" else \
+    sections = {"stream", "quant", "norm", "requant", "linear", "dsv3", "moe", "moe_sorted", "decode"} \
+        if args.only == "all" else \
         set() if args.only == "none" else set(args.only.split(","))
 
     torch.cuda.synchronize()
     head = bench_silu(args.steps, args.warmup, dev)
+    silu_bufs = head.pop("_bufs")
     print(f"[bench] silu_mul_quant cfg2: {head['ms'] * 1e3:.1f} us/launch, {head['gbs']:.0f} GB/s", file=sys.stderr,
           flush=True)
     extra = {}
     small = dict(steps=max(5, args.steps // 2), warmup=max(2, args.warmup // 2), dev=dev)
+    if "stream" in sections:
+        extra["stream_ceiling"] = bench_stream_ceiling(silu_bufs=silu_bufs, silu_ms=head["ms"], **small)
+        print(f"[bench] stream ceiling: {extra['stream_ceiling']}", file=sys.stderr, flush=True)
+    del silu_bufs
+    torch.cuda.empty_cache()
     if "quant" in sections:
         extra["quant_cfg_4096x18432"] = bench_quant(**small)
         print(f"[bench] quant: {extra['quant_cfg_4096x18432']}", file=sys.stderr, flush=True)

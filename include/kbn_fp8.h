@@ -121,6 +121,29 @@ int kbn_fp8_gemm_nt_ws(const void* A, int64_t lda, const float* sA, int64_t sA_s
                        int scale_ue8m0, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * kbn_fp8_gemm_nt_ws with DeepGEMM's packed per-row UE8M0 weight scales, the
+ * layout transform_sf_into_required_layout gives postprocess_fp8_weights
+ * (tasks/baseline/L1/fp8_linear.py:501-510) and the layout of the
+ * reference's own fp8_linear benchmark scenarios (weight_scale_inv int32
+ * [N, ceil(K/512)], bench/kernels/benchmark_scenarios/small/
+ * shape_registry.yaml:18719-18737).
+ *   sW_packed  int32 [N, ceil(K/512)] at sW_packed[n*sWp_stride_n + i*sWp_stride_k]
+ *              (any strides, e.g. DeepGEMM's MN-major (1, aligned N)); byte j
+ *              (little-endian) of word (n, i) is the E8M0 exponent e of weight
+ *              row n for K block 4i + j, i.e. the scale 2^(e-127)
+ *   D[m,n] = bf16_rne( sum_kb ue8m0(sA[m,kb]) * 2^(e(n,kb)-127) * sum_{k in kb} A[m,k] * W[n,k] )
+ * The exponents go to the block-scaled MFMA per lane (one weight row per
+ * lane), so with the exponents of 128x128 block scales repeated on every row
+ * of their block the result is kbn_fp8_gemm_nt_ws's with those block scales
+ * (scale_ue8m0 = 1), bit for bit.  Workspace as kbn_fp8_gemm_nt_ws's, sized by
+ * kbn_fp8_gemm_nt_workspace_bytes(M, N, K, 1).
+ */
+int kbn_fp8_gemm_nt_packed_ws(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m, int64_t sA_stride_k,
+                              const void* W, int64_t ldw, const int32_t* sW_packed, int64_t sWp_stride_n,
+                              int64_t sWp_stride_k, void* D_bf16, int64_t ldd, int64_t M, int64_t N, int64_t K,
+                              void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Fp8Linear.forward's quant + GEMM in one call (tasks/baseline/L1/
  * fp8_linear.py:436-445: per_token_group_quant_fp8 into column-major scales,
  * then fp8_gemm_nt): kbn_per_token_group_quant_fp8(x -> q, scale; eps,

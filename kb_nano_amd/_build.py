@@ -72,8 +72,29 @@ def _compile(src: str, hipcc: str) -> str:
     return obj
 
 
+BENCH_CSRC = os.path.join(HERE, "bench_csrc")
+BENCH_LIB_PATH = os.path.join(HERE, "libkbn_bench.so")
+
+
+def build_bench(hipcc: str | None = None) -> str:
+    """Compile ``bench_csrc/*.hip`` (bench.py's streaming probes, not part of
+    the operator library) into ``libkbn_bench.so``; returns its path."""
+    hipcc = hipcc or _hipcc()
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    sources = sorted(glob.glob(os.path.join(BENCH_CSRC, "*.hip")))
+    objs = [_compile(s, hipcc) for s in sources]
+    tmp = BENCH_LIB_PATH + ".tmp"
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, BENCH_LIB_PATH)
+    return BENCH_LIB_PATH
+
+
 def build(verbose: bool = False) -> str:
-    """Compile all HIP sources and link ``libkbn_fp8.so``; returns its path."""
+    """Compile all HIP sources and link ``libkbn_fp8.so`` (and bench.py's
+    ``libkbn_bench.so``); returns the operator library's path."""
     hipcc = _hipcc()
     os.makedirs(OBJ_DIR, exist_ok=True)
     _generate_silu_lut()
@@ -88,8 +109,9 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB_PATH)
+    build_bench(hipcc)
     if verbose:
-        print(f"built {LIB_PATH} from {len(sources)} sources", file=sys.stderr)
+        print(f"built {LIB_PATH} from {len(sources)} sources, and {BENCH_LIB_PATH}", file=sys.stderr)
     return LIB_PATH
 
 

@@ -28,6 +28,8 @@ SIGNATURES = {
     "kbn_fp8_gemm_nt_workspace_bytes": ([_I64, _I64, _I64, _I], _I64),
     "kbn_fp8_gemm_nt_ws": (
         [_P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P], _I),
+    "kbn_fp8_gemm_nt_packed_ws": (
+        [_P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P], _I),
     "kbn_fp8_linear_forward": ([_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _F, _I, _P, _I64, _P, _I64, _P,
                                 _I64, _I64, _I, _P, _I64, _P], _I),
     "kbn_fp8_gemm_bf16a_workspace_bytes": ([_I64, _I64, _I64], _I64),

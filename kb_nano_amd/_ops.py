@@ -157,8 +157,16 @@ def silu_mul_quant_fp8(inp: torch.Tensor, out_fp8: torch.Tensor, out_scale: torc
 
 def fp8_gemm_nt(q_input: torch.Tensor, input_scale: torch.Tensor, weight: torch.Tensor,
                 weight_scale: torch.Tensor, output: torch.Tensor, use_ue8m0: bool | None = None) -> None:
-    """output[M,N] (bf16) = block-scaled q_input[M,K] x weight[N,K]^T."""
+    """output[M,N] (bf16) = block-scaled q_input[M,K] x weight[N,K]^T.
+
+    ``weight_scale`` is fp32 [ceil(N/128), ceil(K/128)] block scales, or
+    DeepGEMM's packed per-row UE8M0 exponents, int32 [N, ceil(K/512)] (any
+    strides), the layout postprocess_fp8_weights hands the reference's GEMM
+    (tasks/baseline/L1/fp8_linear.py:501-510); those are UE8M0 by nature."""
     what = "fp8_gemm_nt"
+    if weight_scale.dtype is torch.int32:
+        _fp8_gemm_nt_packed(q_input, input_scale, weight, weight_scale, output)
+        return
     idx = q_input.get_device()
     if (idx not in _GFX950_DEVICES or idx != _cur_device() or input_scale.get_device() != idx
             or weight.get_device() != idx or weight_scale.get_device() != idx or output.get_device() != idx):
@@ -202,6 +210,67 @@ def fp8_gemm_nt(q_input: torch.Tensor, input_scale: torch.Tensor, weight: torch.
         ws.data_ptr() if ws is not None else None, ws_bytes, st)
     if rc:
         check(rc, what)
+
+
+def _fp8_gemm_nt_packed(q_input, input_scale, weight, weight_scale, output) -> None:
+    """fp8_gemm_nt with packed per-row UE8M0 weight scales (kbn_fp8_gemm_nt_packed_ws)."""
+    what = "fp8_gemm_nt"
+    idx = _dev_check(what, q_input, input_scale, weight, weight_scale, output)
+    _dtype_check(what, q_input, FP8, "q_input")
+    _dtype_check(what, weight, FP8, "weight")
+    _dtype_check(what, input_scale, torch.float32, "input_scale")
+    _dtype_check(what, output, torch.bfloat16, "output")
+    M, K = q_input.shape
+    N, K2 = weight.shape
+    if K2 != K or output.shape != (M, N):
+        raise ValueError(f"{what}: shapes q {tuple(q_input.shape)}, W {tuple(weight.shape)}, out {tuple(output.shape)}")
+    KB, words = -(-K // GROUP), -(-K // (4 * GROUP))
+    if input_scale.shape != (M, KB):
+        raise ValueError(f"{what}: input_scale must be {(M, KB)}, got {tuple(input_scale.shape)}")
+    if weight_scale.dim() != 2 or weight_scale.shape[0] < N or weight_scale.shape[1] < words:
+        raise ValueError(f"{what}: packed int32 weight_scale must be at least {(N, words)} "
+                         f"(N, ceil(K/512)), got {tuple(weight_scale.shape)}")
+    qs, ss, ws_, os_ = q_input.stride(), input_scale.stride(), weight.stride(), output.stride()
+    if qs[1] != 1 or ws_[1] != 1 or os_[1] != 1:
+        raise ValueError(f"{what}: operands must be contiguous along K (and N for the output)")
+    if M == 0 or N == 0:
+        return
+    L = lib()
+    ws_bytes = _gemm_workspace_bytes(L, idx, M, N, K, True)
+    st = _raw_stream(idx)
+    ws = _workspace(ws_bytes, idx, st, output) if ws_bytes else None
+    wss = weight_scale.stride()
+    check(L.kbn_fp8_gemm_nt_packed_ws(
+        q_input.data_ptr(), qs[0], input_scale.data_ptr(), ss[0], ss[1], weight.data_ptr(), ws_[0],
+        weight_scale.data_ptr(), wss[0], wss[1], output.data_ptr(), os_[0], M, N, K,
+        ws.data_ptr() if ws is not None else None, ws_bytes, st), what)
+
+
+def pack_ue8m0_weight_scales(block_scales: torch.Tensor, N: int, K: int) -> torch.Tensor:
+    """DeepGEMM's packed per-row UE8M0 layout of 128x128 block scales (what
+    transform_sf_into_required_layout makes of them for the weights,
+    tasks/baseline/L1/fp8_linear.py:501-510): int32 [N, ceil(K/512)], byte j of
+    word (n, i) the E8M0 exponent of the (power-of-two, else rounded up)
+    block scale of row n, K block 4i + j, stored MN-major (strides (1, N')
+    with N' = N rounded up to a multiple of 4), as DeepGEMM stores it."""
+    KB = -(-K // GROUP)
+    words = -(-KB // 4)
+    s = block_scales[: -(-N // GROUP), :KB].to(torch.float32)
+    bits = s.contiguous().view(torch.int32)
+    e = (bits >> 23) & 0xFF
+    e = e + ((bits & 0x7FFFFF) != 0).to(torch.int32)          # round up to a power of two
+    e = torch.clamp(e, max=254)
+    rows = e.repeat_interleave(GROUP, dim=0)[:N]                # [N, KB]
+    if KB % 4:
+        rows = torch.nn.functional.pad(rows, (0, 4 * words - KB))
+    b = rows.to(torch.uint8).view(N, words, 4).to(torch.int32)
+    packed = b[..., 0] | (b[..., 1] << 8) | (b[..., 2] << 16) | (b[..., 3] << 24)
+    n_al = -(-N // 4) * 4
+    out = torch.empty(words, n_al, dtype=torch.int32, device=block_scales.device)
+    out[:, :N] = packed.t()
+    if n_al > N:
+        out[:, N:] = 0
+    return out.t()[:N]
 
 
 def fp8_linear_forward(x: torch.Tensor, q_buf: torch.Tensor, s_buf: torch.Tensor, weight: torch.Tensor,

@@ -296,6 +296,18 @@ static Schedule bf16a_schedule(int64_t M, int64_t N, int64_t K, bool allow_split
     return s;
 }
 
+// Dense UE8M0 tiles with packed per-row weight scales (a.sWp).
+static int dispatch_dense_roww(const GemmArgs& a, const Schedule& sc, int64_t K, hipStream_t st, const char* what) {
+    if (sc.bm == 256 && sc.bn == 256) return launch_gemm_256_roww(a, sc, K, st, what);
+    if (sc.bm == 128 && sc.bn == 128) return launch_gemm<128, 128, 4, true, false, 4, 0, true>(a, sc, st, what);
+    if (sc.bm == 64 && sc.bn == 128) {
+        if (sc.stages == 4) return launch_gemm<64, 128, 4, true, false, 4, 0, true>(a, sc, st, what);
+        return launch_gemm<64, 128, 3, true, false, 4, 0, true>(a, sc, st, what);
+    }
+    set_error("%s: no packed-scale kernel for %dx%d tiles", what, sc.bm, sc.bn);
+    return 1;
+}
+
 template <bool kUe8m0>
 static int dispatch_dense(const GemmArgs& a, const Schedule& sc, int64_t K, hipStream_t st, const char* what) {
     if constexpr (kUe8m0) {
@@ -368,19 +380,41 @@ static int check_plan(const GemmArgs& a, const Schedule& sc, const char* what) {
 
 // Arguments, tile plan and workspace of a dense GEMM, all validated; nothing
 // is launched.  gemm_nt_launch then enqueues it.
+// Packed per-row UE8M0 weight scales (sWp != nullptr, scale_ue8m0 = 1):
+// int32 [N, ceil(K/512)] with strides (sWp_sn, sWp_sk) in elements.
+struct PackedW {
+    const int32_t* p = nullptr;
+    int64_t sn = 0, sk = 0;
+};
+
 static int gemm_nt_prepare(const char* what, const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
                            int64_t sA_stride_k, const void* W, int64_t ldw, const float* sW, int64_t sW_ld,
                            void* D_bf16, int64_t ldd, int64_t M, int64_t N, int64_t K, int scale_ue8m0,
-                           void* workspace, int64_t workspace_bytes, bool use_scratch, GemmArgs& a, Schedule& sc) {
+                           void* workspace, int64_t workspace_bytes, bool use_scratch, GemmArgs& a, Schedule& sc,
+                           const PackedW& pw = PackedW{}) {
     if (int rc = check_common(what, A, lda, W, ldw, D_bf16, ldd, M, N, K)) return rc;
     a = GemmArgs{};
     if (M == 0 || N == 0) return 0;
     KBN_CHECK_ARG(K > 0, "%s: K must be positive", what);
-    KBN_CHECK_ARG(sA && sW, "%s: null scale pointer", what);
-    KBN_CHECK_ARG(sW_ld >= K / kGroup, "%s: weight-scale row stride %lld < K/128", what, (long long)sW_ld);
+    KBN_CHECK_ARG(sA && (sW || pw.p), "%s: null scale pointer", what);
     a.A = (const uint8_t*)A; a.lda = lda;
-    if (int rc = check_scale_ranges(what, M, K, sA_stride_m, sA_stride_k, (N + kGroup - 1) / kGroup, sW_ld))
-        return rc;
+    if (pw.p) {
+        KBN_CHECK_ARG(scale_ue8m0, "%s: packed weight scales are UE8M0 exponents", what);
+        const int64_t words = (K / kGroup + 3) / 4;
+        KBN_CHECK_ARG(pw.sn >= 0 && pw.sk >= 0 && (N == 1 || pw.sn > 0) && (words == 1 || pw.sk > 0),
+                      "%s: bad packed weight-scale strides", what);
+        const int64_t span = ((N - 1) * pw.sn + (words - 1) * pw.sk + 1) * 4;
+        KBN_CHECK_ARG(span < 0x7FFFFFFFLL, "%s: packed weight scales span >= 2 GiB", what);
+        KBN_CHECK_ARG(((reinterpret_cast<uintptr_t>(pw.p) & 3u) == 0), "%s: packed weight scales must be 4-byte aligned",
+                      what);
+        a.sWp = pw.p; a.sWp_sn = pw.sn; a.sWp_sk = pw.sk; a.sWp_bytes = span;
+        sW_ld = K / kGroup;   // the block-scale path is not used
+        if (int rc = check_scale_ranges(what, M, K, sA_stride_m, sA_stride_k, 1, 1)) return rc;
+    } else {
+        KBN_CHECK_ARG(sW_ld >= K / kGroup, "%s: weight-scale row stride %lld < K/128", what, (long long)sW_ld);
+        if (int rc = check_scale_ranges(what, M, K, sA_stride_m, sA_stride_k, (N + kGroup - 1) / kGroup, sW_ld))
+            return rc;
+    }
     a.sA = sA; a.sA_sm = sA_stride_m; a.sA_sk = sA_stride_k;
     a.sA_bytes = scale_bytes(M, K / kGroup, sA_stride_m, sA_stride_k);
     a.W = (const uint8_t*)W; a.ldw = ldw; a.w_estride = 0;
@@ -414,6 +448,7 @@ static int gemm_nt_prepare(const char* what, const void* A, int64_t lda, const f
 static int gemm_nt_launch(const GemmArgs& a, const Schedule& sc, int scale_ue8m0, void* stream, const char* what) {
     if (a.M == 0 || a.N == 0) return 0;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (a.sWp) return dispatch_dense_roww(a, sc, a.K, st, what);
     return scale_ue8m0 ? dispatch_dense<true>(a, sc, a.K, st, what) : dispatch_dense<false>(a, sc, a.K, st, what);
 }
 
@@ -448,6 +483,22 @@ extern "C" int kbn_fp8_gemm_nt_ws(const void* A, int64_t lda, const float* sA, i
                                   void* workspace, int64_t workspace_bytes, void* stream) {
     return gemm_nt_impl("fp8_gemm_nt_ws", A, lda, sA, sA_stride_m, sA_stride_k, W, ldw, sW, sW_ld, D_bf16, ldd, M,
                         N, K, scale_ue8m0, workspace, workspace_bytes, stream);
+}
+
+extern "C" int kbn_fp8_gemm_nt_packed_ws(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
+                                         int64_t sA_stride_k, const void* W, int64_t ldw, const int32_t* sW_packed,
+                                         int64_t sWp_stride_n, int64_t sWp_stride_k, void* D_bf16, int64_t ldd,
+                                         int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
+                                         void* stream) {
+    const char* what = "fp8_gemm_nt_packed_ws";
+    GemmArgs a;
+    Schedule sc;
+    PackedW pw;
+    pw.p = sW_packed; pw.sn = sWp_stride_n; pw.sk = sWp_stride_k;
+    if (int rc = gemm_nt_prepare(what, A, lda, sA, sA_stride_m, sA_stride_k, W, ldw, nullptr, 0, D_bf16, ldd, M, N, K,
+                                 1, workspace, workspace_bytes, false, a, sc, pw))
+        return rc;
+    return gemm_nt_launch(a, sc, 1, stream, what);
 }
 
 extern "C" int kbn_per_token_group_quant_fp8(const void* x_bf16, int64_t M, int64_t K, int64_t ld_x, void* q_fp8,

@@ -13,4 +13,10 @@ int launch_gemm_256(const GemmArgs& a, const Schedule& sc, int64_t K, hipStream_
     return launch_gemm<256, 256, 2, true, false>(a, sc, st, what);
 }
 
+// The same tiles with packed per-row UE8M0 weight scales (GemmArgs::sWp).
+int launch_gemm_256_roww(const GemmArgs& a, const Schedule& sc, int64_t K, hipStream_t st, const char* what) {
+    if (K <= 2048) return launch_gemm<256, 256, 2, true, false, 8, 0, true>(a, sc, st, what);
+    return launch_gemm<256, 256, 2, true, false, 4, 0, true>(a, sc, st, what);
+}
+
 }  // namespace kbn

@@ -102,6 +102,12 @@ struct GemmArgs {
     const uint16_t* X;
     int64_t ldx;
     float eps;
+    // Packed per-row UE8M0 weight scales (DeepGEMM's int32 layout): word
+    // (n, i) at sWp[n * sWp_sn + i * sWp_sk] holds the E8M0 exponents of
+    // weight row n for K blocks 4i .. 4i + 3, byte j for block 4i + j.
+    const int32_t* sWp;
+    int64_t sWp_sn, sWp_sk;
+    int64_t sWp_bytes;
 };
 
 // Raw buffer descriptor (base, byte range) built from uniform values so it
@@ -358,7 +364,7 @@ constexpr int gemm_occupancy(int bm, int bn, int stages, int fuse_a = 0) {
 // wavefront quantizes the 4 kFuseA rows its own DMAs brought, in place,
 // with 16 / kFuseA lanes per row.
 template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, bool kSplitK, int kWaves, bool kSorted = false,
-          int kFuseA = 0>
+          int kFuseA = 0, bool kRowW = false>
 __global__ __launch_bounds__(64 * kWaves, (kStages * (gemm_a_stage_bytes(BM, kFuseA) + BN * 128) +
                                                kStages * 512 * kWaves <=
                                            80 * 1024)
@@ -370,6 +376,8 @@ gemm_bs_kernel(const GemmArgs a) {
                               (kFuseA == 1 || kFuseA == 2 || kFuseA == 4)),
                   "in-kernel activation quant: UE8M0, dense, 64-row tiles of four wavefronts, 16/32/64 rows");
     static_assert(kWaves == 4 || kWaves == 8, "2x2 or 2x4 wavefronts");
+    static_assert(!kRowW || (kUe8m0 && !kGrouped && !kSorted && !kFuseA && BN <= 64 * kWaves),
+                  "packed per-row weight scales: dense UE8M0 tiles, one scale word per tile row and lane");
     constexpr int WM = 2, WN = kWaves / 2;
     constexpr int TM = BM / WM, TN = BN / WN;   // wavefront tile
     constexpr int FM = TM / 32, FN = TN / 32;   // 32x32 fragments per wavefront
@@ -435,7 +443,7 @@ gemm_bs_kernel(const GemmArgs a) {
                              : make_desc(a.A + (int64_t)m0 * a.lda, (int64_t)(a.M - m0 - 1) * a.lda + a.K);
     const v4i dW = make_desc(Wbase + (int64_t)n0 * a.ldw, (int64_t)(a.N - n0 - 1) * a.ldw + a.K);
     const v4i dSA = make_desc(a.sA, a.sA_bytes);
-    const v4i dSW = make_desc(sWbase, (int64_t)NB * a.sW_ld * 4);
+    const v4i dSW = kRowW ? make_desc(a.sWp, a.sWp_bytes) : make_desc(sWbase, (int64_t)NB * a.sW_ld * 4);
 
     // DMA lane mapping: one instruction = 8 rows x 128 B starting at row
     // r0 = 8 q; lane i fills slot i % 8 of row r0 + i / 8 with global chunk
@@ -498,9 +506,20 @@ gemm_bs_kernel(const GemmArgs a) {
     const bool sa_live = sa_src >= 0;
     const int sa_kstep = sa_live ? (int)(a.sA_sk * 4) : 0;
     const int sa_off0 = sa_live ? (int)((int64_t)sa_src * a.sA_sm * 4) + kb0 * sa_kstep : kOob;
-    const bool sw_live = (lane < (BN + 127) / 128) & (n0 / 128 + lane < NB);
-    const int sw_kstep = sw_live ? 4 : 0;
-    const int sw_off0 = sw_live ? (n0 / 128 + lane) * (int)a.sW_ld * 4 + kb0 * 4 : kOob;
+    // W scales of a stage: the tile's 128-row block scales (lane < BN / 128),
+    // or with kRowW one packed word per tile row (row wave * 64 + lane): its
+    // four K blocks' exponents, word (kb / 4) of the row
+    int sw_kstep, sw_off0;
+    if constexpr (kRowW) {
+        const int r = wave * 64 + lane;
+        const bool live = r < BN && n0 + r < a.N;
+        sw_kstep = live ? (int)(a.sWp_sk * 4) : 0;
+        sw_off0 = live ? (int)((int64_t)(n0 + r) * a.sWp_sn * 4) : kOob;
+    } else {
+        const bool sw_live = (lane < (BN + 127) / 128) & (n0 / 128 + lane < NB);
+        sw_kstep = sw_live ? 4 : 0;
+        sw_off0 = sw_live ? (n0 / 128 + lane) * (int)a.sW_ld * 4 + kb0 * 4 : kOob;
+    }
     constexpr int kScaleDma = kFuseA ? 1 : 2;    // scale vectors per stage (no A scales when fused)
     constexpr int kDma = kAInstr + kBInstr + kScaleDma;  // DMA instructions per wave per stage
     // Weight rows stream past L2 (non-temporal) where the weights dominate the
@@ -519,7 +538,10 @@ gemm_bs_kernel(const GemmArgs a) {
         if (!kFuseA && d == 0) {
             dma_b32(dSA, base + kA + kB + wave * 256, live ? sa_off0 + s * sa_kstep : kOob);
         } else if (d == kScaleDma - 1) {
-            dma_b32(dSW, base + kA + kB + kSA + wave * 256, live ? sw_off0 + s * sw_kstep : kOob);
+            if constexpr (kRowW)
+                dma_b32(dSW, base + kA + kB + kSA + wave * 256, live ? sw_off0 + ((kb0 + s) >> 2) * sw_kstep : kOob);
+            else
+                dma_b32(dSW, base + kA + kB + kSA + wave * 256, live ? sw_off0 + s * sw_kstep : kOob);
         } else if (d < kScaleDma + kAInstr) {
             const int i = d - kScaleDma;
             int off;
@@ -575,16 +597,33 @@ gemm_bs_kernel(const GemmArgs a) {
     };
     // raw fp32 scales of a stage: per fragment row (lane & 31) and the
     // wavefront's weight block (converted to E8M0 only when consumed)
-    auto read_scales = [&](const uint8_t* st, float (&sa)[FM], float& sw) {
+    // kRowW: the packed word of each fragment's W row (lane & 31)
+    uint32_t swr[kRowW ? FN : 1], nswr[kRowW ? FN : 1];
+    auto read_scales = [&](const uint8_t* st, float (&sa)[FM], float& sw, uint32_t (&wr)[kRowW ? FN : 1]) {
         const float* ssa = reinterpret_cast<const float*>(st + kA + kB);
-        const float* ssw = reinterpret_cast<const float*>(st + kA + kB + kSA + wave * 256);
 #pragma unroll
         for (int i = 0; i < FM; ++i) sa[i] = ssa[wm * TM + i * 32 + (lane & 31)];
-        sw = ssw[nb_local];
+        if constexpr (kRowW) {
+            const uint32_t* sww = reinterpret_cast<const uint32_t*>(st + kA + kB + kSA);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) wr[j] = sww[wn * TN + j * 32 + (lane & 31)];
+            sw = 0.f;
+        } else {
+            const float* ssw = reinterpret_cast<const float*>(st + kA + kB + kSA + wave * 256);
+            sw = ssw[nb_local];
+        }
     };
     v8i fa0[FM], fb0[FN], fa1[FM], fb1[FN];
     float sa[FM], sw = 0.f, nsa[FM], nsw = 0.f;
     int ea[FM], eb = 0, nea[FM], neb = 0;
+    // kRowW: E8M0 byte of each fragment's W row for the current (next) block
+    int ebr[kRowW ? FN : 1], nebr[kRowW ? FN : 1];
+    auto row_bytes = [&](const uint32_t (&wr)[kRowW ? FN : 1], int gkb, int (&e)[kRowW ? FN : 1]) {
+        if constexpr (kRowW) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) e[j] = (int)((wr[j] >> (8 * (gkb & 3))) & 0xFFu);
+        }
+    };
     // FP32 contract: mantissa product mu = mant(sA) mant(sW) in [1, 4) of the
     // current block per fragment row, and the rescale ratio mu_prev / mu for
     // the block about to start (the exponents go to the MFMA).
@@ -642,7 +681,8 @@ gemm_bs_kernel(const GemmArgs a) {
     // block's scales enter as E8M0 operands: eb for the W rows, ea[i] per A row.
     auto mfma_at = [&](int t, const v8i (&fa)[FM], const v8i (&fb)[FN]) {
         const int i = t / FN, j = t % FN;
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], acc[i][j], 0, 0, 0, eb, 0, ea[i]);
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], acc[i][j], 0, 0, 0,
+                                                                      kRowW ? ebr[j] : eb, 0, ea[i]);
     };
     // FP32 contract: bring the running sum to the new block's mantissa base
     // before the block's first MFMA.  One uniform branch around all of it,
@@ -769,11 +809,12 @@ gemm_bs_kernel(const GemmArgs a) {
     wait_dma_n<(kStages - 1) * kDma>();
     quant_rows(stage_ptr(0));   // fused A: block 0 (the loop quantizes block kb+1 in iteration kb)
     __syncthreads();
-    read_scales(stage_ptr(0), sa, sw);
+    read_scales(stage_ptr(0), sa, sw, swr);
 #pragma unroll
     for (int q = 0; q < kR; ++q) read_half(stage_ptr(0), 0, q, fa0, fb0);
 
     convert(sa, sw, ea, eb, -1);
+    row_bytes(swr, kb0, ebr);
 
     for (int kb = 0; kb < KB; ++kb) {
         const uint8_t* cur = stage_ptr(kb);
@@ -810,13 +851,14 @@ gemm_bs_kernel(const GemmArgs a) {
 #pragma unroll
         for (int t = 0; t < kT; ++t) {
             mfma_at(t, fa1, fb1);
-            if (t == 0) read_scales(nxt, nsa, nsw);
+            if (t == 0) read_scales(nxt, nsa, nsw, nswr);
             // converted scales of block kb+1, half a sub-step after their
             // reads (FP32 contract: none past the last block, whose mantissa
             // products the store needs)
             if (t == kT / 2) {
                 if constexpr (kUe8m0) convert(nsa, nsw, nea, neb, kb);
                 else if (kb + 1 < KB) convert(nsa, nsw, nea, neb, kb);
+                row_bytes(nswr, kb0 + kb + 1, nebr);
             }
 #pragma unroll
             for (int q = t * kR / kT; q < (t + 1) * kR / kT; ++q) read_half(nxt, 0, q, fa0, fb0);
@@ -832,6 +874,10 @@ gemm_bs_kernel(const GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < FM; ++i) ea[i] = nea[i];
         eb = neb;
+        if constexpr (kRowW) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) ebr[j] = nebr[j];
+        }
     }
     // the trailing (out-of-range) loads still target this workgroup's LDS
     wait_dma();
@@ -1058,8 +1104,9 @@ unsigned* splitk_flags_for(hipStream_t st, int64_t tail_tiles);
 // unit (gemm_big.hip) without the VGPR-form MFMA option: their 256
 // accumulators per lane need the AGPRs.
 int launch_gemm_256(const GemmArgs& a, const Schedule& sc, int64_t K, hipStream_t st, const char* what);
+int launch_gemm_256_roww(const GemmArgs& a, const Schedule& sc, int64_t K, hipStream_t st, const char* what);
 
-template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, int kWaves = 4, int kFuseA = 0>
+template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, int kWaves = 4, int kFuseA = 0, bool kRowW = false>
 static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const char* what) {
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
@@ -1073,7 +1120,7 @@ static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const cha
         a.kb_per_split = a.K / kRowB;
         const int64_t grid = kGrouped ? moe_dealt_grid(a.tiles_m, a.tiles_n) : dp;
         KBN_CHECK_ARG(grid <= 0x7FFFFFFFLL, "%s: too many tiles", what);
-        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped, false, kWaves, false, kFuseA>
+        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped, false, kWaves, false, kFuseA, kRowW>
             <<<dim3((unsigned)grid), dim3(64 * kWaves), 0, st>>>(a);
         KBN_CHECK_LAUNCH(what);
     }
@@ -1099,7 +1146,7 @@ static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const cha
         // less).  More rows: that sum would run on one workgroup per tile at
         // the end of the launch, so the separate kernel spreads it instead.
         a.flags = (BM <= 64 && sc.fused) ? splitk_flags_for(st, tiles - dp) : nullptr;
-        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped && false, true, kWaves, false, kFuseA>
+        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped && false, true, kWaves, false, kFuseA, kRowW>
             <<<dim3((unsigned)blocks), dim3(64 * kWaves), 0, st>>>(a);
         KBN_CHECK_LAUNCH(what);
         if (!a.flags) {

@@ -131,6 +131,22 @@ class Fp8Linear(nn.Module):
             output = torch.empty(M, N, dtype=torch.bfloat16, device=x2.device)
             torch.ops.kb_nano_fp8.per_token_group_quant_fp8(x2, q_input, input_scale, True)
             torch.ops.kb_nano_fp8.fp8_gemm_nt(q_input, input_scale, weight_fp8, weight_scale_inv, output)
+        elif weight_scale_inv.dtype is torch.int32:
+            # DeepGEMM's packed per-row UE8M0 scales (the layout the
+            # reference's postprocess_fp8_weights returns, :501-510): UE8M0
+            # activation quant, then the GEMM that takes the packed exponents
+            if self._a_buf is not None and M <= self._a_buf.shape[0]:
+                q_buf, s_buf, o_buf = self._a_buf, self._s_buf, self._o_buf
+            elif self._pf is not None and M <= self._pf.a.shape[0]:
+                q_buf, s_buf, o_buf = self._pf.a, self._pf.s, self._pf.o
+            else:
+                q_buf = torch.empty(M, K, dtype=FP8, device=x2.device)
+                s_buf = _alloc_colmajor_scale(M, G, x2.device)
+                o_buf = torch.empty(M, N, dtype=torch.bfloat16, device=x2.device)
+            q, s = (q_buf, s_buf) if q_buf.shape[0] == M else (q_buf[:M], s_buf[:M])
+            output = o_buf if o_buf.shape[0] == M else o_buf[:M]
+            _ops.per_token_group_quant_fp8(x2, q, s, use_ue8m0=True, eps=_QUANT_EPS)
+            _ops.fp8_gemm_nt(q, s, weight_fp8, weight_scale_inv, output)
         elif M <= _ops.BF16A_MAX_M and is_e8m0_used() and _ops.bf16a_preferred(M, N, K, x2.get_device()):
             # small M (the reference's bf16-input branch, :398-417): one
             # launch of the GEMM that quantizes its bf16 activations itself,

@@ -527,3 +527,36 @@ def test_release_workspaces_drops_cached_buffers():
     finally:
         _ops._WS_BUFS.clear()
         _ops._WS_BUFS.update(saved)
+
+
+def test_pack_ue8m0_weight_scales_layout():
+    """The packed per-row UE8M0 layout: byte j of word (n, i) is the rounded-up
+    exponent of row n's block scale for K block 4i + j, MN-major storage."""
+    import numpy as np
+
+    from kb_nano_amd import _ops
+    N, K = 300, 1408                      # 3 row blocks (the last partial), 11 K blocks, 3 words
+    rng = np.random.default_rng(0)
+    s = (2.0 ** rng.integers(-12, 3, size=(3, 11)) * rng.choice([1.0, 1.37], size=(3, 11))).astype(np.float32)
+    p = _ops.pack_ue8m0_weight_scales(torch.from_numpy(s), N, K)
+    assert p.shape == (N, 3) and p.dtype == torch.int32 and p.stride() == (1, 300)
+    words = p.numpy().view(np.uint32)
+    for n in (0, 127, 128, 255, 256, 299):
+        for kb in range(11):
+            e = (words[n, kb // 4] >> (8 * (kb % 4))) & 0xFF
+            v = float(s[n // 128, kb])
+            assert 2.0 ** (int(e) - 127) == 2.0 ** np.ceil(np.log2(v)), (n, kb)
+        assert (words[n, 2] >> 24) == 0   # K block 11 does not exist
+
+
+def test_packed_gemm_rejects_bad_scales_without_device():
+    from kb_nano_amd._lib import lib
+    L = lib()
+    p = ctypes.c_void_p(4096)
+    odd = ctypes.c_void_p(4098)
+    rc = L.kbn_fp8_gemm_nt_packed_ws(p, 256, p, 1, 64, p, 256, odd, 1, 64, p, 128, 64, 128, 256, None, 0, None)
+    assert rc == 1 and "4-byte aligned" in _err()
+    rc = L.kbn_fp8_gemm_nt_packed_ws(p, 256, p, 1, 64, p, 256, p, 0, 64, p, 128, 64, 128, 256, None, 0, None)
+    assert rc == 1 and "strides" in _err()
+    rc = L.kbn_fp8_gemm_nt_packed_ws(p, 256, None, 1, 64, p, 256, p, 1, 128, p, 128, 64, 128, 256, None, 0, None)
+    assert rc == 1 and "null scale" in _err()

@@ -533,3 +533,85 @@ def test_gemm_fused_splitk_forked_capture(gpu_device):
         for i, c in enumerate(cases):
             assert np.array_equal(bf16_bits(c[4]), eager[i]), f"replay {rep}, GEMM {i}"
         assert np.array_equal(bf16_bits(extra), eager[1]), f"eager call between replays {rep}"
+
+
+@pytest.mark.parametrize("M,N,K", [(100, 2304, 4096), (1, 7168, 18432), (8, 8192, 8192), (64, 2048, 2048),
+                                   (77, 200, 1152), (300, 1024, 2048), (512, 768, 4608)])
+def test_gemm_packed_row_scales_equal_block_scales(gpu_device, M, N, K):
+    """DeepGEMM's packed per-row UE8M0 weight scales (int32 [N, ceil(K/512)],
+    MN-major; the reference's own fp8_linear scenarios pass this layout,
+    bench/kernels/benchmark_scenarios/small/shape_registry.yaml:18719-18737):
+    with the block scales' exponents repeated on every row of a block, the
+    output is the fp32-block-scale GEMM's bit for bit (data-parallel, split
+    tails summed in the split launch and by the reduction, 128x128 and
+    256x256 tiles, K not a multiple of 512), every output written."""
+    from kb_nano_amd import _ops
+    from tests._util import assert_all_written
+    qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=M + 2 * N + K)
+    sw = (sw * np.float32(1.37)).astype(np.float32)   # rounded up to powers of two by both paths
+    ref = _gemm_gpu(qa, sa, qw, sw, gpu_device, ue8m0=True)
+    from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
+    A = to_fp8(qa, gpu_device)
+    sA = _alloc_colmajor_scale(M, K // 128, gpu_device)
+    sA.copy_(torch.from_numpy(sa))
+    W = to_fp8(qw, gpu_device)
+    packed = _ops.pack_ue8m0_weight_scales(torch.from_numpy(sw).to(gpu_device), N, K)
+    assert packed.dtype == torch.int32 and packed.shape == (N, -(-K // 512)) and packed.stride(0) == 1
+    D = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu_device)
+    _ops.fp8_gemm_nt(A, sA, W, packed, D)
+    torch.cuda.synchronize()
+    assert_all_written(D, f"packed {M}x{N}x{K}")
+    assert np.array_equal(bf16_bits(D), bf16_bits(ref)), f"packed scales != block scales at {M}x{N}x{K}"
+
+
+def test_gemm_packed_row_scales_per_row_exponents(gpu_device):
+    """Exponents that differ on every weight row and K block (row-major int32
+    storage this time): each output column n checked against the float64
+    oracle with W row n's own scales (a one-row block of the oracle)."""
+    from kb_nano_amd import _ops
+    M, N, K = 48, 320, 1408          # 11 K blocks: 3 words, the last with 3 bytes used
+    qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=77)
+    rng = np.random.default_rng(5)
+    KB = K // 128
+    # each row's exponent within +-2 of its block's own (realistic magnitudes)
+    e_blk = ((np.repeat(sw, 128, axis=0)[:N].view(np.uint32) >> 23) & 0xFF).astype(np.int64)
+    e = (e_blk + rng.integers(-2, 3, size=(N, KB))).astype(np.uint32)
+    words = -(-KB // 4)
+    ep = np.zeros((N, 4 * words), dtype=np.uint32)
+    ep[:, :KB] = e
+    packed = (ep[:, 0::4] | (ep[:, 1::4] << 8) | (ep[:, 2::4] << 16) | (ep[:, 3::4] << 24)).astype(np.uint32)
+    from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
+    A = to_fp8(qa, gpu_device)
+    sA = _alloc_colmajor_scale(M, KB, gpu_device)
+    sA.copy_(torch.from_numpy(sa))
+    W = to_fp8(qw, gpu_device)
+    P = torch.from_numpy(packed.view(np.int32)).to(gpu_device)
+    D = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu_device)
+    _ops.fp8_gemm_nt(A, sA, W, P, D)
+    torch.cuda.synchronize()
+    row_scale = np.ldexp(np.float32(1.0), e.astype(np.int32) - 127).astype(np.float32)   # [N, KB]
+    ref = np.concatenate([oracle.gemm_nt_sample(qa, sa, qw[n:n + 1], row_scale[n:n + 1], ue8m0=True)
+                          for n in range(N)], axis=1)
+    assert_gemm_close(D, ref, "per-row packed exponents")
+
+
+def test_fp8_linear_with_packed_scales(gpu_device):
+    """Fp8Linear given the reference's packed int32 weight_scale_inv: the
+    same output as with the equivalent fp32 block scales, eager and into
+    installed buffers, at M = 16 and 100."""
+    from kb_nano_amd import Fp8Linear, _ops
+    N, K = 2304, 4096
+    _, _, qw, sw = quantized_gemm_inputs(16, N, K, seed=41)
+    W = to_fp8(qw, gpu_device)
+    sW = torch.from_numpy(sw).to(gpu_device)
+    packed = _ops.pack_ue8m0_weight_scales(sW, N, K)
+    for M in (16, 100):
+        x = seeded_bf16((M, K), seed=M).to(gpu_device)
+        ref = Fp8Linear()(x, W, sW)
+        got = Fp8Linear()(x, W, packed)
+        lin = Fp8Linear()
+        lin._ensure_buffers(128, K, N, gpu_device)
+        got2 = lin(x, W, packed)
+        torch.cuda.synchronize()
+        assert np.array_equal(bf16_bits(got), bf16_bits(ref)), f"M={M}"
+        assert np.array_equal(bf16_bits(got2), bf16_bits(ref)), f"M={M} installed buffers"
