@@ -251,6 +251,40 @@ static int check_scale_ranges(const char* what, int64_t M, int64_t K, int64_t sm
     return 0;
 }
 
+// Measured in one process against the 256x256-only plan, same data (DeepSeek-V3
+// recipe, inputs rotated past the MALL): down 7168 x 18432 and o 7168 x 16384
+// at M = 4096 422-425 / 384-389 us against 431-434 / 394-396 us; the partial
+// wave it removes runs at a higher clock (fewer CUs busy under the power
+// cap), so the gain is 2%, not the 11% the wave count suggests.  With short K
+// the second launch's fill costs more than that (3000 x 7168 x 4096: 100 us
+// against 97), so only K of at least 8192 takes it.
+constexpr int64_t kMixedMinK = 8192;
+
+// 256x256 tiles whose last wave would run partly empty: move the last n192
+// columns to 256x192 tiles in a second launch when both launches then fill
+// whole waves.  Cost in units of a 256x256 wave: a wave of 256x192 tiles
+// does 3/4 of the work with about 4% more fetch and fragment traffic per
+// FLOP, so it is counted as 0.78; the mixed plan is taken when it saves at
+// least 5%.  (DeepSeek-V3 down / o at M = 4096: 448 tiles = 1.75 waves on
+// 256 CUs become one wave of 256x256 and one of 256x192 tiles.)
+static void plan_mixed_192(Schedule& s, int64_t M, int64_t N) {
+    const int64_t cus = cu_count();
+    const int64_t tm = (M + 255) / 256;
+    auto waves = [&](int64_t t) { return (t + cus - 1) / cus; };
+    const double base = (double)waves(s.tiles);
+    double best = base * 0.95;
+    for (int64_t b = 1; 192 * b <= N; ++b) {
+        const int64_t rest = N - 192 * b;
+        if (rest % 256) continue;
+        const double cost = (double)waves(tm * (rest / 256)) + 0.78 * (double)waves(tm * b);
+        if (cost < best - 1e-9) {
+            best = cost;
+            s.n192 = (int)(192 * b);
+        }
+    }
+    if (s.n192) s.tiles = s.dp_tiles = tm * ((N - s.n192) / 256 + s.n192 / 192);
+}
+
 // Dense tile configuration: 256x256 (2 LDS stages) when M > 128 (128x256,
 // 3 stages, under the FP32 contract, whose per-row mantissa state does not
 // fit next to a 256x256 tile's accumulators), 128x128 (4 stages) for
@@ -278,6 +312,7 @@ static Schedule dense_schedule(int64_t M, int64_t N, int64_t K, int ue8m0, bool 
     s.dp_tiles = s.tiles;
     s.kb_per_split = (int)(K / kGroup);
     if (allow_split) plan_tail(s, M, (int)(K / kGroup));
+    if (s.bm == 256 && s.splits == 1 && K >= kMixedMinK) plan_mixed_192(s, M, N);
     return s;
 }
 
@@ -364,7 +399,10 @@ static void* scratch_ptr(const char* what) {
 // The checks launch_gemm makes before each launch, made ahead of any launch
 // (kbn_fp8_linear_forward validates its GEMM before it enqueues the quant).
 static int check_plan(const GemmArgs& a, const Schedule& sc, const char* what) {
-    const int64_t tiles = (((int64_t)a.M + sc.bm - 1) / sc.bm) * (((int64_t)a.N + sc.bn - 1) / sc.bn);
+    const int64_t tiles = sc.n192 ? (((int64_t)a.M + 255) / 256) * ((a.N - sc.n192) / 256 + sc.n192 / 192)
+                                  : (((int64_t)a.M + sc.bm - 1) / sc.bm) * (((int64_t)a.N + sc.bn - 1) / sc.bn);
+    KBN_CHECK_ARG(!sc.n192 || (sc.bm == 256 && sc.splits == 1 && (a.N - sc.n192) % 256 == 0 && sc.n192 % 192 == 0),
+                  "%s: bad mixed 256/192 plan", what);
     KBN_CHECK_ARG(tiles == sc.tiles && tiles <= 0x7FFFFFFFLL, "%s: too many tiles", what);
     if (a.P && sc.splits > 1 && sc.dp_tiles < tiles) {
         const int64_t need = (int64_t)sc.splits * (tiles - sc.dp_tiles) * sc.bm * sc.bn * 4;

@@ -383,7 +383,12 @@ gemm_bs_kernel(const GemmArgs a) {
     constexpr int FM = TM / 32, FN = TN / 32;   // 32x32 fragments per wavefront
     static_assert(FM >= 1 && FN >= 1 && TM % 32 == 0 && TN % 32 == 0, "fragment tiling");
     static_assert(BM <= 64 * kWaves && BM % (16 * kWaves) == 0 && BN % (16 * kWaves) == 0, "DMA tiling");
-    static_assert(128 % TN == 0 || TN % 128 == 0, "wave N tile must not straddle a scale block");
+    // A wave N tile that does not divide (or is not a multiple of) a 128-row
+    // weight-scale block (the 96 columns of a 256x192 tile) takes one W scale
+    // per 32-column fragment instead of one per wavefront.
+    constexpr bool kFragW = !kRowW && 128 % TN != 0 && TN % 128 != 0;
+    constexpr bool kPerFragW = kRowW || kFragW;
+    static_assert(!kFragW || (kUe8m0 && TN % 32 == 0), "per-fragment weight scales: UE8M0 contract");
     constexpr int kArow = kFuseA ? 2 * kRowB : kRowB;   // LDS bytes of one A row of a stage
     constexpr int kA = gemm_a_stage_bytes(BM, kFuseA), kB = BN * kRowB, kSA = kWaves * 256, kSW = kWaves * 256;
     constexpr int kAW = 4 * (kFuseA ? kFuseA : 1);     // fused A: LDS rows per wavefront
@@ -516,7 +521,8 @@ gemm_bs_kernel(const GemmArgs a) {
         sw_kstep = live ? (int)(a.sWp_sk * 4) : 0;
         sw_off0 = live ? (int)((int64_t)(n0 + r) * a.sWp_sn * 4) : kOob;
     } else {
-        const bool sw_live = (lane < (BN + 127) / 128) & (n0 / 128 + lane < NB);
+        // the scale blocks the tile's rows touch (a 192-row tile may start mid-block)
+        const bool sw_live = (lane < (((n0 & 127) + BN + 127) >> 7)) & (n0 / 128 + lane < NB);
         sw_kstep = sw_live ? 4 : 0;
         sw_off0 = sw_live ? (n0 / 128 + lane) * (int)a.sW_ld * 4 + kb0 * 4 : kOob;
     }
@@ -598,8 +604,9 @@ gemm_bs_kernel(const GemmArgs a) {
     // raw fp32 scales of a stage: per fragment row (lane & 31) and the
     // wavefront's weight block (converted to E8M0 only when consumed)
     // kRowW: the packed word of each fragment's W row (lane & 31)
-    uint32_t swr[kRowW ? FN : 1], nswr[kRowW ? FN : 1];
-    auto read_scales = [&](const uint8_t* st, float (&sa)[FM], float& sw, uint32_t (&wr)[kRowW ? FN : 1]) {
+    // kFragW: the fp32 block scale (as bits) of each fragment's 32 W rows
+    uint32_t swr[kPerFragW ? FN : 1], nswr[kPerFragW ? FN : 1];
+    auto read_scales = [&](const uint8_t* st, float (&sa)[FM], float& sw, uint32_t (&wr)[kPerFragW ? FN : 1]) {
         const float* ssa = reinterpret_cast<const float*>(st + kA + kB);
 #pragma unroll
         for (int i = 0; i < FM; ++i) sa[i] = ssa[wm * TM + i * 32 + (lane & 31)];
@@ -607,6 +614,11 @@ gemm_bs_kernel(const GemmArgs a) {
             const uint32_t* sww = reinterpret_cast<const uint32_t*>(st + kA + kB + kSA);
 #pragma unroll
             for (int j = 0; j < FN; ++j) wr[j] = sww[wn * TN + j * 32 + (lane & 31)];
+            sw = 0.f;
+        } else if constexpr (kFragW) {
+            const uint32_t* ssw = reinterpret_cast<const uint32_t*>(st + kA + kB + kSA + wave * 256);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) wr[j] = ssw[((n0 & 127) + wn * TN + j * 32) >> 7];
             sw = 0.f;
         } else {
             const float* ssw = reinterpret_cast<const float*>(st + kA + kB + kSA + wave * 256);
@@ -616,12 +628,17 @@ gemm_bs_kernel(const GemmArgs a) {
     v8i fa0[FM], fb0[FN], fa1[FM], fb1[FN];
     float sa[FM], sw = 0.f, nsa[FM], nsw = 0.f;
     int ea[FM], eb = 0, nea[FM], neb = 0;
-    // kRowW: E8M0 byte of each fragment's W row for the current (next) block
-    int ebr[kRowW ? FN : 1], nebr[kRowW ? FN : 1];
-    auto row_bytes = [&](const uint32_t (&wr)[kRowW ? FN : 1], int gkb, int (&e)[kRowW ? FN : 1]) {
+    // kRowW: E8M0 byte of each fragment's W row for the current (next) block;
+    // kFragW: the rounded-up exponent of each fragment's block scale
+    int ebr[kPerFragW ? FN : 1], nebr[kPerFragW ? FN : 1];
+    auto row_bytes = [&](const uint32_t (&wr)[kPerFragW ? FN : 1], int gkb, int (&e)[kPerFragW ? FN : 1]) {
         if constexpr (kRowW) {
 #pragma unroll
             for (int j = 0; j < FN; ++j) e[j] = (int)((wr[j] >> (8 * (gkb & 3))) & 0xFFu);
+        } else if constexpr (kFragW) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) e[j] = ue8m0_ceil_byte(__uint_as_float(wr[j]));
+            (void)gkb;
         }
     };
     // FP32 contract: mantissa product mu = mant(sA) mant(sW) in [1, 4) of the
@@ -682,7 +699,7 @@ gemm_bs_kernel(const GemmArgs a) {
     auto mfma_at = [&](int t, const v8i (&fa)[FM], const v8i (&fb)[FN]) {
         const int i = t / FN, j = t % FN;
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[j], fa[i], acc[i][j], 0, 0, 0,
-                                                                      kRowW ? ebr[j] : eb, 0, ea[i]);
+                                                                      kPerFragW ? ebr[j] : eb, 0, ea[i]);
     };
     // FP32 contract: bring the running sum to the new block's mantissa base
     // before the block's first MFMA.  One uniform branch around all of it,
@@ -874,7 +891,7 @@ gemm_bs_kernel(const GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < FM; ++i) ea[i] = nea[i];
         eb = neb;
-        if constexpr (kRowW) {
+        if constexpr (kPerFragW) {
 #pragma unroll
             for (int j = 0; j < FN; ++j) ebr[j] = nebr[j];
         }
@@ -1079,6 +1096,10 @@ struct Schedule {
     int64_t ws_bytes = 0;         // fp32 slabs of the tail
     bool fused = false;           // the split launch sums the slabs itself
     int fuse_a = 0;               // bf16 activations quantized by the GEMM: rows of four per wavefront (1, 2, 4)
+    // 256-row tiles only: the last n192 columns run as 256x192 tiles in a
+    // second launch (the first N - n192 as 256x256), so that both launches
+    // fill whole waves where 256x256 tiles alone would leave a partial one
+    int n192 = 0;
 };
 
 // Split-K tails of the 64-row tiles summed by the split launch itself (no

@@ -536,7 +536,7 @@ def test_gemm_fused_splitk_forked_capture(gpu_device):
 
 
 @pytest.mark.parametrize("M,N,K", [(100, 2304, 4096), (1, 7168, 18432), (8, 8192, 8192), (64, 2048, 2048),
-                                   (77, 200, 1152), (300, 1024, 2048), (512, 768, 4608)])
+                                   (77, 200, 1152), (300, 1024, 2048), (512, 768, 8704)])
 def test_gemm_packed_row_scales_equal_block_scales(gpu_device, M, N, K):
     """DeepGEMM's packed per-row UE8M0 weight scales (int32 [N, ceil(K/512)],
     MN-major; the reference's own fp8_linear scenarios pass this layout,
@@ -615,3 +615,24 @@ def test_fp8_linear_with_packed_scales(gpu_device):
         torch.cuda.synchronize()
         assert np.array_equal(bf16_bits(got), bf16_bits(ref)), f"M={M}"
         assert np.array_equal(bf16_bits(got2), bf16_bits(ref)), f"M={M} installed buffers"
+
+
+@pytest.mark.parametrize("M,N,K", [(3000, 7168, 8192), (4096, 7168, 8192), (512, 768, 8192)])
+def test_gemm_mixed_256_192_plan(gpu_device, M, N, K):
+    """256x256 tiles whose last wave would be partly empty move their last
+    columns to 256x192 tiles in a second launch when K >= 8192 (two full
+    waves instead of 1.75, DeepSeek-V3 down / o at M = 4096; or only 256x192
+    tiles when they fill one wave better).  The 96-column wave tiles straddle 128-row weight
+    scale blocks, so each 32-column fragment takes its own block scale.
+    Ragged M, NaN-prefilled output entirely written, a point of every
+    64x128 block against the float64 oracle, non-power-of-two weight scales
+    rounded up under the UE8M0 contract."""
+    from tests._util import assert_all_written, tile_cover
+    qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=M + N + K + 1)
+    sw = (sw * np.float32(1.37)).astype(np.float32)
+    D = _gemm_gpu(qa, sa, qw, sw, gpu_device, ue8m0=True)
+    assert_all_written(D, f"mixed plan {M}x{N}x{K}")
+    rows, cols = tile_cover(M, N, np.random.default_rng(M + K))
+    ref = oracle.gemm_nt_sample(qa, sa, qw, sw, rows=rows, cols=cols, ue8m0=True)
+    got = D[torch.from_numpy(rows).to(gpu_device)][:, torch.from_numpy(cols).to(gpu_device)]
+    assert_gemm_close(got, ref, f"mixed plan {M}x{N}x{K}")
