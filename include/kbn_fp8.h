@@ -416,6 +416,18 @@ int kbn_splitk_counter_stats(int64_t* regions_used, int64_t* regions_total, int6
 int kbn_debug_splitk_regions(int64_t n_keys, int32_t* out_region, int64_t* out_fallbacks);
 
 /*
+ * Test hook (no counterpart in the reference): the tile plan the GEMM entry
+ * points would launch for an M x N x K call with a workspace, without a GPU
+ * (a device with 256 CUs is assumed when none is present).  bf16a != 0 asks
+ * for kbn_fp8_gemm_bf16a's plan (M <= 64), else kbn_fp8_gemm_nt_ws's with
+ * scale_ue8m0.  out[0..8] = tile rows, tile columns, LDS stages, tiles,
+ * data-parallel tiles, K splits of the rest, K blocks per split, whether the
+ * split launch sums its own slabs (1) or a reduction launch follows (0), and
+ * workspace bytes.
+ */
+int kbn_debug_gemm_plan(int64_t M, int64_t N, int64_t K, int scale_ue8m0, int bf16a, int64_t* out);
+
+/*
  * Test hook (no counterpart in the reference): the kernels' bf16 SiLU
  * applied elementwise to n bf16 bit patterns, for exhaustive checking.
  */

@@ -53,6 +53,7 @@ SIGNATURES = {
     "kbn_fp8_block_requant": ([_P, _I, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I, _F, _P], _I),
     "kbn_splitk_counter_stats": ([_P, _P, _P], _I),
     "kbn_debug_splitk_regions": ([_I64, _P, _P], _I),
+    "kbn_debug_gemm_plan": ([_I64, _I64, _I64, _I, _I, _P], _I),
     "kbn_debug_silu_bf16": ([_P, _P, _I64, _P], _I),
 }
 

@@ -36,26 +36,45 @@ constexpr int64_t kPadZeroMaxK = KBN_PAD_ZERO_MAX_K;
 // Short K therefore stays unsplit (e.g. 128 x 12288 x 1536: 11.2 us data-
 // parallel against 20.0 us split in two), and long K takes fewer, longer
 // splits than a traffic-only model picks.
-static void plan_tail(Schedule& s, int64_t M, int KBT) {
-    const int occ = gemm_occupancy(s.bm, s.bn, s.stages, s.fuse_a);
+// Splits of the 64x64 tiles run at most this many K blocks: longer ones lose
+// to 64x128 when the GEMM quantizes 33-64 bf16 rows itself (1024 x 28672 at
+// 48 rows, 8 splits of 28 blocks: 27.5 us against 19.9 us; 1024 x 24576 at
+// 64 rows, 8 of 24: 25.4 against 20.1 us), while 14-16 block splits measured
+// faster on both paths (1024 x 28672 at 32 rows, 14 of 16: fp8 input 16.0 ->
+// 14.5 us, bf16 input 19.7 -> 18.9 us).
+constexpr int kNarrowMaxKb = 16;
+
+// Returns the modelled time of the whole plan (data-parallel waves plus the
+// tail).  The 64x64 tiles (narrow) stream fewer bytes per K block but not
+// proportionally faster: their split sweeps fit about 0.40 us per block
+// (41 KB of tile rows per us and workgroup), against 0.30 us at the 55 KB/us
+// of the larger tiles; they count one workgroup slot per CU, as measured,
+// and split K whenever a split fits (unsplit, they measured slower than
+// every split plan at K = 2048: 1024 x 2048 M = 64 above 7.7 us against
+// 7.4 us for three splits).
+static double plan_tail(Schedule& s, int64_t M, int KBT, bool allow_split = true, bool narrow = false) {
+    const int occ = narrow ? 1 : gemm_occupancy(s.bm, s.bn, s.stages, s.fuse_a);
     const int cus = cu_count();
     const int64_t slots = (int64_t)occ * cus;
     s.dp_tiles = s.tiles;
     s.splits = 1;
     s.kb_per_split = KBT;
-    const int64_t waves = s.tiles / slots, rem = s.tiles - waves * slots;
-    if (rem == 0 || KBT < 8) return;
     const double fill = 2.0;
-    const double t_block = (double)(s.bm + s.bn) * kRowB / 55e3;            // us per K block
+    const double t_block = (double)(s.bm + s.bn) * kRowB / (narrow ? 41e3 : 55e3);   // us per K block
+    const int64_t waves = s.tiles / slots, rem = s.tiles - waves * slots;
+    const double t_wave = (KBT + fill) * t_block;
+    if (rem == 0 || KBT < 8 || !allow_split) return (double)(waves + (rem > 0)) * t_wave;
     const double per_mb = 0.45;
     const double slab_mb = (double)std::min<int64_t>(M, s.bm) * s.bn * 4 / 1e6;   // one partial slab
-    double best = (KBT + fill) * t_block;                                    // the tail as one more data-parallel wave
+    // the tail as one more data-parallel wave (narrow tiles: only if no split fits)
+    double best = narrow ? 1e30 : t_wave;
     for (int sp = 2; sp <= 32 && sp <= KBT / 4; ++sp) {
         const int kbps = (KBT + sp - 1) / sp;
         const int ss = (KBT + kbps - 1) / kbps;
         const int64_t wgs = rem * ss;
         if (wgs > slots) break;
-        const bool fused = fused_split_sum(s.bm, M, ss, kbps);
+        const bool fused = fused_split_sum(s.bm, s.bn, M, ss, kbps);
+        if (narrow && (!fused || kbps > kNarrowMaxKb)) continue;   // narrow tiles: the measured regime
         const double fixed = fused ? 2.0 : 3.0, per_split = fused ? 0.4 : 0.2;
         const double cost = (kbps + fill) * t_block + fixed + per_split * ss + per_mb * slab_mb * ss * rem;
         if (cost < best - 1e-9) {
@@ -68,7 +87,44 @@ static void plan_tail(Schedule& s, int64_t M, int KBT) {
     if (s.splits > 1) {
         s.dp_tiles = waves * slots;
         s.ws_bytes = (int64_t)s.splits * rem * s.bm * s.bn * 4;
+    } else {
+        best = t_wave;
     }
+    return (double)waves * t_wave + best;
+}
+
+// Weight-streaming plans (M <= 64, UE8M0).  Narrow weights (at most
+// kNarrowTiles 64x128 tiles, N <= 4096) take 64x64 tiles (four stages, one
+// workgroup per CU): twice the tiles, so the same CUs stream with fewer K
+// splits per tile and half the slab per split.  Measured on MI355X
+// (HIP-graph replays, us per call, best 64x128 plan -> 64x64) at every
+// N in {1024, 2048, 3072, 4096}, K in {2048, 7168}, M in {1, 32, 64}, the
+// fp8-input GEMM was 2-25% faster: 2048 x 2048 M = 64 9.7 -> 7.4, M = 1
+// 7.3 -> 6.3; 4096 x 7168 M = 64 14.0 -> 11.3, M = 1 10.9 -> 9.5.  From 48
+// tiles (6144 columns) up, 64x128 measured as fast or faster (6144 x 7168
+// M = 1 12.6 against 13.7).
+constexpr int64_t kNarrowTiles = 32;
+
+static void plan_weight_stream(Schedule& s, int64_t M, int64_t N, int64_t K, bool allow_split, bool narrow_ok) {
+    const int KBT = (int)(K / kGroup);
+    s.bm = 64; s.bn = 128;
+    s.tiles = ((M + 63) / 64) * ((N + 127) / 128);
+    if (narrow_ok && allow_split && s.tiles <= kNarrowTiles) {
+        // 64x64 only with a split summed in the launch (the measured regime;
+        // long K at 49-64 rows, e.g. 1024 x 28672, finds none and keeps
+        // 64x128 with the separate reduction)
+        Schedule n = s;
+        n.bn = 64;
+        n.tiles = ((M + 63) / 64) * ((N + 63) / 64);
+        n.stages = 4;
+        plan_tail(n, M, KBT, true, true);
+        if (n.splits > 1) {
+            s = n;
+            return;
+        }
+    }
+    s.stages = s.tiles > cu_count() ? 3 : 4;
+    plan_tail(s, M, KBT, allow_split);
 }
 
 // Arrival counters of the fused split-K reduction, in a region of a static
@@ -303,10 +359,10 @@ static Schedule dense_schedule(int64_t M, int64_t N, int64_t K, int ue8m0, bool 
         // are more tiles than CUs; otherwise one per CU with a deeper
         // pipeline (4 stages) and the tail split over K over fewer, longer
         // workgroups (Llama-70B decode qkv / o / down: 8-20% faster than 3
-        // stages at two per CU; gate_up's 448 tiles: 6% slower)
-        s.bm = 64; s.bn = 128;
-        const int64_t t = ((M + 63) / 64) * ((N + 127) / 128);
-        s.stages = t > cu_count() ? 3 : 4;
+        // stages at two per CU; gate_up's 448 tiles: 6% slower); narrow
+        // weights may take 64x64 tiles (plan_weight_stream)
+        plan_weight_stream(s, M, N, K, allow_split, ue8m0 != 0);
+        return s;
     }
     s.tiles = ((M + s.bm - 1) / s.bm) * ((N + s.bn - 1) / s.bn);
     s.dp_tiles = s.tiles;
@@ -320,14 +376,13 @@ static Schedule dense_schedule(int64_t M, int64_t N, int64_t K, int ue8m0, bool 
 // kernel): the 64x128 weight-streaming tiles with 16, 32 or 64 bf16 A rows
 // of 256 B per stage (as M needs), 4 stages when the tiles do not fill the
 // CUs, else 3 (two workgroups per CU up to 32 rows: 66 / 78 KB).
+// The tiles and K partition are those of the fp8-input GEMM's plan for the
+// same shape (plan_weight_stream), so the results are bit-identical to
+// quant + fp8_gemm_nt.
 static Schedule bf16a_schedule(int64_t M, int64_t N, int64_t K, bool allow_split) {
     Schedule s;
-    s.bm = 64; s.bn = 128; s.fuse_a = M <= 16 ? 1 : M <= 32 ? 2 : 4;
-    s.tiles = ((M + 63) / 64) * ((N + 127) / 128);
-    s.stages = s.tiles > cu_count() ? 3 : 4;
-    s.dp_tiles = s.tiles;
-    s.kb_per_split = (int)(K / kGroup);
-    if (allow_split) plan_tail(s, M, (int)(K / kGroup));
+    s.fuse_a = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+    plan_weight_stream(s, M, N, K, allow_split, true);
     return s;
 }
 
@@ -339,6 +394,8 @@ static int dispatch_dense_roww(const GemmArgs& a, const Schedule& sc, int64_t K,
         if (sc.stages == 4) return launch_gemm<64, 128, 4, true, false, 4, 0, true>(a, sc, st, what);
         return launch_gemm<64, 128, 3, true, false, 4, 0, true>(a, sc, st, what);
     }
+    if (sc.bm == 64 && sc.bn == 64 && sc.stages == 4)
+        return launch_gemm<64, 64, 4, true, false, 4, 0, true>(a, sc, st, what);
     set_error("%s: no packed-scale kernel for %dx%d tiles", what, sc.bm, sc.bn);
     return 1;
 }
@@ -354,6 +411,9 @@ static int dispatch_dense(const GemmArgs& a, const Schedule& sc, int64_t K, hipS
     if (sc.bm == 64 && sc.bn == 128) {
         if (sc.stages == 4) return launch_gemm<64, 128, 4, kUe8m0, false>(a, sc, st, what);
         return launch_gemm<64, 128, 3, kUe8m0, false>(a, sc, st, what);
+    }
+    if constexpr (kUe8m0) {
+        if (sc.bm == 64 && sc.bn == 64 && sc.stages == 4) return launch_gemm<64, 64, 4, true, false>(a, sc, st, what);
     }
     set_error("%s: no kernel for %dx%d tiles", what, sc.bm, sc.bn);
     return 1;
@@ -584,12 +644,26 @@ extern "C" int64_t kbn_fp8_gemm_bf16a_workspace_bytes(int64_t M, int64_t N, int6
 // splits K into workgroups of at most 16 blocks within one wave of tiles
 // (2048 x 2048, o); long K per workgroup (qkv 22, down 56 blocks), more
 // tiles than CUs (gate_up: its 102 KB stage set drops to one workgroup per
-// CU) and unsplit plans stay with quant + GEMM.
+// CU) and unsplit plans stay with quant + GEMM.  On the 64x64 tiles of narrow
+// weights the fp8 GEMM gains more than the in-kernel quant, so 64 rows take
+// it only for K <= 4096 (4096 x 7168: 17.5 us, against 11.3 us of GEMM plus
+// the 3-5 us quant launch; 2048 x 2048: 9.8 us against 7.4 us plus the quant).
 extern "C" int kbn_fp8_gemm_bf16a_preferred(int64_t M, int64_t N, int64_t K) {
     if (M <= 0 || M > 64 || N <= 0 || K <= 0 || K % kGroup != 0 || N > 0x7FFFFFFFLL) return 0;
     if (M <= 32) return 1;
     const Schedule s = bf16a_schedule(M, N, K, true);
+    if (s.bn == 64 && K > 4096) return 0;
     return (s.tiles <= (int64_t)cu_count() && s.splits > 1 && s.kb_per_split <= 16) ? 1 : 0;
+}
+
+extern "C" int kbn_debug_gemm_plan(int64_t M, int64_t N, int64_t K, int scale_ue8m0, int bf16a, int64_t* out) {
+    KBN_CHECK_ARG(out && M > 0 && N > 0 && K > 0 && K % kGroup == 0 && (!bf16a || M <= 64),
+                  "debug_gemm_plan: bad arguments");
+    const Schedule s = bf16a ? bf16a_schedule(M, N, K, true) : dense_schedule(M, N, K, scale_ue8m0, true);
+    const int64_t v[9] = {s.bm, s.bn, s.stages, s.tiles, s.dp_tiles, s.splits, s.kb_per_split, s.fused ? 1 : 0,
+                          s.ws_bytes};
+    for (int i = 0; i < 9; ++i) out[i] = v[i];
+    return 0;
 }
 
 extern "C" int kbn_fp8_gemm_bf16a(const void* x_bf16, int64_t ld_x, float eps, const void* W, int64_t ldw,
@@ -630,6 +704,12 @@ extern "C" int kbn_fp8_gemm_bf16a(const void* x_bf16, int64_t ld_x, float eps, c
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     // rows of four each wavefront loads and quantizes: just enough for M
+    if (sc.bn == 64) {
+        KBN_CHECK_ARG(sc.stages == 4, "%s: no %d-stage kernel for 64x64 tiles", what, sc.stages);
+        if (sc.fuse_a == 1) return launch_gemm<64, 64, 4, true, false, 4, 1>(a, sc, st, what);
+        if (sc.fuse_a == 2) return launch_gemm<64, 64, 4, true, false, 4, 2>(a, sc, st, what);
+        return launch_gemm<64, 64, 4, true, false, 4, 4>(a, sc, st, what);
+    }
     if (sc.fuse_a == 1) {
         if (sc.stages == 4) return launch_gemm<64, 128, 4, true, false, 4, 1>(a, sc, st, what);
         return launch_gemm<64, 128, 3, true, false, 4, 1>(a, sc, st, what);

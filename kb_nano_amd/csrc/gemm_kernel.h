@@ -1104,8 +1104,9 @@ struct Schedule {
 
 // Split-K tails of the 64-row tiles summed by the split launch itself (no
 // reduction launch, about 3 us less host time per call): up to 32 rows
-// always, up to 48 rows when a tile has at most 4 splits, up to 64 rows when
-// it also has at most 24 K blocks per split.  The summing workgroup reads
+// always, up to 48 rows when a tile has at most 4 splits (8 for the 64x64
+// tiles, whose slabs are half as wide), up to 64 rows when it also has at
+// most 24 K blocks per split.  The summing workgroup reads
 // its tile's slabs alone, so more rows, deeper splits or long splits (whose
 // workgroups finish far apart) measure slower than the separate reduction
 // spread over 8-row strips (64 rows: 1024 x 28672 15.1 -> 17.1 us,
@@ -1113,9 +1114,10 @@ struct Schedule {
 // blocks: 10240 x 8192 21.9 -> 21.0 us at 49 rows, 8192 x 8192 19.9 -> 18.5
 // us at 49 rows and 20.2 -> 19.9 us at 64, 2048 x 2048 10.9 -> 10.3 us).
 constexpr int kFusedReduceRows = 32, kFusedShallowRows = 48, kFusedShallowSplits = 4, kFusedShortKb = 24;
-constexpr bool fused_split_sum(int bm, int64_t M, int splits, int kb_per_split) {
-    return bm <= 64 && (M <= kFusedReduceRows || (M <= kFusedShallowRows && splits <= kFusedShallowSplits) ||
-                        (M <= 64 && splits <= kFusedShallowSplits && kb_per_split <= kFusedShortKb));
+constexpr bool fused_split_sum(int bm, int bn, int64_t M, int splits, int kb_per_split) {
+    const int max_splits = bn <= 64 ? 2 * kFusedShallowSplits : kFusedShallowSplits;
+    return bm <= 64 && (M <= kFusedReduceRows || (M <= kFusedShallowRows && splits <= max_splits) ||
+                        (M <= 64 && splits <= max_splits && kb_per_split <= kFusedShortKb));
 }
 // Arrival counters of the fused split-K reduction for one launch on `st`, or
 // nullptr (then the separate reduction kernel runs); defined in gemm.hip.

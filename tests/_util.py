@@ -63,15 +63,16 @@ def assert_gemm_close(got_bf16: torch.Tensor, ref: np.ndarray, what: str = "") -
     return {"rel": rel, "cos": cos}
 
 
-def tile_cover(M: int, N: int, rng, bm: int = 64, bn: int = 128) -> tuple[np.ndarray, np.ndarray]:
+def tile_cover(M: int, N: int, rng, bm: int = 64, bn: int = 64) -> tuple[np.ndarray, np.ndarray]:
     """Rows and columns whose cross product puts at least one point inside
     every bm x bn block of an M x N output: one random row of each bm-row
     block and one random column of each bn-column block.  Every output tile
-    the GEMM planner uses (64x128, 128x128, 128x256, 256x256, and the tiles
-    of a split tail) is a union of such blocks, so each of them is sampled.
-    Added to those: the first and last row and column of the matrix, and
-    of the first and the last tile at each tile size (64, 128 and 256 rows;
-    128 and 256 columns), i.e. the edges of every edge tile."""
+    the GEMM planner uses (64x64, 64x128, 128x128, 128x256, 256x192,
+    256x256, and the tiles of a split tail) is a union of such blocks, so
+    each of them is sampled.  Added to those: the first and last row and
+    column of the matrix, and of the first and the last tile at each tile
+    size (64, 128 and 256 rows; 64, 128 and 256 columns), i.e. the edges of
+    every edge tile."""
     def pick(n, b, sizes):
         nb = -(-n // b)
         out = [i * b + int(rng.integers(0, min(b, n - i * b))) for i in range(nb)]
@@ -79,7 +80,7 @@ def tile_cover(M: int, N: int, rng, bm: int = 64, bn: int = 128) -> tuple[np.nda
             last = ((n - 1) // t) * t
             out += [0, min(t, n) - 1, last, n - 1, max(last - 1, 0)]
         return np.unique(np.clip(np.array(out, dtype=np.int64), 0, n - 1))
-    return pick(M, bm, (64, 128, 256)), pick(N, bn, (128, 256))
+    return pick(M, bm, (64, 128, 256)), pick(N, bn, (64, 128, 256))
 
 
 def assert_all_written(D: torch.Tensor, what: str = "") -> None:

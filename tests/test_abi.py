@@ -560,3 +560,45 @@ def test_packed_gemm_rejects_bad_scales_without_device():
     assert rc == 1 and "strides" in _err()
     rc = L.kbn_fp8_gemm_nt_packed_ws(p, 256, None, 1, 64, p, 256, p, 1, 128, p, 128, 64, 128, 256, None, 0, None)
     assert rc == 1 and "null scale" in _err()
+
+
+def _plan(L, M, N, K, ue8m0=1, bf16a=0):
+    import numpy as np
+    out = np.zeros(9, dtype=np.int64)
+    assert L.kbn_debug_gemm_plan(M, N, K, ue8m0, bf16a, out.ctypes.data) == 0, _err()
+    return out
+
+
+def test_weight_stream_plans_narrow_and_wide():
+    """The tile planner (no GPU: 256 CUs assumed).  Weight-streaming shapes
+    (M <= 64) with narrow weights (N <= 4096) take 64x64 tiles with K split
+    and summed in the split launch; wider weights keep the 64x128 tiles
+    (Llama-70B decode shapes: qkv 3 splits, o and down 4, gate_up
+    data-parallel); the bf16-activation GEMM plans exactly as the fp8 GEMM
+    (its results are bit-identical to quant + GEMM); the FP32 contract keeps
+    64x128; the workspace the plan writes is what the entry point asks for."""
+    import numpy as np
+    from kb_nano_amd._lib import lib
+    L = lib()
+    for M in (1, 8, 32, 48, 64):
+        for N, K in ((2048, 2048), (1024, 7168), (4096, 7168), (200, 1152), (4032, 2048)):
+            p = _plan(L, M, N, K)
+            assert (p[0], p[1], p[2]) == (64, 64, 4) and p[5] > 1 and p[7] == 1, (M, N, K, p)
+            assert p[3] == -(-N // 64) and p[4] == 0 and p[5] * p[6] >= K // 128 > (p[5] - 1) * p[6]
+            assert p[8] == p[5] * p[3] * 64 * 64 * 4 == L.kbn_fp8_gemm_nt_workspace_bytes(M, N, K, 1)
+            assert np.array_equal(p, _plan(L, M, N, K, bf16a=1))
+            assert _plan(L, M, N, K, ue8m0=0)[1] == 128
+        for N, K, splits in ((10240, 8192, 3), (8192, 8192, 4), (8192, 28672, 4), (57344, 8192, 1)):
+            p = _plan(L, M, N, K)
+            assert (p[0], p[1], p[5]) == (64, 128, splits), (M, N, K, p)
+            assert np.array_equal(p, _plan(L, M, N, K, bf16a=1))
+    # config 1 takes the one-launch bf16-activation GEMM at 64 rows; long K on
+    # 64x64 tiles does not (quant + GEMM measured faster there)
+    assert L.kbn_fp8_gemm_bf16a_preferred(64, 2048, 2048) == 1
+    assert L.kbn_fp8_gemm_bf16a_preferred(64, 4096, 7168) == 0
+    assert L.kbn_fp8_gemm_bf16a_preferred(32, 4096, 7168) == 1
+    # larger M: the 128x128 and 256x256 tiles, unchanged
+    assert tuple(_plan(L, 128, 24576, 1536)[:2]) == (128, 128)
+    assert tuple(_plan(L, 4096, 7168, 18432)[:2]) == (256, 256)
+    assert L.kbn_debug_gemm_plan(65, 2048, 2048, 1, 1, np.zeros(9, np.int64).ctypes.data) == 1
+    assert "bad arguments" in _err()

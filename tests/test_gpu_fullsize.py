@@ -180,7 +180,7 @@ def test_fp8_linear_cfg5_every_tile(gpu_device, name, N, K):
     where the plan prefers it, the GEMM over bf16 activations), and the
     bf16-activation GEMM itself.  Each output is prefilled with NaN and must
     come back entirely written and finite, and each is compared with oracle
-    quant + oracle GEMM at a point inside every 64x128 block (every tile of
+    quant + oracle GEMM at a point inside every 64x64 block (every tile of
     every plan, split tails included) plus the edge rows and columns."""
     from kb_nano_amd import Fp8Linear, _ops, synthetic
     from kb_nano_amd.fp8_linear import _alloc_colmajor_scale

@@ -86,7 +86,7 @@ def test_gemm_dsv3_every_tile(gpu_device, name, N, K, M):
     recipe (seed 2 for the weights, 20 for the activations).  The output is
     prefilled with NaN and must come back entirely written and finite; the
     oracle is evaluated on a row set x column set that puts a point inside
-    every 64x128 block of the output (so inside every tile of every plan,
+    every 64x64 block of the output (so inside every tile of every plan,
     split-tail tiles included) plus the first and last rows and columns of
     the edge tiles."""
     from kb_nano_amd import _ops, synthetic
@@ -625,7 +625,7 @@ def test_gemm_mixed_256_192_plan(gpu_device, M, N, K):
     tiles when they fill one wave better).  The 96-column wave tiles straddle 128-row weight
     scale blocks, so each 32-column fragment takes its own block scale.
     Ragged M, NaN-prefilled output entirely written, a point of every
-    64x128 block against the float64 oracle, non-power-of-two weight scales
+    64x64 block against the float64 oracle, non-power-of-two weight scales
     rounded up under the UE8M0 contract."""
     from tests._util import assert_all_written, tile_cover
     qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=M + N + K + 1)
@@ -636,3 +636,84 @@ def test_gemm_mixed_256_192_plan(gpu_device, M, N, K):
     ref = oracle.gemm_nt_sample(qa, sa, qw, sw, rows=rows, cols=cols, ue8m0=True)
     got = D[torch.from_numpy(rows).to(gpu_device)][:, torch.from_numpy(cols).to(gpu_device)]
     assert_gemm_close(got, ref, f"mixed plan {M}x{N}x{K}")
+
+
+def _plan(M, N, K, bf16a=False):
+    import ctypes
+    from kb_nano_amd._lib import lib
+    out = np.zeros(9, dtype=np.int64)
+    assert lib().kbn_debug_gemm_plan(M, N, K, 1, int(bf16a), out.ctypes.data) == 0
+    return out
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 2048, 2048), (64, 2048, 2048), (17, 1024, 7168), (64, 4096, 7168),
+                                   (33, 200, 1152), (48, 3072, 2048), (8, 4032, 7168)])
+def test_gemm_narrow_64x64_plans(gpu_device, M, N, K):
+    """Weight-streaming shapes with narrow weights (N <= 4096, M <= 64) run
+    64x64 tiles with K split and summed in the split launch.  Every 64x64
+    block of the NaN-prefilled output is written and matches the float64
+    oracle; the packed per-row scales, the allocation-free entry point and
+    graph replays give the same bits as the workspace entry point, and the
+    bf16-activation GEMM gives the bits of quant + GEMM."""
+    import ctypes
+    from kb_nano_amd import _ops
+    from kb_nano_amd._lib import lib
+    from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
+    from tests._util import assert_all_written, tile_cover
+    print(f"narrow {M}x{N}x{K}", flush=True)
+    plan = _plan(M, N, K)
+    assert plan[0] == 64 and plan[1] == 64 and plan[5] > 1 and plan[7] == 1, plan
+    assert np.array_equal(plan, _plan(M, N, K, bf16a=True))
+    x = seeded_bf16((M, K), seed=M + K).to(gpu_device)
+    A = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=gpu_device)
+    sA = _alloc_colmajor_scale(M, K // 128, gpu_device)
+    _ops.per_token_group_quant_fp8(x, A, sA)
+    qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=N + K)
+    W = to_fp8(qw, gpu_device)
+    sW = torch.from_numpy(sw).to(gpu_device)
+    D = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu_device)
+    _ops.fp8_gemm_nt(A, sA, W, sW, D, use_ue8m0=True)
+    torch.cuda.synchronize()
+    assert_all_written(D, f"narrow {M}x{N}x{K}")
+    rows, cols = tile_cover(M, N, np.random.default_rng(M + N))
+    ref = oracle.gemm_nt_sample(fp8_codes(A), sA.cpu().numpy(), qw, sw, rows=rows, cols=cols, ue8m0=True)
+    got = D[torch.from_numpy(rows).to(gpu_device)][:, torch.from_numpy(cols).to(gpu_device)]
+    assert_gemm_close(got, ref, f"narrow {M}x{N}x{K}")
+    base = bf16_bits(D)
+    # bf16 activations, quantized inside the GEMM: the same bits
+    D2 = torch.full_like(D, float("nan"))
+    _ops.fp8_gemm_bf16a(x, W, sW, D2)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(D2), base), "bf16a != quant + GEMM"
+    # packed per-row UE8M0 exponents of the same (power-of-two) block scales
+    packed = _ops.pack_ue8m0_weight_scales(sW, N, K)
+    D3 = torch.full_like(D, float("nan"))
+    _ops.fp8_gemm_nt(A, sA, W, packed, D3)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(D3), base), "packed scales != block scales"
+    # the allocation-free entry point
+    D4 = torch.full_like(D, float("nan"))
+    st = torch.cuda.current_stream().cuda_stream
+    rc = lib().kbn_fp8_gemm_nt_noalloc(A.data_ptr(), K, sA.data_ptr(), sA.stride(0), sA.stride(1), W.data_ptr(), K,
+                                       sW.data_ptr(), sW.stride(0), D4.data_ptr(), N, M, N, K, 1, st)
+    assert rc == 0, lib().kbn_last_error()
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(D4), base), "noalloc != workspace entry point"
+    # graph replays (the split launch's arrival counters under capture)
+    D5 = torch.full_like(D, float("nan"))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        _ops.fp8_gemm_nt(A, sA, W, sW, D5, use_ue8m0=True)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _ops.fp8_gemm_nt(A, sA, W, sW, D5, use_ue8m0=True)
+    for _ in range(3):
+        D5.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bf16_bits(D5), base), "graph replay"
+        _ops.fp8_gemm_nt(A, sA, W, sW, D4, use_ue8m0=True)   # eager work between replays
+        torch.cuda.synchronize()
+    del g

@@ -12,7 +12,7 @@ import torch
 import oracle
 from tests._util import assert_all_written, assert_gemm_close, quantized_gemm_inputs, tile_cover
 
-TILES = [(64, 128), (128, 128), (128, 256), (256, 256)]
+TILES = [(64, 64), (64, 128), (128, 128), (128, 256), (256, 256)]
 SHAPES = [(1, 10240), (8, 57344), (64, 8192), (128, 24576), (4096, 7168), (4096, 36864), (77, 203), (300, 1000)]
 
 
