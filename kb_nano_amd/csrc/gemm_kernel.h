@@ -400,9 +400,10 @@ gemm_bs_kernel(const GemmArgs a) {
     static_assert(!kGrouped || BM == 128, "grouped tiles cover one 128-row block of the contiguous layout");
 
     int tm, tn, trel = 0, split = 0;
-    // MoE tiles walk 8 tile rows per column group: an expert's row tiles then
-    // share its weight panel in L2 more often (cfg4: 1% faster than 4; dense
-    // tiles keep 4, which the split reduction's tile order also assumes)
+    // MoE tiles walk column groups of kMoeGroupM row tiles dealt over the
+    // XCDs (tile_coords_dealt), so an expert's row tiles meet its weight panel
+    // in one L2; dense tiles walk groups of 4 row tiles, which the split
+    // reduction's tile order also assumes
     if constexpr (kGrouped || kSorted) {
         static_assert(!kSplitK, "MoE layouts run data-parallel");
         if (!tile_coords_dealt<kMoeGroupM>(a.tiles_m, a.tiles_n, tm, tn)) return;
