@@ -706,14 +706,22 @@ def test_gemm_narrow_64x64_plans(gpu_device, M, N, K):
     with torch.cuda.stream(side):
         _ops.fp8_gemm_nt(A, sA, W, sW, D5, use_ue8m0=True)
     torch.cuda.current_stream().wait_stream(side)
+    D6 = torch.full_like(D, float("nan"))
+    with torch.cuda.stream(side):
+        _ops.fp8_gemm_bf16a(x, W, sW, D6)
+    torch.cuda.current_stream().wait_stream(side)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         _ops.fp8_gemm_nt(A, sA, W, sW, D5, use_ue8m0=True)
+        _ops.fp8_gemm_bf16a(x, W, sW, D6)
     for _ in range(3):
         D5.fill_(float("nan"))
+        D6.fill_(float("nan"))
         g.replay()
         torch.cuda.synchronize()
         assert np.array_equal(bf16_bits(D5), base), "graph replay"
+        assert np.array_equal(bf16_bits(D6), base), "graph replay, bf16 activations"
         _ops.fp8_gemm_nt(A, sA, W, sW, D4, use_ue8m0=True)   # eager work between replays
+        _ops.fp8_gemm_bf16a(x, W, sW, D2)
         torch.cuda.synchronize()
     del g
