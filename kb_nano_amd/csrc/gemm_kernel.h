@@ -981,20 +981,23 @@ gemm_bs_kernel(const GemmArgs a) {
         const int h = lane >> 5;
         const int ncol = n0 + wn * TN + 8 * h;
         const bool vec = a.vec_store && (n0 + BN <= a.N || a.N % 8 == 0);
-        // 256-row dense tiles: the fragments' natural stores write each
-        // 128-B line of D as four 32-B pieces (32 rows x 32 B per
-        // instruction), and the tiles of a wave of workgroups all end at once.
-        // Instead each wavefront parks its bf16 block in the (now idle) LDS
-        // stages, row-major with each row's 16-B chunks rotated by the row
-        // index (conflict-spreading), reads it back by whole rows and stores
-        // full lines, non-temporal (4 rows x 256 B per instruction for 128
-        // columns, 8 x 128 B for 64, 4 x 192 B for 96).  Bit-identical;
-        // q_b M = 4096 167 -> 160 us, gate_up 836 -> 825 us, 1024 x 7168 x 4096
-        // 56.4 -> 54.3 us (one box, interleaved runs).  With the natural
-        // partial-line stores the non-temporal hint was much slower (q_b
-        // 157 -> 284 us): those pieces must merge in L2.
-        constexpr bool kLdsEpi = BM == 256 && !kGrouped && !kSorted && !kSplitK &&
-                                 (TN == 128 || TN == 96 || TN == 64) && BM * BN * 2 <= kStages * kStage;
+        // 256-row dense tiles and the 128-row MoE tiles: the fragments'
+        // natural stores write each 128-B line of D as four 32-B pieces (32
+        // rows x 32 B per instruction), and the tiles of a wave of workgroups
+        // all end at once.  Instead each wavefront parks its bf16 block in the
+        // (now idle) LDS stages, row-major with each row's 16-B chunks rotated
+        // by the row index (conflict-spreading), reads it back by whole rows
+        // and stores full lines, non-temporal (4 rows x 256 B per instruction
+        // for 128 columns, 8 x 128 B for 64, 4 x 192 B for 96).  Bit-identical;
+        // one box, interleaved runs: q_b M = 4096 167 -> 160 us, gate_up 836 ->
+        // 825 us; cfg4 grouped down 1007 -> 935 us, gate_up 1965 -> 1929 us
+        // (UE8M0), layer 3165 -> 3112 us.  With the natural partial-line
+        // stores the non-temporal hint was much slower (q_b 157 -> 284 us):
+        // those pieces must merge in L2.  The 64- and 128-row weight-streaming
+        // tiles keep the direct stores: their outputs are small and their
+        // calls short.
+        constexpr bool kLdsEpi = ((BM == 256 && !kGrouped && !kSorted) || ((kGrouped || kSorted) && BM == 128)) &&
+                                 !kSplitK && (TN == 128 || TN == 96 || TN == 64) && BM * BN * 2 <= kStages * kStage;
         if (kLdsEpi && vec) {
             constexpr int kCh = TN / 8;                            // 16-B chunks per wavefront row
             constexpr int kRowB2 = TN * 2;                         // bytes per wavefront row
@@ -1021,6 +1024,13 @@ gemm_bs_kernel(const GemmArgs a) {
                     }
                 }
             }
+            // grouped: rows of another expert (padding) are not stored
+            uint64_t row_mask = ~0ull;
+            if constexpr (kGrouped) {
+                static_assert(!kGrouped || TM <= 64, "one mask bit per wavefront row");
+                const int r = m0 + wm * TM + lane;
+                row_mask = __ballot(lane < TM && r < a.M && a.expert_ids[r] == expert);
+            }
             wait_lds();
             const bool active = lane < kRowsPer * kCh;             // 96 columns: 48 lanes of 64 store
             const int cl = active ? lane % kCh : 0, rsub = active ? lane / kCh : 0;
@@ -1030,7 +1040,18 @@ gemm_bs_kernel(const GemmArgs a) {
             for (int it = 0; it < TM / kRowsPer; ++it) {
                 const int rl = it * kRowsPer + rsub;
                 const u32x4 v = *reinterpret_cast<const u32x4*>(reg + rl * kRowB2 + ((cl + rl) % kCh) * 16);
-                const int voff = col_ok ? (wm * TM + rl) * (int)a.ldd * 2 + col * 2 : kOob;
+                int roff;
+                if constexpr (kSorted) {
+                    // the output row (routed pair) of wavefront row rl, held by
+                    // lane rl % 32 for fragment rl / 32 (rl / 32 is it / 8)
+                    const int orow = __shfl(out_row[(it * kRowsPer) / 32], rl & 31);
+                    roff = orow >= 0 ? orow * (int)a.ldd * 2 : kOob;
+                } else if constexpr (kGrouped) {
+                    roff = ((row_mask >> rl) & 1ull) ? (wm * TM + rl) * (int)a.ldd * 2 : kOob;
+                } else {
+                    roff = (wm * TM + rl) * (int)a.ldd * 2;
+                }
+                const int voff = col_ok && roff != kOob ? roff + col * 2 : kOob;
                 __builtin_amdgcn_raw_buffer_store_b128(v, dD, voff, 0, kNt);
             }
         } else if (vec) {
