@@ -51,6 +51,19 @@ int kbn_per_token_group_quant_fp8(const void* x_bf16, int64_t M, int64_t K, int6
                                   float eps, int use_ue8m0, void* stream);
 
 /*
+ * The same quantization of fp16 or fp32 rows (and bf16): the reference's
+ * kernel loads any float input and widens it to fp32 before the group
+ * absmax (tasks/baseline/L1/fp8_linear.py:197), which is exact for these
+ * types, so each group's codes and scale are those of the fp32 values.
+ *   x_dtype 0 bf16, 1 fp16, 2 fp32; x rows 16-byte aligned, ld_x % 8 == 0
+ *   (elements); every other argument as kbn_per_token_group_quant_fp8.
+ */
+int kbn_per_token_group_quant_fp8_typed(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld_x,
+                                        void* q_fp8, int64_t ld_q, float* scale,
+                                        int64_t s_stride_m, int64_t s_stride_g,
+                                        float eps, int use_ue8m0, void* stream);
+
+/*
  * Fused SiLU*Mul + per-token-group FP8 quantization.
  * Replaces the Triton kernel _silu_mul_per_token_group_quant_fp8_colmajor and
  * SiluMulQuantFp8.forward (tasks/baseline/L1/silu_mul_quant_fp8.py:23-76, :87-143).

@@ -22,6 +22,7 @@ SIGNATURES = {
     "kbn_abi_version": ([], _I),
     "kbn_device_arch": ([_I, ctypes.c_char_p, _I], _I),
     "kbn_per_token_group_quant_fp8": ([_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _F, _I, _P], _I),
+    "kbn_per_token_group_quant_fp8_typed": ([_P, _I, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _F, _I, _P], _I),
     "kbn_silu_mul_quant_fp8": ([_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _F, _I, _P], _I),
     "kbn_silu_mul_quant_fp8_rows": ([_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _F, _I, _P, _P], _I),
     "kbn_fp8_gemm_nt": ([_P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _P], _I),

@@ -38,6 +38,8 @@ _capturing = torch._C._cuda_isCurrentStreamCapturing
 _GFX950_DEVICES: set = set()
 _BF16 = torch.bfloat16
 _F32 = torch.float32
+# input dtype codes of kbn_per_token_group_quant_fp8_typed
+_QUANT_IN = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -87,8 +89,10 @@ def is_e8m0_used() -> bool:
 
 def per_token_group_quant_fp8(x: torch.Tensor, out_fp8: torch.Tensor, out_scale: torch.Tensor,
                               use_ue8m0: bool = True, eps: float = QUANT_EPS) -> None:
-    """1x128 quant of bf16 ``x [M,K]`` into ``out_fp8 [M,K]`` and ``out_scale
-    [M,K/128]`` (any strides for the scales, e.g. column-major)."""
+    """1x128 quant of ``x [M,K]`` into ``out_fp8 [M,K]`` and ``out_scale
+    [M,K/128]`` (any strides for the scales, e.g. column-major).  ``x`` is
+    bf16, or fp16 / fp32 as the reference's kernel also takes (its values
+    widened to fp32 exactly, tasks/baseline/L1/fp8_linear.py:197)."""
     what = "per_token_group_quant_fp8"
     idx = x.get_device()
     shape = x.shape
@@ -96,7 +100,8 @@ def per_token_group_quant_fp8(x: torch.Tensor, out_fp8: torch.Tensor, out_scale:
             or out_scale.get_device() != idx):
         _dev_check(what, x, out_fp8, out_scale)
     if x.dtype is not _BF16 or out_fp8.dtype is not FP8 or out_scale.dtype is not _F32:
-        _dtype_check(what, x, torch.bfloat16, "input")
+        if x.dtype not in _QUANT_IN:
+            raise TypeError(f"{what}: input must be bfloat16, float16 or float32, got {x.dtype}")
         _dtype_check(what, out_fp8, FP8, "output_fp8")
         _dtype_check(what, out_scale, torch.float32, "output_scale")
     if len(shape) != 2 or out_fp8.shape != shape:
@@ -109,9 +114,14 @@ def per_token_group_quant_fp8(x: torch.Tensor, out_fp8: torch.Tensor, out_scale:
     xs, qs, ss = x.stride(), out_fp8.stride(), out_scale.stride()
     if xs[1] != 1 or qs[1] != 1:
         raise ValueError(f"{what}: input and output rows must be contiguous")
-    rc = lib().kbn_per_token_group_quant_fp8(
-        x.data_ptr(), M, K, xs[0], out_fp8.data_ptr(), qs[0], out_scale.data_ptr(), ss[0], ss[1],
-        float(eps), 1 if use_ue8m0 else 0, _raw_stream(idx))
+    if x.dtype is _BF16:
+        rc = lib().kbn_per_token_group_quant_fp8(
+            x.data_ptr(), M, K, xs[0], out_fp8.data_ptr(), qs[0], out_scale.data_ptr(), ss[0], ss[1],
+            float(eps), 1 if use_ue8m0 else 0, _raw_stream(idx))
+    else:
+        rc = lib().kbn_per_token_group_quant_fp8_typed(
+            x.data_ptr(), _QUANT_IN[x.dtype], M, K, xs[0], out_fp8.data_ptr(), qs[0], out_scale.data_ptr(),
+            ss[0], ss[1], float(eps), 1 if use_ue8m0 else 0, _raw_stream(idx))
     if rc:
         check(rc, what)
 

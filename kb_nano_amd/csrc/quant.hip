@@ -62,7 +62,7 @@ constexpr int kXcds = 8;             // MI355X: workgroups are dealt round-robin
 constexpr int kLineRows = 32;        // rows sharing one 128-B line of column-major scales
 
 struct QuantArgs {
-    const uint16_t* x;      // bf16 input rows
+    const uint16_t* x;      // input rows: bf16 (fp16 or fp32 for the plain quant's kIn)
     int64_t ld_x;           // row stride (elements)
     int64_t up_off;         // SiLU kernel: column offset of the up half
     uint8_t* q;
@@ -183,6 +183,56 @@ __device__ __forceinline__ float quant8_store(const uint32_t (&w)[4], float eps,
     return sc;
 }
 
+// Input element types of the plain quant (the reference's Triton kernel loads
+// any float input and widens it to fp32, tasks/baseline/L1/fp8_linear.py:197).
+enum QuantIn : int { kInBf16 = 0, kInF16 = 1, kInF32 = 2 };
+
+// The 8 values of this lane as fp32 (exact widening): from four words of
+// fp16 pairs, or from two 16-B chunks of fp32.
+__device__ __forceinline__ void widen_f16(const u32x4& x, float (&v)[8]) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const h2 h = __builtin_bit_cast(h2, w[i]);
+        v[2 * i] = (float)h.x;
+        v[2 * i + 1] = (float)h.y;
+    }
+}
+__device__ __forceinline__ void widen_f32(const u32x4& x0, const u32x4& x1, float (&v)[8]) {
+    v[0] = __uint_as_float(x0.x); v[1] = __uint_as_float(x0.y);
+    v[2] = __uint_as_float(x0.z); v[3] = __uint_as_float(x0.w);
+    v[4] = __uint_as_float(x1.x); v[5] = __uint_as_float(x1.y);
+    v[6] = __uint_as_float(x1.z); v[7] = __uint_as_float(x1.w);
+}
+
+// Quantize 8 fp32 values of this lane (16 lanes per group), the fp16 and
+// fp32 inputs' path: the bf16 general path above on the widened values.
+// The absmax ignores NaN (fmaxf), an infinity gives an infinite scale;
+// UE8M0 codes are x times the exact reciprocal of the power-of-two scale
+// (x / s exactly, but where it falls below fp32's normal range, far under
+// e4m3's smallest subnormal, so the code is the same), FP32-contract codes
+// the correctly rounded x / s, both converted by the hardware RNE.
+template <bool kUe8m0>
+__device__ __forceinline__ float quant8f_store(const float (&v)[8], float eps, int sub, uint8_t* __restrict__ qptr) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = __uint_as_float(row16_max_u32(__float_as_uint(amax)));
+    amax = fmaxf(amax, eps);
+    const float sc = kUe8m0 ? ue8m0_ceil_div448(amax) : amax / kFp8Max;
+    uint32_t lo, hi;
+    if constexpr (kUe8m0) {
+        lo = pack4_e4m3_ue8m0_general(v[0], v[1], v[2], v[3], sc);
+        hi = pack4_e4m3_ue8m0_general(v[4], v[5], v[6], v[7], sc);
+    } else {
+        lo = pack4_e4m3(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
+        hi = pack4_e4m3(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);
+    }
+    *reinterpret_cast<u32x2*>(qptr + sub * 8) = u32x2{lo, hi};
+    return sc;
+}
+
 // One persistent kernel for both ops.  Each XCD owns a contiguous slice of
 // rows (a multiple of 32, so every 128-B line of column-major scales is
 // written through one L2 and merges there); inside the slice the XCD's
@@ -194,8 +244,10 @@ __device__ __forceinline__ float quant8_store(const uint32_t (&w)[4], float eps,
 // XCDs in blocks of 32 (block b to XCD b % 8) instead of contiguous slices:
 // skipped rows cluster (an expert segment's padding, the layout's unused
 // tail), and contiguous slices would leave whole XCDs without work.
-template <bool kSilu, bool kUe8m0, bool kRows = false>
+template <bool kSilu, bool kUe8m0, bool kRows = false, int kIn = kInBf16>
 __global__ __launch_bounds__(kThreads) void group_quant_kernel(const QuantArgs a) {
+    static_assert(kIn == kInBf16 || (!kSilu && !kRows), "the SiLU and row-skipping kernels take bf16 input");
+    constexpr int kEb = kIn == kInF32 ? 4 : 2;   // input bytes per element
     __shared__ __attribute__((aligned(16))) uint16_t lut[kSilu ? 65536 : 8];
     if constexpr (kSilu) {  // stage the bf16 SiLU table: 8192 x 16 B
         const u32x4* src = reinterpret_cast<const u32x4*>(kSiluLut);
@@ -243,9 +295,17 @@ __global__ __launch_bounds__(kThreads) void group_quant_kernel(const QuantArgs a
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u)
             if (cu[u].row < row_end && !(kRows && skip[kRows ? u : 0])) {
-                const uint16_t* p = a.x + (int64_t)grow(cu[u].row) * a.ld_x + (int64_t)cu[u].g * kGroup + sub * 8;
-                xa[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-                if constexpr (kSilu) xb[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + a.up_off));
+                if constexpr (kIn == kInBf16) {
+                    const uint16_t* p = a.x + (int64_t)grow(cu[u].row) * a.ld_x + (int64_t)cu[u].g * kGroup + sub * 8;
+                    xa[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+                    if constexpr (kSilu) xb[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + a.up_off));
+                } else {
+                    // fp16: 16 B, fp32: 32 B (two chunks) per lane
+                    const uint8_t* p = reinterpret_cast<const uint8_t*>(a.x) +
+                                       ((int64_t)cu[u].row * a.ld_x + (int64_t)cu[u].g * kGroup + sub * 8) * kEb;
+                    xa[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+                    if constexpr (kIn == kInF32) xb[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + 16));
+                }
             }
         c.advance(a.step_q, a.step_r, a.G);
         if constexpr (kRows) {
@@ -262,6 +322,15 @@ __global__ __launch_bounds__(kThreads) void group_quant_kernel(const QuantArgs a
             if (cu[u].row >= row_end) break;  // uniform over the group's 16 lanes; rows grow with u
             if constexpr (kRows)
                 if (skip[u]) continue;        // a skipped row (uniform over the group's lanes)
+            if constexpr (kIn != kInBf16) {
+                float v[8];
+                if constexpr (kIn == kInF16) widen_f16(xa[u], v);
+                else widen_f32(xa[u], xb[u], v);
+                const int64_t r = cu[u].row;
+                const float sc = quant8f_store<kUe8m0>(v, a.eps, sub, a.q + r * a.ld_q + (int64_t)cu[u].g * kGroup);
+                if (sub == 0) a.s[r * a.s_sm + (int64_t)cu[u].g * a.s_sg] = sc;
+                continue;
+            }
             uint32_t w[4];
             if constexpr (kSilu) {
                 w[0] = silu_mul_pair(lut, xa[u].x, xb[u].x);
@@ -317,23 +386,44 @@ static int check_quant_args(const char* what, const void* x, int64_t M, int64_t 
     return 0;
 }
 
-extern "C" int kbn_per_token_group_quant_fp8(const void* x_bf16, int64_t M, int64_t K, int64_t ld_x,
-                                             void* q_fp8, int64_t ld_q, float* scale, int64_t s_stride_m,
-                                             int64_t s_stride_g, float eps, int use_ue8m0, void* stream) {
-    const char* what = "per_token_group_quant_fp8";
-    if (int rc = check_quant_args(what, x_bf16, M, K, ld_x, q_fp8, ld_q, scale)) return rc;
+static int quant_typed(const char* what, const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld_x,
+                       void* q_fp8, int64_t ld_q, float* scale, int64_t s_stride_m, int64_t s_stride_g, float eps,
+                       int use_ue8m0, void* stream) {
+    KBN_CHECK_ARG(x_dtype == kInBf16 || x_dtype == kInF16 || x_dtype == kInF32,
+                  "%s: input dtype code %d (0 bf16, 1 fp16, 2 fp32)", what, x_dtype);
+    if (int rc = check_quant_args(what, x, M, K, ld_x, q_fp8, ld_q, scale)) return rc;
     if (M == 0 || K == 0) return 0;
     KBN_CHECK_ARG(ld_x >= K, "%s: input row stride smaller than K", what);
-    QuantArgs a{(const uint16_t*)x_bf16, ld_x, 0, (uint8_t*)q_fp8, ld_q, scale, s_stride_m, s_stride_g,
+    QuantArgs a{(const uint16_t*)x, ld_x, 0, (uint8_t*)q_fp8, ld_q, scale, s_stride_m, s_stride_g,
                 (int)M, (int)(K / kGroup), 0, 0, 0, eps};
     const int blocks = plan(a, KBN_QUANT_PER_CU, kUnrollOf<false>);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (use_ue8m0)
-        group_quant_kernel<false, true><<<blocks, kThreads, 0, st>>>(a);
-    else
-        group_quant_kernel<false, false><<<blocks, kThreads, 0, st>>>(a);
+    if (x_dtype == kInBf16) {
+        if (use_ue8m0) group_quant_kernel<false, true><<<blocks, kThreads, 0, st>>>(a);
+        else group_quant_kernel<false, false><<<blocks, kThreads, 0, st>>>(a);
+    } else if (x_dtype == kInF16) {
+        if (use_ue8m0) group_quant_kernel<false, true, false, kInF16><<<blocks, kThreads, 0, st>>>(a);
+        else group_quant_kernel<false, false, false, kInF16><<<blocks, kThreads, 0, st>>>(a);
+    } else {
+        if (use_ue8m0) group_quant_kernel<false, true, false, kInF32><<<blocks, kThreads, 0, st>>>(a);
+        else group_quant_kernel<false, false, false, kInF32><<<blocks, kThreads, 0, st>>>(a);
+    }
     KBN_CHECK_LAUNCH(what);
     return 0;
+}
+
+extern "C" int kbn_per_token_group_quant_fp8(const void* x_bf16, int64_t M, int64_t K, int64_t ld_x,
+                                             void* q_fp8, int64_t ld_q, float* scale, int64_t s_stride_m,
+                                             int64_t s_stride_g, float eps, int use_ue8m0, void* stream) {
+    return quant_typed("per_token_group_quant_fp8", x_bf16, kInBf16, M, K, ld_x, q_fp8, ld_q, scale, s_stride_m,
+                       s_stride_g, eps, use_ue8m0, stream);
+}
+
+extern "C" int kbn_per_token_group_quant_fp8_typed(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld_x,
+                                                   void* q_fp8, int64_t ld_q, float* scale, int64_t s_stride_m,
+                                                   int64_t s_stride_g, float eps, int use_ue8m0, void* stream) {
+    return quant_typed("per_token_group_quant_fp8_typed", x, x_dtype, M, K, ld_x, q_fp8, ld_q, scale, s_stride_m,
+                       s_stride_g, eps, use_ue8m0, stream);
 }
 
 extern "C" int kbn_silu_mul_quant_fp8(const void* in_bf16, int64_t M, int64_t N_half, int64_t ld_in, void* q_fp8,

@@ -147,7 +147,8 @@ class Fp8Linear(nn.Module):
             output = o_buf if o_buf.shape[0] == M else o_buf[:M]
             _ops.per_token_group_quant_fp8(x2, q, s, use_ue8m0=True, eps=_QUANT_EPS)
             _ops.fp8_gemm_nt(q, s, weight_fp8, weight_scale_inv, output)
-        elif M <= _ops.BF16A_MAX_M and is_e8m0_used() and _ops.bf16a_preferred(M, N, K, x2.get_device()):
+        elif (M <= _ops.BF16A_MAX_M and x2.dtype is torch.bfloat16 and is_e8m0_used()
+              and _ops.bf16a_preferred(M, N, K, x2.get_device())):
             # small M (the reference's bf16-input branch, :398-417): one
             # launch of the GEMM that quantizes its bf16 activations itself,
             # the same codes and scales as the quant launch would write, where
@@ -172,8 +173,15 @@ class Fp8Linear(nn.Module):
                 q_buf = torch.empty(M, K, dtype=FP8, device=x2.device)
                 s_buf = _alloc_colmajor_scale(M, G, x2.device)
                 o_buf = torch.empty(M, N, dtype=torch.bfloat16, device=x2.device)
-            _ops.fp8_linear_forward(x2, q_buf, s_buf, weight_fp8, weight_scale_inv, o_buf)
             output = o_buf if o_buf.shape[0] == M else o_buf[:M]
+            if x2.dtype is torch.bfloat16:
+                _ops.fp8_linear_forward(x2, q_buf, s_buf, weight_fp8, weight_scale_inv, o_buf)
+            else:
+                # fp16 / fp32 activations, which the reference's quant also
+                # takes (widened to fp32): the quant, then the GEMM
+                q, s = (q_buf, s_buf) if q_buf.shape[0] == M else (q_buf[:M], s_buf[:M])
+                _ops.per_token_group_quant_fp8(x2, q, s, use_ue8m0=True, eps=_QUANT_EPS)
+                _ops.fp8_gemm_nt(q, s, weight_fp8, weight_scale_inv, output)
 
         if bias is not None:
             output = output + bias

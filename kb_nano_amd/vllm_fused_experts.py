@@ -47,9 +47,14 @@ def _moe_align_block_size_fresh(topk_ids: torch.Tensor, block_size: int, num_exp
 
 class VllmFusedExperts(nn.Module):
     """``forward(hidden_states, w13, w2, topk_weights, topk_ids, num_experts,
-    w13_scale, w2_scale, block_shape)`` (reference :100-237): bf16 [M, K]
-    hidden states, fp8 w13 [E, 2N, K] and w2 [E, K, N] with 128x128 block
-    scales, routing [M, top_k].  Returns bf16 [M, K]."""
+    w13_scale, w2_scale, block_shape)`` (reference :100-237): bf16, fp16 or
+    fp32 [M, K] hidden states, fp8 w13 [E, 2N, K] and w2 [E, K, N] with
+    128x128 block scales, routing [M, top_k].  Returns [M, K] in the hidden
+    states' dtype.  fp16 / fp32 hidden states are quantized from their own
+    values (as the reference's quant widens them to fp32); the GEMM outputs,
+    the SiLU*Mul product and the top-k sum stay bf16 and the sum is cast to
+    the input dtype at the end, where the reference keeps those
+    intermediates in the input dtype (:152-164)."""
 
     def __init__(self):
         super().__init__()
@@ -62,14 +67,13 @@ class VllmFusedExperts(nn.Module):
         assert hidden_states.is_contiguous(), "hidden_states must be contiguous"
         assert w13.stride(-1) == 1 and w2.stride(-1) == 1
         assert topk_weights.size() == topk_ids.size()
-        if hidden_states.dtype != torch.bfloat16:
-            raise NotImplementedError("VllmFusedExperts: bf16 activations only on this path")
+        assert hidden_states.dtype in (torch.bfloat16, torch.float16, torch.float32)
         M, K = hidden_states.size()
         E, N2, _ = w13.size()
         N = N2 // 2
         top_k = topk_ids.size(1)
         device = hidden_states.device
-        dtype = hidden_states.dtype
+        dtype = torch.bfloat16   # the intermediates' dtype on this path
 
         config = get_triton_config(M, w13.shape, w2.shape, top_k, use_fp8=True, block_shape=block_shape)
         block_m = config["BLOCK_SIZE_M"]
@@ -110,4 +114,6 @@ class VllmFusedExperts(nn.Module):
 
         out_hidden_states = torch.empty(M, K, device=device, dtype=dtype)
         _ops.moe_sum(intermediate_cache3.view(M, top_k, K), out_hidden_states)
+        if hidden_states.dtype is not dtype:
+            return out_hidden_states.to(hidden_states.dtype)
         return out_hidden_states

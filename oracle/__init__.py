@@ -94,6 +94,8 @@ def lib():
             qargs = [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, ctypes.c_float, ctypes.c_int]
             L.orc_quant_group128.restype = ctypes.c_int
             L.orc_quant_group128.argtypes = qargs
+            L.orc_quant_group128_f32.restype = ctypes.c_int
+            L.orc_quant_group128_f32.argtypes = qargs
             L.orc_silu_mul_quant.restype = ctypes.c_int
             L.orc_silu_mul_quant.argtypes = qargs
             L.orc_gemm_nt_sample.restype = ctypes.c_int
@@ -192,6 +194,22 @@ def quant_group128(x_bits: np.ndarray, eps: float = EPS, use_ue8m0: bool = True)
                                   float(eps), int(use_ue8m0))
     if rc:
         raise ValueError(f"orc_quant_group128 failed ({rc}); K must be a multiple of 128")
+    return q, s
+
+
+def quant_group128_f32(x: np.ndarray, eps: float = EPS, use_ue8m0: bool = True):
+    """Per-token-group 1x128 quant of fp16 or fp32 values
+    (tasks/baseline/L1/fp8_linear.py:181-215; :197 widens the input to fp32,
+    exactly for these types).  ``x``: float16 or float32 [M, K].  Returns
+    (q uint8 [M,K], s float32 [M, K/128] row-major)."""
+    v = np.ascontiguousarray(np.asarray(x).astype(np.float32))
+    M, K = v.shape
+    q = np.empty((M, K), dtype=np.uint8)
+    s = np.empty((M, K // GROUP), dtype=np.float32)
+    rc = lib().orc_quant_group128_f32(_ptr(v), M, K, K, _ptr(q), K, _ptr(s), K // GROUP, 1,
+                                      float(eps), int(use_ue8m0))
+    if rc:
+        raise ValueError(f"orc_quant_group128_f32 failed ({rc}); K must be a multiple of 128")
     return q, s
 
 

@@ -17,6 +17,8 @@
  *   orc_quant_group128     tasks/baseline/L1/fp8_linear.py:181-215 (one 1x128 group:
  *                          absmax, eps clamp, scale, divide, clamp, cast) with the
  *                          stride-addressed scale store of :214-215.
+ *   orc_quant_group128_f32 the same on fp32 values: fp16 and fp32 inputs, which
+ *                          :197 widens to fp32 (exactly) before the absmax.
  *   orc_silu_bf16          tasks/baseline/L1/silu_mul_quant_fp8.py:57-59, silu rounded
  *                          once to bf16; pinned here as the correctly rounded value
  *                          of g/(1+e^-g) (evaluated in double).
@@ -161,6 +163,33 @@ int orc_quant_group128(const uint16_t* x, int64_t M, int64_t K, int64_t ld_x,
             float sc = group_scale(amax, eps, use_ue8m0);
             uint8_t* qr = q + m * ld_q + g * 128;
             for (int i = 0; i < 128; ++i) qr[i] = quant_one(v[i], sc);
+            s[m * s_stride_m + g * s_stride_g] = sc;
+        }
+    }
+    return 0;
+}
+
+/* The same quantization of fp32 values [M,K] (K % 128 == 0): fp16 and fp32
+ * inputs, which the reference's kernel widens to fp32 before the absmax
+ * (tasks/baseline/L1/fp8_linear.py:197); the widening is exact, so the
+ * caller passes the fp32 values. */
+int orc_quant_group128_f32(const float* x, int64_t M, int64_t K, int64_t ld_x,
+                           uint8_t* q, int64_t ld_q, float* s, int64_t s_stride_m,
+                           int64_t s_stride_g, float eps, int use_ue8m0) {
+    if (K % 128) return 1;
+    int64_t G = K / 128;
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t g = 0; g < G; ++g) {
+            const float* xr = x + m * ld_x + g * 128;
+            float amax = 0.0f;
+            for (int i = 0; i < 128; ++i) {
+                float a = fabsf(xr[i]);
+                if (a > amax) amax = a;
+            }
+            float sc = group_scale(amax, eps, use_ue8m0);
+            uint8_t* qr = q + m * ld_q + g * 128;
+            for (int i = 0; i < 128; ++i) qr[i] = quant_one(xr[i], sc);
             s[m * s_stride_m + g * s_stride_g] = sc;
         }
     }

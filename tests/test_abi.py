@@ -49,6 +49,21 @@ def test_quant_rejects_ragged_k_without_device():
     assert rc == 1 and "multiple of 128" in _err()
 
 
+def test_typed_quant_rejects_bad_arguments_without_device():
+    """The fp16 / fp32 quant entry validates before any device call: an
+    unknown dtype code, a ragged K, misaligned rows; empty input is a no-op."""
+    from kb_nano_amd._lib import lib
+    L = lib()
+    p = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    assert L.kbn_per_token_group_quant_fp8_typed(p, 3, 4, 128, 128, p, 128, p, 1, 1, 1e-10, 1, None) == 1
+    assert "dtype code 3" in _err()
+    assert L.kbn_per_token_group_quant_fp8_typed(p, 2, 4, 100, 100, p, 100, p, 1, 1, 1e-10, 1, None) == 1
+    assert "multiple of 128" in _err()
+    assert L.kbn_per_token_group_quant_fp8_typed(p, 1, 4, 128, 132, p, 128, p, 1, 1, 1e-10, 1, None) == 1
+    assert "16-byte" in _err()
+    assert L.kbn_per_token_group_quant_fp8_typed(None, 2, 0, 128, 128, None, 128, None, 1, 1, 1e-10, 1, None) == 0
+
+
 def test_silu_rows_rejects_null_row_ids():
     from kb_nano_amd._lib import lib
     p = ctypes.c_void_p(4096)  # never dereferenced: validation fails first

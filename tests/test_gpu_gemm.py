@@ -205,6 +205,40 @@ def test_fp8_linear_decode_sizes(gpu_device):
         assert_gemm_close(y, ref, f"decode M={M}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_fp8_linear_fp16_fp32_input(gpu_device, dtype):
+    """fp16 / fp32 activations, which the reference's Fp8Linear quantizes as
+    well (its quant widens them to fp32; only its bf16 FlashInfer branch
+    needs bf16): the quant of the values themselves, then the GEMM, bf16
+    out; every M path (decode sizes that take the bf16-input GEMM for bf16,
+    installed buffers, prefill) against the oracle's float-input quant and
+    GEMM, and bit-identical to the two ops called in turn."""
+    from kb_nano_amd import Fp8Linear, _ops
+    from kb_nano_amd.fp8_linear import _alloc_colmajor_scale
+    N, K = 512, 2048
+    _, _, qw, sw = quantized_gemm_inputs(8, N, K, seed=7)
+    W, sW = to_fp8(qw, gpu_device), torch.from_numpy(sw).to(gpu_device)
+    for M, installed in ((1, False), (32, False), (64, True), (200, False)):
+        print(f"Fp8Linear {dtype} M={M} installed={installed}", flush=True)
+        x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).to(dtype)
+        qa, sa = oracle.quant_group128_f32(x.numpy())
+        ref = oracle.gemm_nt_sample(qa, sa, qw, sw)
+        lin = Fp8Linear()
+        if installed:
+            lin._ensure_buffers(128, K, N, gpu_device)
+        y = lin(x.to(gpu_device), W, sW)
+        q = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=gpu_device)
+        s = _alloc_colmajor_scale(M, K // 128, gpu_device)
+        _ops.per_token_group_quant_fp8(x.to(gpu_device), q, s)
+        y2 = torch.empty(M, N, dtype=torch.bfloat16, device=gpu_device)
+        _ops.fp8_gemm_nt(q, s, W, sW, y2)
+        torch.cuda.synchronize()
+        assert y.dtype == torch.bfloat16 and y.shape == (M, N)
+        assert np.array_equal(fp8_codes(q), qa)
+        assert_gemm_close(y, ref, f"Fp8Linear {dtype} M={M}")
+        assert torch.equal(y, y2)
+
+
 def test_postprocess_weights_roundtrip(gpu_device):
     """Requant of UE8M0 block weights is value-preserving."""
     from kb_nano_amd import postprocess_fp8_weights

@@ -176,10 +176,14 @@ def test_fused_moe_gemm_naive_blocks(gpu_device):
 def _oracle_vllm_moe(hidden_bits, topk, topk_w, w13, s13, w2, s2, E, block):
     """The reference's step order (vllm_fused_experts.py:140-237) in the
     oracle: quant, align, GEMM1 -> bf16, SiLU*Mul + quant, GEMM2 * w -> bf16,
-    moe_sum."""
+    moe_sum.  ``hidden_bits``: bf16 bit patterns, or fp16 / fp32 values
+    (quantized as such; the intermediates stay bf16 as on this path)."""
     M, K = hidden_bits.shape
     k = topk.shape[1]
-    qa, sa = oracle.quant_group128(hidden_bits, use_ue8m0=True)
+    if hidden_bits.dtype == np.uint16:
+        qa, sa = oracle.quant_group128(hidden_bits, use_ue8m0=True)
+    else:
+        qa, sa = oracle.quant_group128_f32(hidden_bits, use_ue8m0=True)
     s_ids, e_ids, total, _ = oracle.moe_align_block_size(topk, E, block)
     r1 = oracle.fused_moe_gemm_sample(qa, sa, w13, s13, s_ids, e_ids, total, block, M * k, k)
     mm1 = np.stack([r1[t] for t in range(M * k)]).astype(np.float32)
@@ -209,6 +213,33 @@ def test_vllm_fused_experts_matches_oracle(gpu_device, M, K, I, E, k):
                              torch.from_numpy(s13).to(dev), torch.from_numpy(s2).to(dev), [128, 128])
     torch.cuda.synchronize()
     assert_gemm_close(out, ref, "VllmFusedExperts")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_vllm_fused_experts_fp16_fp32_hidden(gpu_device, dtype):
+    """fp16 / fp32 hidden states, which the reference accepts (:131): the
+    output has the input dtype and matches the oracle's composition on the
+    same values (their own quant, bf16 intermediates)."""
+    from kb_nano_amd import VllmFusedExperts
+    from kb_nano_amd.moe_grouped_gemm import get_triton_config
+    dev = gpu_device
+    M, K, I, E, k = 80, 512, 384, 16, 4
+    print(f"VllmFusedExperts {dtype}", flush=True)
+    hidden = torch.randn(M, K, generator=torch.Generator().manual_seed(12)).to(dtype)
+    topk = _routing(M, k, E, seed=13)
+    rng = np.random.default_rng(14)
+    topk_w = rng.random((M, k)).astype(np.float32)
+    topk_w /= topk_w.sum(axis=1, keepdims=True)
+    w13, s13 = _experts(E, 2 * I, K, seed=15)
+    w2, s2 = _experts(E, K, I, seed=16)
+    block = get_triton_config(M, w13.shape, w2.shape, k, True, [128, 128])["BLOCK_SIZE_M"]
+    ref = _oracle_vllm_moe(hidden.numpy(), topk, topk_w, w13, s13, w2, s2, E, block)
+    args = (to_fp8(w13, dev), to_fp8(w2, dev), torch.from_numpy(topk_w).to(dev), torch.from_numpy(topk).to(dev), E,
+            torch.from_numpy(s13).to(dev), torch.from_numpy(s2).to(dev), [128, 128])
+    out = VllmFusedExperts()(hidden.to(dev), *args)
+    torch.cuda.synchronize()
+    assert out.dtype == dtype and out.shape == (M, K)
+    assert_gemm_close(out, ref, f"VllmFusedExperts {dtype}")
 
 
 def test_sorted_and_contiguous_layers_agree(gpu_device):

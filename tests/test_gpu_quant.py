@@ -98,6 +98,72 @@ def test_quant_rejects_bad_args(gpu_device):
                                        torch.empty(4, 2))
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("M,K", [(1, 128), (3, 2048), (130, 7168), (257, 1536)])
+@pytest.mark.parametrize("use_ue8m0", [True, False])
+def test_quant_fp16_fp32_inputs_match_oracle(gpu_device, dtype, M, K, use_ue8m0):
+    """fp16 and fp32 rows (kbn_per_token_group_quant_fp8_typed): codes and
+    scales bit-exact against the oracle's quant of the same values, with
+    zero rows, each type's subnormals and values near its max; column-major
+    scales on every other shape."""
+    print(f"quant {dtype} M={M} K={K} ue8m0={use_ue8m0}", flush=True)
+    g = torch.Generator().manual_seed(M * 3 + K)
+    x = torch.randn(M, K, generator=g)
+    x = torch.where(torch.rand(M, K, generator=g) < 1e-3, x * 50, x)
+    if M > 2:
+        x[1, :] = 0
+        x[2, :128] = torch.randn(128, generator=g) * (3e-7 if dtype == torch.float16 else 1e-39)
+        x[2, 128:] = torch.randn(K - 128, generator=g) * (6.0e4 / 8 if dtype == torch.float16 else 3e37)
+    x = x.to(dtype)
+    qo, so = oracle.quant_group128_f32(x.numpy(), use_ue8m0=use_ue8m0)
+    q, s = _quant_gpu(x.to(gpu_device), col_major=(M % 2 == 1), use_ue8m0=use_ue8m0)
+    assert np.array_equal(s.cpu().numpy(), so)
+    assert np.array_equal(fp8_codes(q), qo)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_quant_fp16_fp32_nonfinite_groups(gpu_device, dtype):
+    """fp16 / fp32 groups holding +-inf or NaN follow the bf16 kernel's rules
+    (NaN ignored by the absmax, an infinite absmax gives an infinite scale,
+    finite values then code to +-0): equal to the oracle up to the NaN
+    code's sign bit, and to the bf16 kernel on the same (bf16) values."""
+    x = seeded_bf16((16, 1024), seed=22).float().numpy()
+    x[0, 5] = np.inf
+    x[1, 130] = -np.inf
+    x[2, 300] = np.nan
+    x[3, :128] = np.nan
+    x[4, 513] = np.inf
+    x[4, 514] = np.nan
+    x[5, 640:768] = np.inf
+    xt = torch.from_numpy(x).to(dtype)
+    qo, so = oracle.quant_group128_f32(xt.numpy())
+    q, s = _quant_gpu(xt.to(gpu_device))
+    assert np.array_equal(s.cpu().numpy(), so)
+    assert np.array_equal(_canon_nan(fp8_codes(q)), _canon_nan(qo))
+    qb, sb = _quant_gpu(torch.from_numpy(x).bfloat16().to(gpu_device))
+    assert np.array_equal(fp8_codes(q), fp8_codes(qb)) and torch.equal(s, sb)
+
+
+def test_quant_module_and_op_fp16_fp32(gpu_device):
+    """The module and the registered op take fp16 / fp32 input as the
+    reference's do; a dtype outside bf16 / fp16 / fp32 is rejected."""
+    from kb_nano_amd import PerTokenGroupQuantFp8, _ops
+    for dtype in (torch.float16, torch.float32):
+        x = torch.randn(40, 384, generator=torch.Generator().manual_seed(6)).to(dtype)
+        qo, so = oracle.quant_group128_f32(x.numpy())
+        for call in (lambda xx, qq, ss: PerTokenGroupQuantFp8()(xx, qq, ss),
+                     lambda xx, qq, ss: torch.ops.kb_nano_fp8.per_token_group_quant_fp8(xx, qq, ss, False)):
+            q = torch.empty(40, 384, dtype=torch.float8_e4m3fn, device=gpu_device)
+            s = torch.empty(40, 3, dtype=torch.float32, device=gpu_device)
+            call(x.to(gpu_device), q, s)
+            torch.cuda.synchronize()
+            assert np.array_equal(fp8_codes(q), qo) and np.array_equal(s.cpu().numpy(), so)
+    with pytest.raises(TypeError):
+        _ops.per_token_group_quant_fp8(torch.zeros(4, 128, dtype=torch.float64, device=gpu_device),
+                                       torch.empty(4, 128, dtype=torch.float8_e4m3fn, device=gpu_device),
+                                       torch.empty(4, 1, device=gpu_device))
+
+
 def test_quant_empty(gpu_device):
     q, s = _quant_gpu(torch.empty(0, 256, dtype=torch.bfloat16, device=gpu_device))
     assert q.shape == (0, 256) and s.shape == (0, 2)

@@ -201,6 +201,48 @@ def test_quant_group128_vs_reference_formula(use_ue8m0):
     assert np.array_equal(q, qw)
 
 
+def _edge_tensor_typed(dtype, rows=16):
+    """Edge rows at the range of fp16 or fp32: zeros, a 448 ramp, each type's
+    subnormals, outliers, values near the type's max, an amax of 448 * 2^k."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(rows, 1024, generator=g)
+    big = 6.0e4 if dtype == torch.float16 else 3.0e38
+    tiny = 3.0e-7 if dtype == torch.float16 else 1.0e-39    # fp16 / fp32 subnormals
+    x[0] = 0.0
+    x[1, :128] = 448.0 * torch.linspace(-1, 1, 128)
+    x[2, :] = torch.randn(1024, generator=g) * tiny
+    x[3, ::7] *= 50.0
+    x[4, :] = big * torch.sign(torch.randn(1024, generator=g))
+    x[5, 128:256] = 1.0
+    x[5, 130] = 448.0 * 2 ** 3
+    x[6, :] = torch.randn(1024, generator=g) * 1e-3
+    return x.to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("use_ue8m0", [True, False])
+def test_quant_group128_f32_vs_reference_formula(dtype, use_ue8m0):
+    """fp16 / fp32 inputs: the oracle's float-input quant against the
+    reference's formula executed by torch on the same values (its kernel
+    widens them to fp32, tasks/baseline/L1/fp8_linear.py:197)."""
+    x = torch.cat([_edge_tensor_typed(dtype),
+                   torch.randn(48, 1024, generator=torch.Generator().manual_seed(2)).to(dtype)])
+    q, s = oracle.quant_group128_f32(x.numpy(), use_ue8m0=use_ue8m0)
+    qw, sw = _torch_reference_quant(x, use_ue8m0)
+    assert np.array_equal(s, sw)
+    assert np.array_equal(q, qw)
+
+
+def test_quant_group128_f32_equals_bf16_quant_on_bf16_values():
+    """On values that are bf16 numbers the float-input quant and the bf16
+    quant are one function."""
+    x = torch.cat([_edge_tensor(), torch.randn(16, 1024, generator=torch.Generator().manual_seed(3)).bfloat16()])
+    for ue8m0 in (True, False):
+        q1, s1 = oracle.quant_group128(x.view(torch.int16).numpy().astype(np.uint16), use_ue8m0=ue8m0)
+        q2, s2 = oracle.quant_group128_f32(x.float().numpy(), use_ue8m0=ue8m0)
+        assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
+
+
 def test_quant_group128_rejects_ragged_k():
     with pytest.raises(ValueError):
         oracle.quant_group128(np.zeros((2, 100), dtype=np.uint16))
