@@ -302,9 +302,11 @@ int kbn_moe_unpermute_reduce(const void* y_bf16, int64_t M_sum, int64_t H, int64
  * kb_nano_norm::fused_add_rmsnorm_fp8_quant (tasks/baseline/L1/rmsnorm_quant.py:27-55;
  * kernels tasks/baseline/L1/csrc/rmsnorm_quant.cu:21-93, :124-201).
  *   x         bf16 [M, H], row stride ld_x; w bf16 [H]; 16-byte aligned, H % 8 == 0
- *   residual  NULL: plain RMSNorm of x (H <= 16384).  Otherwise bf16 [M, H],
- *             row stride ld_r (H <= 8192): residual <- bf16(residual + x), the
- *             norm is taken of the fp32 sums, and x <- bf16(normalized row).
+ *   residual  NULL: plain RMSNorm of x.  Otherwise bf16 [M, H], row stride
+ *             ld_r: residual <- bf16(residual + x), the norm is taken of the
+ *             fp32 sums, and x <- bf16(normalized row).  Any H (multiple of 8):
+ *             rows of up to 16384 (8192 with the add) are held in registers,
+ *             longer ones read twice, in the same summation order.
  *   q         fp8 [M, H], row stride ld_q (multiple of 8)
  *   scale     fp32 (m, g) at scale[m*s_stride_m + g*s_stride_g], g < ceil(H/128)
  *             (the reference's column-major buffer: (1, M))
@@ -317,6 +319,17 @@ int kbn_moe_unpermute_reduce(const void* y_bf16, int64_t M_sum, int64_t H, int64
 int kbn_rmsnorm_fp8_quant(void* x_bf16, int64_t M, int64_t H, int64_t ld_x, const void* w_bf16,
                           void* residual_bf16, int64_t ld_r, void* q_fp8, int64_t ld_q, float* scale,
                           int64_t s_stride_m, int64_t s_stride_g, float eps, void* stream);
+
+/*
+ * The same for bf16, fp16 or fp32 rows: the reference dispatches its kernels
+ * over the float types (tasks/baseline/L1/csrc/rmsnorm_quant.cu:111).
+ *   x_dtype   0 bf16, 1 fp16, 2 fp32; x, w and residual all of that type
+ *   The residual sum and the normalized row written back are rounded to the
+ *   type (nearest even); every other argument as kbn_rmsnorm_fp8_quant.
+ */
+int kbn_rmsnorm_fp8_quant_typed(void* x, int x_dtype, int64_t M, int64_t H, int64_t ld_x, const void* w,
+                                void* residual, int64_t ld_r, void* q_fp8, int64_t ld_q, float* scale,
+                                int64_t s_stride_m, int64_t s_stride_g, float eps, void* stream);
 
 /*
  * Sorted-token MoE layout: moe_align_block_size.

@@ -46,6 +46,7 @@ SIGNATURES = {
          _P, _I64, _P], _I),
     "kbn_moe_unpermute_reduce": ([_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I, _P, _I64, _P], _I),
     "kbn_rmsnorm_fp8_quant": ([_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _F, _P], _I),
+    "kbn_rmsnorm_fp8_quant_typed": ([_P, _I, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _F, _P], _I),
     "kbn_moe_align_block_size": ([_P, _I, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _P], _I),
     "kbn_fp8_fused_moe_gemm": ([_P, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64,
                                 _P, _I64, _I64, _I64, _P, _I64, _P], _I),

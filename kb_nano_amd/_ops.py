@@ -599,7 +599,9 @@ def rmsnorm_fp8_quant(output_fp8: torch.Tensor, output_scales: torch.Tensor, inp
     """RMSNorm of ``input [..., H]`` (of ``residual + input`` when ``residual``
     is given, updating both in place as the reference does) quantized 1x128
     into ``output_fp8 [T, H]`` and ``output_scales [T, ceil(H/128)]`` (any
-    strides; the reference allocates them column-major)."""
+    strides; the reference allocates them column-major).  ``input``,
+    ``weight`` and ``residual`` share one dtype: bfloat16, float16 or
+    float32, as the reference's kernel dispatches (rmsnorm_quant.cu:111)."""
     idx = input.get_device()
     add = residual is not None
     if (idx not in _GFX950_DEVICES or idx != _cur_device() or output_fp8.get_device() != idx
@@ -612,9 +614,11 @@ def rmsnorm_fp8_quant(output_fp8: torch.Tensor, output_scales: torch.Tensor, inp
         what = "fused_add_rmsnorm_fp8_quant" if add else "rmsnorm_fp8_quant"
         _dtype_check(what, output_fp8, FP8, "output_fp8")
         _dtype_check(what, output_scales, torch.float32, "output_scales")
-        for t, name in ((input, "input"), (weight, "weight")) + (((residual, "residual"),) if add else ()):
-            if t.dtype != torch.bfloat16:
-                raise TypeError(f"{what}: {name} must be bfloat16 on this path, got {t.dtype}")
+        if input.dtype not in _QUANT_IN:
+            raise TypeError(f"{what}: input must be bfloat16, float16 or float32, got {input.dtype}")
+        for t, name in ((weight, "weight"),) + (((residual, "residual"),) if add else ()):
+            if t.dtype != input.dtype:
+                raise TypeError(f"{what}: {name} must have the input's dtype {input.dtype}, got {t.dtype}")
     shape = input.shape
     H = shape[-1] if len(shape) else 1
     T = input.numel() // H if H else 0
@@ -633,9 +637,15 @@ def rmsnorm_fp8_quant(output_fp8: torch.Tensor, output_scales: torch.Tensor, inp
         if output_fp8.shape != (T, H) or qs[1] != 1:
             raise ValueError(f"{what}: output_fp8 must be [{T}, {H}] with contiguous rows")
         raise ValueError(f"{what}: output_scales must be [{T}, {G}], got {tuple(output_scales.shape)}")
-    rc = lib().kbn_rmsnorm_fp8_quant(
-        input.data_ptr(), T, H, H, weight.data_ptr(), residual.data_ptr() if add else None, H,
-        output_fp8.data_ptr(), qs[0], output_scales.data_ptr(), ss[0], ss[1], float(eps), _raw_stream(idx))
+    if input.dtype is _BF16:
+        rc = lib().kbn_rmsnorm_fp8_quant(
+            input.data_ptr(), T, H, H, weight.data_ptr(), residual.data_ptr() if add else None, H,
+            output_fp8.data_ptr(), qs[0], output_scales.data_ptr(), ss[0], ss[1], float(eps), _raw_stream(idx))
+    else:
+        rc = lib().kbn_rmsnorm_fp8_quant_typed(
+            input.data_ptr(), _QUANT_IN[input.dtype], T, H, H, weight.data_ptr(),
+            residual.data_ptr() if add else None, H, output_fp8.data_ptr(), qs[0], output_scales.data_ptr(), ss[0],
+            ss[1], float(eps), _raw_stream(idx))
     if rc:
         check(rc, "fused_add_rmsnorm_fp8_quant" if add else "rmsnorm_fp8_quant")
 

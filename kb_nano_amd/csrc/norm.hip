@@ -99,6 +99,12 @@ __device__ __forceinline__ void load_row(const NormArgs& a, int m, int wave, int
 // semantics (NaN -> -448).
 __device__ __forceinline__ float clamp448(float v) { return __builtin_amdgcn_fmed3f(v, -kFp8Max, kFp8Max); }
 
+// Factor that divides by the power-of-two scale sc exactly: its reciprocal,
+// or 0 for an infinite scale (a group whose absmax overflowed), so that
+// v * 0 gives v / inf's +-0 for finite v and NaN (clamped to -448) for
+// infinite v, as the reference's division does.
+__device__ __forceinline__ float inv_scale(float sc) { return sc < __builtin_inff() ? pow2_recip(sc) : 0.f; }
+
 // Normalize and quantize one token.  `wf` holds this wavefront's weights,
 // `part` the LDS slots of the W wavefront sums (double-buffered by token
 // parity, so one barrier per token suffices), `wok` whether this wavefront's
@@ -179,7 +185,7 @@ __device__ __forceinline__ void norm_row(const NormArgs& a, int m, int wave, int
             amax = fmaxf(amax, kGroupEps);
             const float sc = ue8m0_ceil_div448(amax);
             if constexpr (kClamp) {
-                const float is = pow2_recip(sc);
+                const float is = inv_scale(sc);
                 float t[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) t[j] = clamp448(v[j] * is);
@@ -313,36 +319,208 @@ int launch_norm(const NormArgs& a, hipStream_t st) {
     return 0;
 }
 
+// ------------------------------------------------------------- general
+// Any H (a multiple of 8) and bf16 / fp16 / fp32 rows, as the reference
+// dispatches its kernel over the float types (rmsnorm_quant.cu:111) for any
+// hidden size.  The same summation order as rmsnorm_quant_kernel: W
+// wavefronts, wavefront w owning the 512-element chunks c = w, w + W, ...,
+// 8 elements per lane, fmaf in chunk then element order, the xor butterfly,
+// the wavefront sums added in order; inv by the correctly rounded sqrt and
+// divide.  The row is read twice (the second time mostly from L2) instead of
+// held in registers.  Weight and residual share the input's type.  The fused
+// add recomputes r + x in the second pass (the same fp32 sum), rounds it to
+// the type, stores it to the residual and normalizes it, so no pass reads
+// what another wrote.  Codes always take the clamped conversion (equal to
+// the unclamped one for finite rows).  One workgroup per token at a time.
+constexpr int kNormBf16 = 0, kNormF16 = 1, kNormF32 = 2;   // element type codes
+
+template <int kT>
+constexpr int elt_bytes() { return kT == kNormF32 ? 4 : 2; }
+
+// Eight elements at byte offset `off` as fp32 (reads past the range are zeros).
+template <int kT>
+__device__ __forceinline__ void load8(__amdgpu_buffer_rsrc_t rs, int off, float (&v)[8]) {
+    if constexpr (kT == kNormF32) {
+        const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kNtLoad);
+        const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16, 0, kNtLoad);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[j] = __uint_as_float(lo[j]);
+            v[4 + j] = __uint_as_float(hi[j]);
+        }
+    } else {
+        const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kNtLoad);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if constexpr (kT == kNormBf16) {
+                v[2 * j] = bf16lo(w[j]);
+                v[2 * j + 1] = bf16hi(w[j]);
+            } else {
+                typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                const uint32_t word = w[j];   // (a vector element is not a bit_cast operand)
+                const h2 h = __builtin_bit_cast(h2, word);
+                v[2 * j] = (float)h.x;
+                v[2 * j + 1] = (float)h.y;
+            }
+        }
+    }
+}
+
+// Two fp32 values rounded to the 16-bit type (nearest even), packed.
+template <int kT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    if constexpr (kT == kNormBf16) {
+        return pack_bf16_rne(lo, hi);
+    } else {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, h2{(_Float16)lo, (_Float16)hi});
+    }
+}
+
+// v rounded to the type (nearest even), as fp32.
+template <int kT>
+__device__ __forceinline__ float round_to(float v) {
+    if constexpr (kT == kNormBf16) return __uint_as_float(pack_bf16_rne(v, 0.f) << 16);
+    else if constexpr (kT == kNormF16) return (float)(_Float16)v;
+    else return v;
+}
+
+// Eight fp32 values stored in the type at byte offset `off` (dropped past the range).
+template <int kT>
+__device__ __forceinline__ void store8(__amdgpu_buffer_rsrc_t rs, int off, const float (&v)[8]) {
+    if constexpr (kT == kNormF32) {
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])}, rs,
+            off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])}, rs,
+            off + 16, 0, 0);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u32x4{pack2<kT>(v[0], v[1]), pack2<kT>(v[2], v[3]), pack2<kT>(v[4], v[5]), pack2<kT>(v[6], v[7])}, rs,
+            off, 0, 0);
+    }
+}
+
+template <int kW, int kT, bool kAdd>
+__global__ __launch_bounds__(64 * kW) void rmsnorm_quant_any_kernel(const NormArgs a) {
+#pragma clang fp contract(off)
+    __shared__ float part[2][kW];
+    constexpr int kB = elt_bytes<kT>();
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int C = (a.H + 511) / 512;
+    const int row_bytes = kB * a.H;
+    const __amdgpu_buffer_rsrc_t wr = row_rsrc(a.w, row_bytes);
+    const __amdgpu_buffer_rsrc_t sw = row_rsrc(a.s, a.s_bytes);
+    int parity = 0;
+    for (int m = blockIdx.x; m < a.M; m += gridDim.x, parity ^= 1) {
+        const uint8_t* xrow = reinterpret_cast<const uint8_t*>(a.x) + (int64_t)m * a.ld_x * kB;
+        const uint8_t* rrow = kAdd ? reinterpret_cast<const uint8_t*>(a.r) + (int64_t)m * a.ld_r * kB : xrow;
+        const __amdgpu_buffer_rsrc_t xr = row_rsrc(xrow, row_bytes);
+        const __amdgpu_buffer_rsrc_t rr = row_rsrc(rrow, kAdd ? row_bytes : 0);
+        const __amdgpu_buffer_rsrc_t qw = row_rsrc(a.q + (int64_t)m * a.ld_q, a.H);
+        // ---- pass 1: sum of squares of x (fused add: of r + x, unrounded);
+        // lanes past the row read zeros and add nothing
+        float p = 0.f;
+        for (int c = wave; c < C; c += kW) {
+            const int off = kB * (c * 512 + 8 * lane);
+            float xv[8], rv[8];
+            load8<kT>(xr, off, xv);
+            if constexpr (kAdd) load8<kT>(rr, off, rv);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float t = kAdd ? rv[j] + xv[j] : xv[j];
+                p = fmaf(t, t, p);
+            }
+        }
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) p = p + __shfl_xor(p, d, 64);
+        if (lane == 0) part[parity][wave] = p;
+        __syncthreads();   // (the other parity's slots are free: every wavefront has read them)
+        p = part[parity][0];
+#pragma unroll
+        for (int w = 1; w < kW; ++w) p = p + part[parity][w];
+        const float inv = 1.0f / sqrtf(p / (float)a.H + a.eps);
+        // ---- pass 2: normalize, quantize, store
+        for (int c = wave; c < C; c += kW) {
+            const int e0 = c * 512 + 8 * lane;
+            const int off = kB * e0;
+            float xv[8], rv[8], wv[8], base[8], v[8];
+            load8<kT>(xr, off, xv);
+            if constexpr (kAdd) load8<kT>(rr, off, rv);
+            load8<kT>(wr, off, wv);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) base[j] = kAdd ? round_to<kT>(rv[j] + xv[j]) : xv[j];
+            if constexpr (kAdd) store8<kT>(rr, off, base);   // residual <- r + x in the type
+            float amax = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                v[j] = (base[j] * inv) * wv[j];
+                amax = fmaxf(amax, fabsf(v[j]));
+            }
+            amax = __uint_as_float(row16_max_u32(__float_as_uint(amax)));
+            amax = fmaxf(amax, kGroupEps);
+            const float sc = ue8m0_ceil_div448(amax);
+            const float is = inv_scale(sc);
+            float t[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) t[j] = clamp448(v[j] * is);
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            __builtin_amdgcn_raw_buffer_store_b64(
+                u32x2{pack4_e4m3(t[0], t[1], t[2], t[3]), pack4_e4m3(t[4], t[5], t[6], t[7])}, qw, e0, 0, 0);
+            const bool owner = (lane & 15) == 0 && e0 < a.H;
+            __builtin_amdgcn_raw_buffer_store_b32(
+                __float_as_uint(sc), sw, owner ? (int)(4 * ((int64_t)m * a.s_m + (int64_t)(e0 >> 7) * a.s_g)) : kOob,
+                0, 0);
+            if constexpr (kAdd) store8<kT>(xr, off, v);       // input <- normalized row in the type
+        }
+    }
+}
+
+template <int kW, int kT, bool kAdd>
+void launch_norm_any_cfg(const NormArgs& a, hipStream_t st) {
+    const int blocks = (int)std::min<int64_t>(a.M, (int64_t)cu_count() * 4);
+    rmsnorm_quant_any_kernel<kW, kT, kAdd><<<dim3((unsigned)blocks), dim3(64 * kW), 0, st>>>(a);
+}
+
+// W = 8 from 8 chunks (H > 3584) up, else 4, as the fast kernel.
+template <int kT, bool kAdd>
+void launch_norm_any(const NormArgs& a, hipStream_t st) {
+    if ((a.H + 511) / 512 >= 8) launch_norm_any_cfg<8, kT, kAdd>(a, st);
+    else launch_norm_any_cfg<4, kT, kAdd>(a, st);
+}
+
 }  // namespace
 }  // namespace kbn
 
 using namespace kbn;
 
-extern "C" int kbn_rmsnorm_fp8_quant(void* x_bf16, int64_t M, int64_t H, int64_t ld_x, const void* w_bf16,
-                                     void* residual_bf16, int64_t ld_r, void* q_fp8, int64_t ld_q, float* scale,
-                                     int64_t s_stride_m, int64_t s_stride_g, float eps, void* stream) {
-    const char* what = residual_bf16 ? "fused_add_rmsnorm_fp8_quant" : "rmsnorm_fp8_quant";
-    const bool add = residual_bf16 != nullptr;
-    const int64_t max_h = add ? 8192 : 16384;
+static int rmsnorm_impl(const char* what, void* x, int x_dtype, int64_t M, int64_t H, int64_t ld_x, const void* w,
+                        void* residual, int64_t ld_r, void* q_fp8, int64_t ld_q, float* scale, int64_t s_stride_m,
+                        int64_t s_stride_g, float eps, void* stream) {
+    const bool add = residual != nullptr;
+    KBN_CHECK_ARG(x_dtype == kNormBf16 || x_dtype == kNormF16 || x_dtype == kNormF32,
+                  "%s: input dtype code %d (0 bf16, 1 fp16, 2 fp32)", what, x_dtype);
     KBN_CHECK_ARG(M >= 0 && M <= 0x7FFFFFFFLL, "%s: bad M=%lld", what, (long long)M);
-    KBN_CHECK_ARG(H > 0 && H % 8 == 0 && H <= max_h, "%s: hidden size %lld must be a positive multiple of 8, "
-                  "at most %lld", what, (long long)H, (long long)max_h);
+    KBN_CHECK_ARG(H > 0 && H % 8 == 0 && H * 4 + 1024 < 0x7FFFFFFFLL,
+                  "%s: hidden size %lld must be a positive multiple of 8", what, (long long)H);
     if (M == 0) return 0;
-    KBN_CHECK_ARG(x_bf16 && w_bf16 && q_fp8 && scale, "%s: null pointer", what);
-    KBN_CHECK_ARG(aligned16(x_bf16) && aligned16(w_bf16) && ld_x >= H && ld_x % 8 == 0,
+    KBN_CHECK_ARG(x && w && q_fp8 && scale, "%s: null pointer", what);
+    KBN_CHECK_ARG(aligned16(x) && aligned16(w) && ld_x >= H && ld_x % 8 == 0,
                   "%s: input and weight must be 16-byte aligned, input row stride >= H and a multiple of 8", what);
     KBN_CHECK_ARG(ld_q >= H && ld_q % 8 == 0 && (reinterpret_cast<uintptr_t>(q_fp8) & 7u) == 0,
                   "%s: output rows must be 8-byte aligned with a stride >= H", what);
     KBN_CHECK_ARG((reinterpret_cast<uintptr_t>(scale) & 3u) == 0, "%s: scales must be 4-byte aligned", what);
     if (add)
-        KBN_CHECK_ARG(aligned16(residual_bf16) && ld_r >= H && ld_r % 8 == 0,
+        KBN_CHECK_ARG(aligned16(residual) && ld_r >= H && ld_r % 8 == 0,
                       "%s: residual must be 16-byte aligned with a row stride >= H and a multiple of 8", what);
     KBN_CHECK_ARG(s_stride_m >= 0 && s_stride_g >= 0, "%s: negative scale stride", what);
     NormArgs a{};
-    a.x = static_cast<uint16_t*>(x_bf16);
+    a.x = static_cast<uint16_t*>(x);
     a.ld_x = ld_x;
-    a.w = static_cast<const uint16_t*>(w_bf16);
-    a.r = static_cast<uint16_t*>(residual_bf16);
+    a.w = static_cast<const uint16_t*>(w);
+    a.r = static_cast<uint16_t*>(residual);
     a.ld_r = ld_r;
     a.q = static_cast<uint8_t*>(q_fp8);
     a.ld_q = ld_q;
@@ -356,10 +534,38 @@ extern "C" int kbn_rmsnorm_fp8_quant(void* x_bf16, int64_t M, int64_t H, int64_t
     a.H = (int)H;
     a.eps = eps;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (add ? launch_norm<true>(a, st) : launch_norm<false>(a, st)) {
-        set_error("%s: no kernel for hidden size %lld", what, (long long)H);
-        return 1;
+    // bf16 rows of up to 16384 columns (8192 with the add): the register-
+    // resident kernel; everything else: the general one (same order)
+    const int64_t fast_h = add ? 8192 : 16384;
+    if (x_dtype == kNormBf16 && H <= fast_h) {
+        if (add ? launch_norm<true>(a, st) : launch_norm<false>(a, st)) {
+            set_error("%s: no kernel for hidden size %lld", what, (long long)H);
+            return 1;
+        }
+    } else if (x_dtype == kNormBf16) {
+        if (add) launch_norm_any<kNormBf16, true>(a, st);
+        else launch_norm_any<kNormBf16, false>(a, st);
+    } else if (x_dtype == kNormF16) {
+        if (add) launch_norm_any<kNormF16, true>(a, st);
+        else launch_norm_any<kNormF16, false>(a, st);
+    } else {
+        if (add) launch_norm_any<kNormF32, true>(a, st);
+        else launch_norm_any<kNormF32, false>(a, st);
     }
     KBN_CHECK_LAUNCH(what);
     return 0;
+}
+
+extern "C" int kbn_rmsnorm_fp8_quant(void* x_bf16, int64_t M, int64_t H, int64_t ld_x, const void* w_bf16,
+                                     void* residual_bf16, int64_t ld_r, void* q_fp8, int64_t ld_q, float* scale,
+                                     int64_t s_stride_m, int64_t s_stride_g, float eps, void* stream) {
+    return rmsnorm_impl(residual_bf16 ? "fused_add_rmsnorm_fp8_quant" : "rmsnorm_fp8_quant", x_bf16, kNormBf16, M, H,
+                        ld_x, w_bf16, residual_bf16, ld_r, q_fp8, ld_q, scale, s_stride_m, s_stride_g, eps, stream);
+}
+
+extern "C" int kbn_rmsnorm_fp8_quant_typed(void* x, int x_dtype, int64_t M, int64_t H, int64_t ld_x, const void* w,
+                                           void* residual, int64_t ld_r, void* q_fp8, int64_t ld_q, float* scale,
+                                           int64_t s_stride_m, int64_t s_stride_g, float eps, void* stream) {
+    return rmsnorm_impl(residual ? "fused_add_rmsnorm_fp8_quant" : "rmsnorm_fp8_quant", x, x_dtype, M, H, ld_x, w,
+                        residual, ld_r, q_fp8, ld_q, scale, s_stride_m, s_stride_g, eps, stream);
 }

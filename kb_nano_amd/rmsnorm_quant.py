@@ -10,9 +10,12 @@ one workgroup of 4 or 8 wavefronts per token.
 Numerics (reference ``csrc/rmsnorm_quant.cu:21-201``): the normalized value
 ``(x * inv_rms) * w`` stays fp32 until the UE8M0 1x128 quantization; the
 fused variant adds the residual first (fp32), stores it back as bf16, and
-overwrites ``input`` with the bf16 normalized row.  bf16 activations only
-(the reference also dispatches fp16/fp32); hidden sizes up to 16384 (8192
-with the residual add), any multiple of 8.
+overwrites ``input`` with the normalized row.  bf16, fp16 or fp32
+activations, as the reference dispatches (weight and residual of the
+input's type), any hidden size that is a multiple of 8: rows of up to 16384
+columns (8192 with the residual add) in registers, longer rows and the
+fp16 / fp32 types by a kernel that reads each row twice, in the same
+summation order.
 """
 from __future__ import annotations
 
@@ -51,7 +54,7 @@ class RMSNormFP8Quant(nn.Module):
 
 class FusedAddRMSNormFP8Quant(nn.Module):
     """``forward(input, residual, weight, eps=1e-6) -> (output_fp8,
-    output_scales, residual)``; modifies ``input`` (normalized bf16 row) and
+    output_scales, residual)``; modifies ``input`` (normalized row) and
     ``residual`` (residual + input) in place (reference :101-134)."""
 
     def forward(self, input: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,

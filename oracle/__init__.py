@@ -105,6 +105,13 @@ def lib():
             L.orc_grouped_gemm_nt_sample.argtypes = [_P, _P, _I64, _I64, _P, _P, _P,
                                                      _I64, _I64, _I64, _I64,
                                                      _P, _I64, _P, _I64, _P, ctypes.c_int]
+            L.orc_rmsnorm_quant_f32.restype = ctypes.c_int
+            L.orc_rmsnorm_quant_f32.argtypes = [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _I64,
+                                                ctypes.c_float, ctypes.c_int]
+            L.orc_float_to_f16.restype = ctypes.c_uint16
+            L.orc_float_to_f16.argtypes = [ctypes.c_float]
+            L.orc_f16_to_float.restype = ctypes.c_float
+            L.orc_f16_to_float.argtypes = [ctypes.c_uint16]
             L.orc_rmsnorm_quant.restype = ctypes.c_int
             L.orc_rmsnorm_quant.argtypes = [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _I64,
                                             ctypes.c_float]
@@ -550,6 +557,41 @@ def rmsnorm_quant(x_bits: np.ndarray, w_bits: np.ndarray, eps: float = 1e-6, res
     if rc:
         raise ValueError(f"orc_rmsnorm_quant failed ({rc})")
     return (q, s) if r is None else (q, s, r, x)
+
+
+_RND = {"bf16": 0, "fp16": 1, "fp32": 2}
+
+
+def rmsnorm_quant_values(x: np.ndarray, w: np.ndarray, dtype: str, eps: float = 1e-6, residual=None):
+    """``rmsnorm_quant`` for bf16, fp16 or fp32 rows (``dtype``): ``x [M, H]``,
+    ``w [H]`` and ``residual`` are float arrays holding numbers of that type;
+    the residual sum and the normalized row written back are rounded to it
+    (tasks/baseline/L1/csrc/rmsnorm_quant.cu:111 dispatches over the float
+    types).  Returns ``(codes, scales)``, plus ``(residual_out, x_out)`` as
+    float32 values for the residual variant.  Same summation order as
+    ``rmsnorm_quant``."""
+    v = np.array(x, dtype=np.float32, copy=True, order="C")
+    wf = np.ascontiguousarray(w, dtype=np.float32)
+    M, H = v.shape
+    if wf.shape != (H,):
+        raise ValueError("weight must be [H]")
+    G = -(-H // 128)
+    q = np.empty((M, H), dtype=np.uint8)
+    s = np.empty((M, G), dtype=np.float32)
+    r = None if residual is None else np.array(residual, dtype=np.float32, copy=True, order="C")
+    rc = lib().orc_rmsnorm_quant_f32(_ptr(v), M, H, H, _ptr(wf), None if r is None else _ptr(r), H, _ptr(q), H,
+                                     _ptr(s), G, 1, float(eps), _RND[dtype])
+    if rc:
+        raise ValueError(f"orc_rmsnorm_quant_f32 failed ({rc})")
+    return (q, s) if r is None else (q, s, r, v)
+
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    """IEEE binary16 bits of float32 values, nearest even (the oracle's C
+    rounding, used by rmsnorm_quant_values)."""
+    f = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    L = lib()
+    return np.array([L.orc_float_to_f16(float(t)) for t in f], dtype=np.uint16).reshape(np.shape(x))
 
 
 # ---------------------------------------------------------------------------

@@ -36,6 +36,8 @@
  *   orc_rmsnorm_quant      tasks/baseline/L1/csrc/rmsnorm_quant.cu:21-93 and :124-201
  *                          (RMSNorm, optional residual add, UE8M0 1x128 quant of the
  *                          fp32 normalized values), in a fixed fp32 reduction order.
+ *   orc_rmsnorm_quant_f32  the same for bf16, fp16 or fp32 rows (the kernel's type
+ *                          dispatch, :111), with orc_float_to_f16 / orc_f16_to_float.
  *
  * Everything is plain scalar C99 on the host; no GPU code.
  */
@@ -56,6 +58,34 @@ uint16_t orc_float_to_bf16(float f) {
     uint32_t lsb = (u >> 16) & 1u;
     u += 0x7FFFu + lsb;
     return (uint16_t)(u >> 16);
+}
+
+/* IEEE binary16: decode, and round a float to it (nearest even; fp16
+ * subnormals kept, magnitudes from 65520 up to infinity, NaN kept quiet). */
+float orc_f16_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    float v;
+    if (e == 0x1F) return u2f(sign | 0x7F800000u | (m << 13));
+    if (e == 0) v = ldexpf((float)m, -24);
+    else v = ldexpf((float)(m | 0x400u), (int)e - 25);
+    return sign ? -v : v;
+}
+
+uint16_t orc_float_to_f16(float f) {
+    const uint32_t u = f2u(f);
+    const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    const uint32_t a = u & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return sign | 0x7E00u | (uint16_t)((a >> 13) & 0x3FFu);
+    if (a >= 0x477FF000u) return sign | 0x7C00u;          /* >= 65520: infinity (ties to the even 2^16) */
+    if (a < 0x38800000u) {                                /* below 2^-14: multiples of 2^-24 */
+        const float t = u2f(a) * 16777216.0f;             /* exact */
+        return sign | (uint16_t)nearbyintf(t);            /* round to nearest even; 1024 is 2^-14 */
+    }
+    uint32_t h = ((((a >> 23) - 112u) << 10) | ((a & 0x7FFFFFu) >> 13));
+    const uint32_t rest = a & 0x1FFFu;
+    if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) h += 1;
+    return sign | (uint16_t)h;
 }
 
 /* Round a double to bf16 directly (one rounding, RNE), including bf16
@@ -408,6 +438,85 @@ int orc_rmsnorm_quant(uint16_t* x, int64_t M, int64_t H, int64_t ld_x, const uin
                  * a NaN quotient becomes -448 */
                 q[m * ld_q + e] = orc_e4m3_encode(fminf(fmaxf(v / sc, -448.0f), 448.0f));
                 if (rr) xr[e] = orc_float_to_bf16(v);
+            }
+            s[m * s_m + g * s_g] = sc;
+        }
+        free(base);
+    }
+    return bad ? 2 : 0;
+}
+
+/* v rounded to bf16 (rnd 0) or fp16 (rnd 1) and back; fp32 (rnd 2) as is. */
+static inline float round_type(float v, int rnd) {
+    if (rnd == 0) return orc_bf16_to_float(orc_float_to_bf16(v));
+    if (rnd == 1) return orc_f16_to_float(orc_float_to_f16(v));
+    return v;
+}
+
+/* orc_rmsnorm_quant for rows of bf16, fp16 or fp32 (rnd 0 / 1 / 2; the
+ * reference dispatches its kernel over the float types,
+ * rmsnorm_quant.cu:111): x, w and r hold the fp32 values of the type's
+ * numbers; the residual sum and the normalized row written back are rounded
+ * to the type.  The same fixed summation order as orc_rmsnorm_quant. */
+int orc_rmsnorm_quant_f32(float* x, int64_t M, int64_t H, int64_t ld_x, const float* w, float* r,
+                          int64_t ld_r, uint8_t* q, int64_t ld_q, float* s, int64_t s_m, int64_t s_g, float eps,
+                          int rnd) {
+    if (H <= 0 || H % 8 || rnd < 0 || rnd > 2) return 1;
+    const int64_t G = (H + 127) / 128, C = (H + 511) / 512;
+    int bad = 0;
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m) {
+        float* base = (float*)malloc((size_t)H * sizeof(float));
+        if (!base) { bad = 1; continue; }
+        float* xr = x + m * ld_x;
+        float* rr = r ? r + m * ld_r : NULL;
+        const int W = C >= 8 ? 8 : 4;
+        float P[8];
+        for (int wv = 0; wv < W; ++wv) {
+            float part[64];
+            for (int l = 0; l < 64; ++l) {
+                float p = 0.0f;
+                for (int64_t c = wv; c < C; c += W) {
+                    const int64_t e0 = c * 512 + 8 * l;
+                    if (e0 >= H) continue;
+                    for (int j = 0; j < 8; ++j) {
+                        const int64_t e = e0 + j;
+                        float a = xr[e];
+                        if (rr) {
+                            a = rr[e] + xr[e];
+                            rr[e] = round_type(a, rnd);
+                            base[e] = rr[e];
+                        } else {
+                            base[e] = a;
+                        }
+                        p = fmaf(a, a, p);
+                    }
+                }
+                part[l] = p;
+            }
+            for (int d = 32; d >= 1; d >>= 1) {
+                float t[64];
+                for (int l = 0; l < 64; ++l) t[l] = part[l] + part[l ^ d];
+                memcpy(part, t, sizeof(t));
+            }
+            P[wv] = part[0];
+        }
+        float ptot = P[0];
+        for (int wv = 1; wv < W; ++wv) ptot = ptot + P[wv];
+        const float inv = 1.0f / sqrtf(ptot / (float)H + eps);
+        for (int64_t g = 0; g < G; ++g) {
+            const int64_t e1 = (g + 1) * 128 < H ? (g + 1) * 128 : H;
+            float amax = 0.0f;
+            for (int64_t e = g * 128; e < e1; ++e) {
+                const float v = (base[e] * inv) * w[e];
+                const float av = fabsf(v);
+                if (av > amax) amax = av;
+            }
+            const float sc = group_scale(amax, 1e-10f, 1);
+            for (int64_t e = g * 128; e < e1; ++e) {
+                const float v = (base[e] * inv) * w[e];
+                q[m * ld_q + e] = orc_e4m3_encode(fminf(fmaxf(v / sc, -448.0f), 448.0f));
+                if (rr) xr[e] = round_type(v, rnd);
             }
             s[m * s_m + g * s_g] = sc;
         }

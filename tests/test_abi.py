@@ -342,17 +342,24 @@ def test_fused_experts_surface():
                      "w2_scale", "w13_scale_dg", "w2_scale_dg", "use_fp8_w8a8", "block_shape"]
 
 
-def test_rmsnorm_quant_rejects_bad_hidden_sizes():
+def test_rmsnorm_quant_rejects_bad_arguments():
+    """Validation before any device call: hidden sizes that are not a
+    multiple of 8, an unknown dtype code, misaligned rows; empty input is a
+    no-op (any H that is a multiple of 8 is accepted)."""
     from kb_nano_amd._lib import lib
     L = lib()
     p = ctypes.c_void_p(4096)   # never dereferenced: validation fails first
     assert L.kbn_rmsnorm_fp8_quant(p, 4, 100, 100, p, None, 0, p, 104, p, 1, 4, 1e-6, None) == 1
     assert "multiple of 8" in _err()
-    assert L.kbn_rmsnorm_fp8_quant(p, 4, 16392, 16392, p, None, 0, p, 16392, p, 1, 4, 1e-6, None) == 1
-    assert "at most 16384" in _err()
-    assert L.kbn_rmsnorm_fp8_quant(p, 4, 8200, 8200, p, p, 8200, p, 8200, p, 1, 4, 1e-6, None) == 1
-    assert "at most 8192" in _err()
+    assert L.kbn_rmsnorm_fp8_quant_typed(p, 3, 4, 1024, 1024, p, None, 0, p, 1024, p, 1, 4, 1e-6, None) == 1
+    assert "dtype code 3" in _err()
+    assert L.kbn_rmsnorm_fp8_quant_typed(p, 2, 4, 1028, 1028, p, None, 0, p, 1032, p, 1, 4, 1e-6, None) == 1
+    assert "multiple of 8" in _err()
+    assert L.kbn_rmsnorm_fp8_quant_typed(p, 1, 4, 1024, 1020, p, None, 0, p, 1024, p, 1, 4, 1e-6, None) == 1
+    assert "row stride" in _err()
     assert L.kbn_rmsnorm_fp8_quant(None, 0, 1024, 1024, None, None, 0, None, 1024, None, 1, 0, 1e-6, None) == 0
+    assert L.kbn_rmsnorm_fp8_quant_typed(None, 2, 0, 40960, 40960, None, None, 0, None, 40960, None, 1, 0, 1e-6,
+                                         None) == 0
 
 
 def test_rmsnorm_quant_surface_matches_reference():

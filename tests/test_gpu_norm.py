@@ -94,19 +94,84 @@ def test_rmsnorm_quant_op_on_3d_input(gpu_device):
 
 
 def test_rmsnorm_quant_rejects_off_path_inputs(gpu_device):
-    from kb_nano_amd import FusedAddRMSNormFP8Quant, RMSNormFP8Quant
+    from kb_nano_amd import RMSNormFP8Quant
     from kb_nano_amd._lib import KbnError
     dev = gpu_device
-    with pytest.raises(TypeError):   # fp16 activations are not on this path
+    with pytest.raises(TypeError):   # float64 is not a type the reference dispatches
+        RMSNormFP8Quant()(torch.zeros(4, 256, dtype=torch.float64, device=dev),
+                          torch.ones(256, dtype=torch.float64, device=dev))
+    with pytest.raises(TypeError, match="dtype"):   # weight of another type than the input
         RMSNormFP8Quant()(torch.zeros(4, 256, dtype=torch.float16, device=dev),
-                          torch.ones(256, dtype=torch.float16, device=dev))
+                          torch.ones(256, dtype=torch.bfloat16, device=dev))
     with pytest.raises(KbnError, match="multiple of 8"):
         RMSNormFP8Quant()(torch.zeros(4, 260, dtype=torch.bfloat16, device=dev),
                           torch.ones(260, dtype=torch.bfloat16, device=dev))
-    with pytest.raises(KbnError, match="at most 8192"):
-        FusedAddRMSNormFP8Quant()(torch.zeros(2, 8200, dtype=torch.bfloat16, device=dev),
-                                  torch.zeros(2, 8200, dtype=torch.bfloat16, device=dev),
-                                  torch.ones(8200, dtype=torch.bfloat16, device=dev))
+
+
+_NP = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}
+
+
+def _check_typed(x, w, r, dev, eps=1e-6):
+    """Run the module (fused add when r is given) on x, w (and r) of one
+    dtype and compare codes, scales, the residual and the normalized row
+    bit for bit with the typed oracle."""
+    from kb_nano_amd import FusedAddRMSNormFP8Quant, RMSNormFP8Quant
+    dt = _NP[x.dtype]
+    f = lambda t: t.float().numpy()
+    if r is None:
+        q, s = RMSNormFP8Quant()(x.to(dev), w.to(dev), eps)
+        torch.cuda.synchronize()
+        q_ref, s_ref = oracle.rmsnorm_quant_values(f(x), f(w), dt, eps=eps)
+    else:
+        xd, rd = x.to(dev), r.to(dev)
+        q, s, _ = FusedAddRMSNormFP8Quant()(xd, rd, w.to(dev), eps)
+        torch.cuda.synchronize()
+        q_ref, s_ref, r_ref, x_ref = oracle.rmsnorm_quant_values(f(x), f(w), dt, eps=eps, residual=f(r))
+        assert rd.dtype == x.dtype and xd.dtype == x.dtype
+        assert np.array_equal(f(rd.cpu()), r_ref, equal_nan=True)
+        assert np.array_equal(f(xd.cpu()), x_ref, equal_nan=True)
+    assert np.array_equal(fp8_codes(q), q_ref)
+    assert np.array_equal(s.cpu().numpy(), s_ref, equal_nan=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M,H", [(3, 200), (17, 4096), (64, 7168), (5, 20480), (4, 8200), (2, 16392)])
+@pytest.mark.parametrize("add", [False, True])
+def test_rmsnorm_quant_any_dtype_and_size(gpu_device, dtype, M, H, add):
+    """fp16 / fp32 rows and rows longer than the register-resident kernel's
+    (bf16 past 16384 columns, or 8192 with the residual add) take the
+    two-pass kernel: bit for bit against the typed oracle, in the same
+    summation order as the bf16 kernel (whose cases below 8192 / 16384
+    columns this also runs)."""
+    print(f"rmsnorm typed {dtype} M={M} H={H} add={add}", flush=True)
+    g = torch.Generator().manual_seed(M * 7 + H + add)
+    x = torch.randn(M, H, generator=g).to(dtype)
+    w = torch.randn(H, generator=g).to(dtype)
+    r = (torch.randn(M, H, generator=g) * 4).to(dtype) if add else None
+    _check_typed(x, w, r, gpu_device)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.bfloat16])
+def test_rmsnorm_quant_typed_edge_rows(gpu_device, dtype):
+    """Zero rows, squares that overflow or underflow fp32, a single non-zero
+    element, NaN and infinity rows, and weights so large that a group's
+    absmax overflows (an infinite scale: finite values code to +-0, as the
+    reference's v / inf; the bf16 case runs the register-resident kernel)."""
+    H = 1024
+    rows = [np.zeros(H, np.float32), np.full(H, 1e30 if dtype != torch.float16 else 6e4, np.float32),
+            np.full(H, 1e-30 if dtype != torch.float16 else 1e-7, np.float32),
+            np.eye(1, H, 77, dtype=np.float32)[0] * 5.0]
+    nan_row = np.linspace(-3, 3, H).astype(np.float32)
+    nan_row[5] = np.nan
+    inf_row = np.linspace(-3, 3, H).astype(np.float32)
+    inf_row[700] = np.inf
+    rows += [nan_row, inf_row, np.linspace(-3, 3, H).astype(np.float32)]
+    x = torch.from_numpy(np.stack(rows)).to(dtype)
+    w = np.linspace(-2, 2, H).astype(np.float32)
+    w[130] = 6e4 if dtype == torch.float16 else 3e38      # group 1's absmax overflows where x is not small
+    _check_typed(x, torch.from_numpy(w).to(dtype), None, gpu_device)
+
+
 
 
 def test_fused_add_rounding_edge_cases(gpu_device):

@@ -610,6 +610,83 @@ def test_rmsnorm_quant_residual_variant():
     assert np.all(np.abs(xo - dq) <= np.abs(xo) * 2.0 ** -3 + np.repeat(s, 128, axis=1) * 2.0 ** -9 + 1e-30)
 
 
+def test_f16_rounding_matches_numpy():
+    """The oracle's binary16 rounding (nearest even, subnormals, overflow from
+    65520) and decoding against numpy's float16 on random fp32 bit patterns,
+    the boundaries, and every binary16 value."""
+    rng = np.random.default_rng(8)
+    bits = np.concatenate([rng.integers(0, 2 ** 32, 100000, dtype=np.uint64).astype(np.uint32),
+                           np.array([0x477FEFFF, 0x477FF000, 0x477FF001, 0x477FE000, 0x38800000, 0x387FFFFF,
+                                     0x33800000, 0x33000000, 0x33000001, 0x32FFFFFF, 0x7F800000, 0xFF800000,
+                                     0, 0x80000000], np.uint32)])
+    f = bits.view(np.float32)
+    f = f[~np.isnan(f)]
+    with np.errstate(over="ignore"):
+        ref = f.astype(np.float16).view(np.uint16)
+    assert np.array_equal(oracle.f32_to_f16_bits(f), ref)
+    L = oracle.lib()
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    dec = np.array([L.orc_f16_to_float(int(h)) for h in allh], np.float32)
+    ref = allh.view(np.float16).astype(np.float32)
+    assert np.all((dec.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(dec) & np.isnan(ref)))
+
+
+def test_rmsnorm_quant_values_bf16_equals_bits_oracle():
+    """The typed restatement on bf16 rows is the bf16 oracle (plain and fused
+    add, H below and above the 8-chunk wavefront switch, and past 16384)."""
+    rng = np.random.default_rng(9)
+    for H in (1024, 7168, 20480):
+        xb, rb, wb = _bf16(rng.standard_normal((5, H))), _bf16(rng.standard_normal((5, H)) * 4), \
+            _bf16(rng.standard_normal(H))
+        f = oracle.bf16_bits_to_f32
+        q1, s1 = oracle.rmsnorm_quant(xb, wb, eps=1e-6)
+        q2, s2 = oracle.rmsnorm_quant_values(f(xb), f(wb), "bf16", eps=1e-6)
+        assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
+        q1, s1, r1, x1 = oracle.rmsnorm_quant(xb, wb, eps=1e-6, residual_bits=rb)
+        q2, s2, r2, x2 = oracle.rmsnorm_quant_values(f(xb), f(wb), "bf16", eps=1e-6, residual=f(rb))
+        assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
+        assert np.array_equal(f(r1), r2) and np.array_equal(f(x1), x2)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
+def test_rmsnorm_quant_values_fp16_fp32_pins(dtype):
+    """fp16 / fp32 rows: the reference's two-kernel bar (RMSNorm, then the
+    1x128 quant; fewer than 7% of codes differ, scales within 0.016), the
+    float64 math (codes equal or adjacent on the e4m3 grid), scale
+    invariance, and the fused add's residual = r + x rounded once to the
+    type, with the normalized row written back in the type."""
+    npt = np.float16 if dtype == "fp16" else np.float32
+    rng = np.random.default_rng(10)
+    M, H, eps = 32, 4096, 1e-6
+    x = rng.standard_normal((M, H)).astype(npt).astype(np.float32)
+    w = rng.standard_normal(H).astype(npt).astype(np.float32)
+    q, s = oracle.rmsnorm_quant_values(x, w, dtype, eps=eps)
+    xd, wd = x.astype(np.float64), w.astype(np.float64)
+    v = xd / np.sqrt((xd * xd).mean(axis=1, keepdims=True) + eps) * wd[None, :]
+    amax = np.maximum(np.abs(v).reshape(M, H // 128, 128).max(axis=2), 1e-10)
+    s64 = np.exp2(np.ceil(np.log2(amax / 448.0)))
+    assert np.mean(s == s64) > 0.999
+    codes64 = oracle.e4m3_encode(np.clip(v / np.repeat(s, 128, axis=1), -448, 448).astype(np.float32))
+    same = q == codes64
+    assert same.mean() > 0.999
+    dq, d64 = oracle.e4m3_decode(q).astype(np.float64), oracle.e4m3_decode(codes64).astype(np.float64)
+    assert np.all(np.abs(dq - d64)[~same] <= (np.abs(d64) * 2.0 ** -3 + 2.0 ** -9)[~same] + 1e-12)
+    norm = (x * (1.0 / np.sqrt((xd * xd).mean(axis=1, keepdims=True) + eps)).astype(np.float32))
+    norm = norm.astype(npt).astype(np.float32) * w[None, :]
+    q2, s2 = oracle.quant_group128_f32(norm.astype(npt).astype(np.float32), use_ue8m0=True)
+    assert np.mean(q != q2) < 0.07 and np.max(np.abs(s - s2)) <= 0.016
+    for k in (-6, 5):
+        qk, sk = oracle.rmsnorm_quant_values(x * np.float32(2.0 ** k), w, dtype, eps=0.0)
+        q0, s0 = oracle.rmsnorm_quant_values(x, w, dtype, eps=0.0)
+        assert np.array_equal(q0, qk) and np.array_equal(s0, sk)
+    r = (rng.standard_normal((M, H)) * 4).astype(npt).astype(np.float32)
+    qa, sa, r_out, x_out = oracle.rmsnorm_quant_values(x, w, dtype, eps=eps, residual=r)
+    assert np.array_equal(r_out, (r + x).astype(npt).astype(np.float32))
+    assert np.array_equal(x_out, x_out.astype(npt).astype(np.float32))
+    qp, sp = oracle.rmsnorm_quant_values(r_out, w, dtype, eps=eps)
+    assert np.mean(qa == qp) > 0.99 and np.mean(sa == sp) > 0.99
+
+
 # ------------------------------------------------------- weight block requant
 
 def _torch_per_block_cast(x: torch.Tensor, use_ue8m0: bool):
