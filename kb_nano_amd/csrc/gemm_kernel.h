@@ -927,6 +927,49 @@ gemm_bs_kernel(const GemmArgs a) {
         const int64_t bytes = (int64_t)min(a.M - m0, BM) * BN * 4;
         const __amdgpu_buffer_rsrc_t dP = __builtin_amdgcn_make_buffer_rsrc(
             a.P + ((int64_t)split * a.tile_count + trel) * BM * BN, (short)0, (int)bytes, (int)kRsrcWord3);
+        // Slabs that fit the idle LDS stages leave as whole rows: each
+        // wavefront parks its fp32 block row-major (16-B chunks rotated by the
+        // row index) and stores TN * 4 bytes per row, whole 128-B lines,
+        // instead of four 32-B pieces per line (which the L2 fills from memory
+        // before merging).  Same slab layout, same values.  One box, HIP
+        // events, weights rotated past the MALL: qkv 64 x 10240 x 8192 22.2 ->
+        // 20.0 us, o 64 x 8192 x 8192 19.8 -> 17.5 us, 32 rows 6-7% faster.
+        // Tiles with few live rows (decode at M < 16) keep the direct
+        // stores: they write few lines, and the LDS round trip cost them
+        // 0.1-0.5 us.
+        constexpr bool kLdsSlab = BM * BN * 4 <= kStages * kStage && (TN == 64 || TN == 32);
+        if constexpr (kLdsSlab) if (min(a.M - m0, BM) >= 16) {
+            constexpr int kCh = TN / 4;                 // 16-B chunks per wavefront row
+            constexpr int kRowB4 = TN * 4;              // bytes per wavefront row
+            constexpr int kRowsPer = 64 / kCh;          // rows per store instruction
+            uint8_t* reg = smem + wave * (TM * kRowB4);
+            __syncthreads();   // every wavefront is past its last stage reads
+            const int h = lane >> 5;
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const int rl = i * 32 + (lane & 31);
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) {
+                        const int c = 8 * j + 2 * p + h;   // this lane's 16-B chunk of the row (4 columns)
+                        const u32x4 v = {__float_as_uint(acc[i][j][4 * p]), __float_as_uint(acc[i][j][4 * p + 1]),
+                                         __float_as_uint(acc[i][j][4 * p + 2]), __float_as_uint(acc[i][j][4 * p + 3])};
+                        *reinterpret_cast<u32x4*>(reg + rl * kRowB4 + ((c + rl) % kCh) * 16) = v;
+                    }
+            }
+            wait_lds();
+            const int cl = lane % kCh, rsub = lane / kCh;
+#pragma unroll
+            for (int it = 0; it < TM / kRowsPer; ++it) {
+                const int rl = it * kRowsPer + rsub;
+                const u32x4 v = *reinterpret_cast<const u32x4*>(reg + rl * kRowB4 + ((cl + rl) % kCh) * 16);
+                const int voff = (wm * TM + rl) * BN * 4 + (wn * TN + cl * 4) * 4;
+                if (a.flags) __builtin_amdgcn_raw_buffer_store_b128(v, dP, voff, 0, kDeviceCoherent);
+                else __builtin_amdgcn_raw_buffer_store_b128(v, dP, voff, 0, 0);
+            }
+            return;
+        }
         const int ncol = wn * TN + 4 * (lane >> 5);
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
