@@ -1024,7 +1024,8 @@ gemm_bs_kernel(const GemmArgs a) {
         const int h = lane >> 5;
         const int ncol = n0 + wn * TN + 8 * h;
         const bool vec = a.vec_store && (n0 + BN <= a.N || a.N % 8 == 0);
-        // 256-row dense tiles and the 128-row MoE tiles: the fragments'
+        // 256-row dense tiles, the 128-row MoE tiles (and short-K 64/128-row
+        // dense tiles, below): the fragments'
         // natural stores write each 128-B line of D as four 32-B pieces (32
         // rows x 32 B per instruction), and the tiles of a wave of workgroups
         // all end at once.  Instead each wavefront parks its bf16 block in the
@@ -1036,12 +1037,15 @@ gemm_bs_kernel(const GemmArgs a) {
         // 825 us; cfg4 grouped down 1007 -> 935 us, gate_up 1965 -> 1929 us
         // (UE8M0), layer 3165 -> 3112 us.  With the natural partial-line
         // stores the non-temporal hint was much slower (q_b 157 -> 284 us):
-        // those pieces must merge in L2.  The 64- and 128-row weight-streaming
-        // tiles keep the direct stores: their outputs are small and their
-        // calls short.
-        constexpr bool kLdsEpi = ((BM == 256 && !kGrouped && !kSorted) || ((kGrouped || kSorted) && BM == 128)) &&
-                                 !kSplitK && (TN == 128 || TN == 96 || TN == 64) && BM * BN * 2 <= kStages * kStage;
-        if (kLdsEpi && vec) {
+        // those pieces must merge in L2.
+        constexpr bool kLdsEpi =
+            !kSplitK && (TN == 128 || TN == 96 || TN == 64) && BM * BN * 2 <= kStages * kStage;
+        // 64- and 128-row dense tiles stage their block only for short K (at
+        // most 16 blocks) and at least 16 live rows: q_b at M = 128 (12
+        // blocks) 13.5 -> 12.7 us, while long-K weight-streaming tiles lost
+        // 2-4% (their workgroup's exit waits on the staging while its
+        // neighbour on the CU streams) and decode rows write few lines
+        if (kLdsEpi && vec && (kGrouped || kSorted || BM == 256 || (KB <= 16 && min(a.M - m0, BM) >= 16))) {
             constexpr int kCh = TN / 8;                            // 16-B chunks per wavefront row
             constexpr int kRowB2 = TN * 2;                         // bytes per wavefront row
             constexpr int kRowsPer = kCh == 12 ? 4 : 64 / kCh;     // rows per store instruction
