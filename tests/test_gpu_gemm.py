@@ -759,3 +759,32 @@ def test_gemm_narrow_64x64_plans(gpu_device, M, N, K):
         _ops.fp8_gemm_bf16a(x, W, sW, D2)
         torch.cuda.synchronize()
     del g
+
+
+@pytest.mark.parametrize("M,N,K,tile", [(16, 200, 896, (64, 128, 1)), (48, 9000, 1024, (64, 128, 1)),
+                                        (100, 200, 896, (128, 128, 1)), (128, 3000, 1536, (128, 128, 1)),
+                                        (16, 1032, 4096, (64, 64, 4)), (16, 8200, 2048, (64, 128, 3)),
+                                        (20, 1004, 1024, (64, 64, 2))])
+def test_gemm_whole_line_store_paths(gpu_device, M, N, K, tile):
+    """Tiles of 16 or more live rows leave the GEMM through LDS as whole
+    lines (short-K data-parallel tiles: the bf16 block; split tiles: the fp32
+    slab); tiles of fewer rows, and rows whose stride is not a multiple of
+    8 columns, store directly.  Each shape plans as `tile` (bm, bn, splits)
+    for both M and M - 1; the NaN-prefilled output is fully written and
+    matches the oracle in every 64x64 block, and the first M - 1 rows are
+    bit-identical to the run on those rows alone (M = 16 against 15: the
+    staged path against the direct one on the same rows)."""
+    print(f"store paths {M}x{N}x{K}", flush=True)
+    from tests._util import assert_all_written, tile_cover
+    for m in (M, M - 1):
+        p = _plan(m, N, K)
+        assert (p[0], p[1], p[5]) == tile, (m, p)
+    qa, sa, qw, sw = quantized_gemm_inputs(M, N, K, seed=M * 3 + N + K)
+    D = _gemm_gpu(qa, sa, qw, sw, gpu_device)
+    assert_all_written(D, f"{M}x{N}x{K}")
+    rows, cols = tile_cover(M, N, np.random.default_rng(M + N + K))
+    ref = oracle.gemm_nt_sample(qa, sa, qw, sw, rows=rows, cols=cols, ue8m0=True)
+    got = D[torch.from_numpy(rows).to(gpu_device)][:, torch.from_numpy(cols).to(gpu_device)]
+    assert_gemm_close(got, ref, f"store paths {M}x{N}x{K}")
+    D1 = _gemm_gpu(qa[:M - 1], sa[:M - 1], qw, sw, gpu_device)
+    assert np.array_equal(bf16_bits(D1), bf16_bits(D[:M - 1])), "rows depend on the row count"
