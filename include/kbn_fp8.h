@@ -238,6 +238,28 @@ int kbn_fp8_grouped_gemm_nt_contiguous(const void* A, int64_t lda, const float* 
                                        int64_t E, int scale_ue8m0, void* stream);
 
 /*
+ * The contiguous grouped GEMM of the experts' gate/up projection with the
+ * SiLU*Mul + 1x128 FP8 quant of its output in the same launch: what
+ * kbn_fp8_grouped_gemm_nt_contiguous into C [M_sum, N2] followed by
+ * kbn_silu_mul_quant_fp8_rows(C, row ids = expert_ids) writes, without C.
+ * Replaces, inside FusedExperts._forward_deep_gemm, the GEMM1 call and the
+ * SiLU*Mul+quant call that reads its output (tasks/baseline/L2/
+ * fused_experts.py:264-270; tasks/baseline/L1/silu_mul_quant_fp8.py:23-76).
+ *   A, sA, B, sB, expert_ids, M_sum, K, E, scale_ue8m0   as the grouped GEMM, B [E, N2, K]
+ *   N2 % 256 == 0: B's rows [0, N2/2) are the gate, [N2/2, N2) the up rows
+ *   q        fp8 [M_sum, N2/2], row stride ldq (multiple of 8)
+ *   q_scale  fp32 (r, g) at q_scale[r*qs_stride_m + g*qs_stride_g]
+ *   For every row r with an expert id in [0, E): h = bf16 GEMM row, y =
+ *   bf16(bf16(silu(h[:N2/2])) * h[N2/2:]), then the 1x128 quant of y with
+ *   absmax floor eps, UE8M0 scales when q_ue8m0.  Other rows are not written.
+ */
+int kbn_fp8_grouped_gemm_silu_quant(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
+                                    int64_t sA_stride_k, const void* B, const float* sB, const int32_t* expert_ids,
+                                    int64_t M_sum, int64_t N2, int64_t K, int64_t E, int scale_ue8m0,
+                                    void* q_fp8, int64_t ldq, float* q_scale, int64_t qs_stride_m,
+                                    int64_t qs_stride_g, float eps, int q_ue8m0, void* stream);
+
+/*
  * Workspace bytes of kbn_moe_permute_contiguous for num_pairs = M * top_k
  * routed pairs and num_experts experts; -1 if num_experts is outside
  * [1, 1024] or num_pairs outside [0, 2^31).  (The reference's torch ops
@@ -456,8 +478,11 @@ int kbn_debug_gemm_plan(int64_t M, int64_t N, int64_t K, int scale_ue8m0, int bf
 /*
  * Test hook (no counterpart in the reference): the kernels' bf16 SiLU
  * applied elementwise to n bf16 bit patterns, for exhaustive checking.
+ * path 0 reads the table as the SiLU*Mul + quant kernels do; path 1 reads it
+ * at the device address hipGetSymbolAddress gives, as the grouped GEMM's
+ * SiLU*Mul epilogue (kbn_fp8_grouped_gemm_silu_quant) does.
  */
-int kbn_debug_silu_bf16(const uint16_t* g_bf16, uint16_t* out_bf16, int64_t n, void* stream);
+int kbn_debug_silu_bf16(const uint16_t* g_bf16, uint16_t* out_bf16, int64_t n, int path, void* stream);
 
 #ifdef __cplusplus
 }

@@ -40,6 +40,9 @@ SIGNATURES = {
     "kbn_fp8_gemm_nt_noalloc": ([_P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _P], _I),
     "kbn_fp8_grouped_gemm_nt_contiguous": (
         [_P, _I64, _P, _I64, _I64, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _P], _I),
+    "kbn_fp8_grouped_gemm_silu_quant": (
+        [_P, _I64, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _I64, _F, _I, _P],
+        _I),
     "kbn_moe_permute_workspace_bytes": ([_I64, _I64], _I64),
     "kbn_moe_permute_contiguous": (
         [_P, _I, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _P, _I,
@@ -56,7 +59,7 @@ SIGNATURES = {
     "kbn_splitk_counter_stats": ([_P, _P, _P], _I),
     "kbn_debug_splitk_regions": ([_I64, _P, _P], _I),
     "kbn_debug_gemm_plan": ([_I64, _I64, _I64, _I, _I, _P], _I),
-    "kbn_debug_silu_bf16": ([_P, _P, _I64, _P], _I),
+    "kbn_debug_silu_bf16": ([_P, _P, _I64, _I, _P], _I),
 }
 
 ABI_VERSION = 1

@@ -518,6 +518,47 @@ def m_grouped_gemm_nt_contiguous(a_fp8: torch.Tensor, a_scale: torch.Tensor, b_f
         M_sum, N, K, E, int(not disable_ue8m0_cast), _stream(c_bf16)), what)
 
 
+def grouped_gemm_silu_quant(a_fp8: torch.Tensor, a_scale: torch.Tensor, b_fp8: torch.Tensor, b_scale: torch.Tensor,
+                            expert_ids: torch.Tensor, disable_ue8m0_cast: bool, out_fp8: torch.Tensor,
+                            out_scale: torch.Tensor, use_ue8m0: bool = True, eps: float = QUANT_EPS) -> None:
+    """The contiguous grouped GEMM of ``b_fp8 [E, N2, K]`` (rows [0, N2/2) the
+    gate, [N2/2, N2) the up projection) with SiLU*Mul + 1x128 quant in its
+    epilogue: ``out_fp8 [M_sum, N2/2]`` and ``out_scale [M_sum, N2/256]`` get
+    exactly what ``m_grouped_gemm_nt_contiguous`` into a bf16 buffer followed
+    by ``silu_mul_quant_fp8(buffer, row_ids=expert_ids)`` writes; rows with id
+    -1 are not written."""
+    what = "grouped_gemm_silu_quant"
+    _dev_check(what, a_fp8, a_scale, b_fp8, b_scale, expert_ids, out_fp8, out_scale)
+    _dtype_check(what, a_fp8, FP8, "a_fp8")
+    _dtype_check(what, b_fp8, FP8, "b_fp8")
+    _dtype_check(what, a_scale, torch.float32, "a_scale")
+    _dtype_check(what, b_scale, torch.float32, "b_scale")
+    _dtype_check(what, expert_ids, torch.int32, "expert_ids")
+    _dtype_check(what, out_fp8, FP8, "out_fp8")
+    _dtype_check(what, out_scale, torch.float32, "out_scale")
+    M_sum, K = a_fp8.shape
+    E, N2, K2 = b_fp8.shape
+    if K2 != K or N2 % 256:
+        raise ValueError(f"{what}: K mismatch {K} vs {K2} or N2={N2} not a multiple of 256")
+    KB, NB = -(-K // GROUP), N2 // GROUP
+    if tuple(out_fp8.shape) != (M_sum, N2 // 2) or tuple(out_scale.shape) != (M_sum, N2 // 2 // GROUP):
+        raise ValueError(f"{what}: outputs must be {(M_sum, N2 // 2)} and {(M_sum, N2 // 2 // GROUP)}")
+    if tuple(expert_ids.shape) != (M_sum,):
+        raise ValueError(f"{what}: expert_ids must be {(M_sum,)}")
+    if tuple(a_scale.shape) != (M_sum, KB) or tuple(b_scale.shape) != (E, NB, KB):
+        raise ValueError(f"{what}: scales must be {(M_sum, KB)} and {(E, NB, KB)}, got "
+                         f"{tuple(a_scale.shape)} / {tuple(b_scale.shape)}")
+    if not (b_fp8.is_contiguous() and b_scale.is_contiguous() and expert_ids.is_contiguous()):
+        raise ValueError(f"{what}: b_fp8, b_scale and expert_ids must be contiguous")
+    if a_fp8.stride(1) != 1 or out_fp8.stride(1) != 1:
+        raise ValueError(f"{what}: a_fp8 and out_fp8 rows must be contiguous")
+    check(lib().kbn_fp8_grouped_gemm_silu_quant(
+        a_fp8.data_ptr(), a_fp8.stride(0), a_scale.data_ptr(), a_scale.stride(0), a_scale.stride(1),
+        b_fp8.data_ptr(), b_scale.data_ptr(), expert_ids.data_ptr(), M_sum, N2, K, E, int(not disable_ue8m0_cast),
+        out_fp8.data_ptr(), out_fp8.stride(0), out_scale.data_ptr(), out_scale.stride(0), out_scale.stride(1),
+        float(eps), int(use_ue8m0), _stream(out_fp8)), what)
+
+
 def moe_permute_contiguous(x: torch.Tensor, x_scale: torch.Tensor, topk_ids: torch.Tensor, num_experts: int,
                            alignment: int, M_sum: int, x_perm: torch.Tensor, scale_perm: torch.Tensor,
                            expert_ids: torch.Tensor, inv_perm: torch.Tensor, zero_padding: bool = True) -> None:
@@ -811,12 +852,15 @@ def fp8_block_requant(w_in: torch.Tensor, s_in: torch.Tensor | None, w_out: torc
         w_out.data_ptr(), s_out.data_ptr(), so_e, so_ld, int(bool(use_ue8m0)), float(eps), _stream(w_out)), what)
 
 
-def debug_silu_bf16(g_bits: torch.Tensor, out_bits: torch.Tensor) -> None:
-    """Test hook: the kernels' silu (bf16 in, bf16 out) on int16 bit patterns."""
+def debug_silu_bf16(g_bits: torch.Tensor, out_bits: torch.Tensor, path: int = 0) -> None:
+    """Test hook: the kernels' silu (bf16 in, bf16 out) on int16 bit patterns;
+    path 0 reads the table as the SiLU kernels do, path 1 at the symbol
+    address the grouped GEMM's SiLU*Mul epilogue is given."""
     _dev_check("debug_silu_bf16", g_bits, out_bits)
     if g_bits.dtype != torch.int16 or out_bits.dtype != torch.int16 or not g_bits.is_contiguous():
         raise TypeError("debug_silu_bf16: contiguous int16 bit patterns expected")
-    check(lib().kbn_debug_silu_bf16(g_bits.data_ptr(), out_bits.data_ptr(), g_bits.numel(), _stream(g_bits)),
+    check(lib().kbn_debug_silu_bf16(g_bits.data_ptr(), out_bits.data_ptr(), g_bits.numel(), int(path),
+                                   _stream(g_bits)),
           "debug_silu_bf16")
 
 

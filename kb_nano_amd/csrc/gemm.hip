@@ -767,6 +767,53 @@ extern "C" int kbn_fp8_grouped_gemm_nt_contiguous(const void* A, int64_t lda, co
     return launch_gemm<128, 256, 3, false, true>(a, sc, st, what);
 }
 
+extern "C" int kbn_fp8_grouped_gemm_silu_quant(const void* A, int64_t lda, const float* sA, int64_t sA_stride_m,
+                                               int64_t sA_stride_k, const void* B, const float* sB,
+                                               const int32_t* expert_ids, int64_t M_sum, int64_t N2, int64_t K,
+                                               int64_t E, int scale_ue8m0, void* q_fp8, int64_t ldq, float* q_scale,
+                                               int64_t qs_stride_m, int64_t qs_stride_g, float eps, int q_ue8m0,
+                                               void* stream) {
+    const char* what = "grouped_gemm_silu_quant";
+    KBN_CHECK_ARG(N2 >= 0 && N2 % 256 == 0, "%s: N2=%lld must be a multiple of 256 ([gate | up], 1x128 groups)",
+                  what, (long long)N2);
+    if (int rc = check_common(what, A, lda, B, K, q_fp8, ldq, M_sum, N2 / 2, K)) return rc;
+    if (M_sum == 0 || N2 == 0) return 0;
+    KBN_CHECK_ARG(K > 0 && E > 0, "%s: K and E must be positive", what);
+    KBN_CHECK_ARG(sA && sB && expert_ids && q_fp8 && q_scale, "%s: null pointer", what);
+    KBN_CHECK_ARG(M_sum % 128 == 0, "%s: M_sum=%lld must be a multiple of the 128-row alignment", what,
+                  (long long)M_sum);
+    KBN_CHECK_ARG((reinterpret_cast<uintptr_t>(q_fp8) & 7u) == 0 && ldq % 8 == 0,
+                  "%s: output rows must be 8-byte aligned", what);
+    KBN_CHECK_ARG(qs_stride_m >= 0 && qs_stride_g >= 0 && (reinterpret_cast<uintptr_t>(q_scale) & 3u) == 0,
+                  "%s: bad output scale strides or alignment", what);
+    KBN_CHECK_ARG(N2 * K < 0x7FFFFFFFLL, "%s: an expert's weights span 2 GiB or more", what);
+    const int64_t NB = N2 / kGroup, KB = K / kGroup;
+    GemmArgs a{};
+    a.A = (const uint8_t*)A; a.lda = lda;
+    if (int rc = check_scale_ranges(what, M_sum, K, sA_stride_m, sA_stride_k, NB, KB)) return rc;
+    a.sA = sA; a.sA_sm = sA_stride_m; a.sA_sk = sA_stride_k;
+    a.sA_bytes = scale_bytes(M_sum, KB, sA_stride_m, sA_stride_k);
+    a.W = (const uint8_t*)B; a.ldw = K; a.w_estride = N2 * K;
+    a.sW = sB; a.sW_ld = KB; a.sW_estride = NB * KB;
+    a.D = nullptr; a.ldd = 0;
+    a.vec_store = 1;
+    a.expert_ids = expert_ids;
+    KBN_CHECK_ARG(E <= 0x7FFFFFFFLL, "%s: too many experts", what);
+    a.M = (int)M_sum; a.N = (int)N2; a.K = (int)K; a.E = (int)E;
+    a.a_pad_zero = K <= kPadZeroMaxK;
+    a.glu_half = (int)(N2 / 2);
+    a.glu_ue8m0 = q_ue8m0 ? 1 : 0;
+    a.glu_eps = eps;
+    a.q2 = static_cast<uint8_t*>(q_fp8); a.ldq2 = ldq;
+    a.s2 = q_scale; a.s2_sm = qs_stride_m; a.s2_sg = qs_stride_g;
+    a.silu_lut = silu_lut_device(what);
+    if (!a.silu_lut) return 1;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    Schedule sc;
+    if (scale_ue8m0) return launch_gemm<128, 256, 3, true, true, 4, 0, false, true>(a, sc, st, what);
+    return launch_gemm<128, 256, 3, false, true, 4, 0, false, true>(a, sc, st, what);
+}
+
 extern "C" int64_t kbn_fp8_fused_moe_gemm_workspace_bytes(int64_t EM, int64_t K) {
     if (EM < 0 || K <= 0 || K % kGroup != 0 || EM > 0x7FFFFFFFLL) return -1;
     return EM * (K / kGroup) * 4;

@@ -108,6 +108,18 @@ struct GemmArgs {
     const int32_t* sWp;
     int64_t sWp_sn, sWp_sk;
     int64_t sWp_bytes;
+    // Grouped gate/up GEMM with SiLU*Mul + 1x128 quant in its epilogue
+    // (kGlu): W rows [0, glu_half) are the gate, [glu_half, 2 glu_half) the
+    // up rows; tile column block t covers gate columns [128 t, 128 t + 128)
+    // and the same up columns.  Row r's y = bf16(silu(bf16 gate) * bf16 up)
+    // leaves as fp8 codes q2[r, 128 t + j] with scale s2[r * s2_sm + t * s2_sg].
+    int glu_half, glu_ue8m0;
+    float glu_eps;
+    uint8_t* q2;
+    int64_t ldq2;
+    float* s2;
+    int64_t s2_sm, s2_sg;
+    const uint16_t* silu_lut;    // device address of the bf16 SiLU table
 };
 
 // Raw buffer descriptor (base, byte range) built from uniform values so it
@@ -239,8 +251,6 @@ static inline int64_t moe_dealt_grid(int64_t tiles_m, int64_t tiles_n) {
     return 8 * (dealt + (total - 8 * dealt + 7) / 8);
 }
 
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
     const bf16x2 p = __builtin_convertvector((f32x2{lo, hi}), bf16x2);  // v_cvt_pk_bf16_f32, RNE
@@ -364,7 +374,7 @@ constexpr int gemm_occupancy(int bm, int bn, int stages, int fuse_a = 0) {
 // wavefront quantizes the 4 kFuseA rows its own DMAs brought, in place,
 // with 16 / kFuseA lanes per row.
 template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, bool kSplitK, int kWaves, bool kSorted = false,
-          int kFuseA = 0, bool kRowW = false>
+          int kFuseA = 0, bool kRowW = false, bool kGlu = false>
 __global__ __launch_bounds__(64 * kWaves, (kStages * (gemm_a_stage_bytes(BM, kFuseA) + BN * 128) +
                                                kStages * 512 * kWaves <=
                                            80 * 1024)
@@ -376,6 +386,8 @@ gemm_bs_kernel(const GemmArgs a) {
                               (kFuseA == 1 || kFuseA == 2 || kFuseA == 4)),
                   "in-kernel activation quant: UE8M0, dense, 64-row tiles of four wavefronts, 16/32/64 rows");
     static_assert(kWaves == 4 || kWaves == 8, "2x2 or 2x4 wavefronts");
+    static_assert(!kGlu || (kGrouped && BM == 128 && BN == 256 && kWaves == 4),
+                  "SiLU*Mul epilogue: the grouped 128x256 tiles (128 gate + 128 up columns, two per wavefront row)");
     static_assert(!kRowW || (kUe8m0 && !kGrouped && !kSorted && !kFuseA && BN <= 64 * kWaves),
                   "packed per-row weight scales: dense UE8M0 tiles, one scale word per tile row and lane");
     constexpr int WM = 2, WN = kWaves / 2;
@@ -410,7 +422,7 @@ gemm_bs_kernel(const GemmArgs a) {
     } else {
         tile_coords<4>(a.tiles_m, a.tiles_n, a.tile_base, kSplitK ? a.splits : 1, tm, tn, trel, split);
     }
-    const int m0 = tm * BM, n0 = tn * BN;
+    const int m0 = tm * BM, n0 = tn * (kGlu ? BN / 2 : BN);   // kGlu: the first gate column
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WN, wn = wave % WN;
@@ -463,7 +475,10 @@ gemm_bs_kernel(const GemmArgs a) {
     const int ch_o = ((lane & 7) ^ ((lane >> 4) | 4)) << 4;
     const int a_e = (int)((wave * kAInstr * 8 + drow) * a.lda) + ch_e + kb0 * kRowB;
     const int a_o = a_e - ch_e + ch_o;
-    const int w_e = (int)((wave * kBInstr * 8 + drow) * a.ldw) + ch_e + kb0 * kRowB;
+    // kGlu: the tile's W rows 128..255 (wavefronts 2 and 3) are the up rows,
+    // glu_half - 128 rows further on than the tile's row index says
+    const int glu_w = kGlu && wave * kBInstr * 8 >= BN / 2 ? (a.glu_half - BN / 2) * (int)a.ldw : 0;
+    const int w_e = (int)((wave * kBInstr * 8 + drow) * a.ldw) + ch_e + kb0 * kRowB + glu_w;
     const int w_o = w_e - ch_e + ch_o;
     // fused A: instruction i of wavefront w fills LDS rows 4 kFuseA w + 4 i + lane / 16
     // with tile row r = w + 16 i + 4 (lane / 16); slot lane % 16 <- global chunk
@@ -523,9 +538,11 @@ gemm_bs_kernel(const GemmArgs a) {
         sw_off0 = live ? (int)((int64_t)(n0 + r) * a.sWp_sn * 4) : kOob;
     } else {
         // the scale blocks the tile's rows touch (a 192-row tile may start mid-block)
-        const bool sw_live = (lane < (((n0 & 127) + BN + 127) >> 7)) & (n0 / 128 + lane < NB);
+        const bool sw_live = kGlu ? lane < 2 : (lane < (((n0 & 127) + BN + 127) >> 7)) & (n0 / 128 + lane < NB);
         sw_kstep = sw_live ? 4 : 0;
-        sw_off0 = sw_live ? (n0 / 128 + lane) * (int)a.sW_ld * 4 + kb0 * 4 : kOob;
+        // kGlu: the gate block, then the up block
+        const int sw_blk = kGlu ? (lane == 0 ? n0 : a.glu_half + n0) / 128 : n0 / 128 + lane;
+        sw_off0 = sw_live ? sw_blk * (int)a.sW_ld * 4 + kb0 * 4 : kOob;
     }
     constexpr int kScaleDma = kFuseA ? 1 : 2;    // scale vectors per stage (no A scales when fused)
     constexpr int kDma = kAInstr + kBInstr + kScaleDma;  // DMA instructions per wave per stage
@@ -1048,7 +1065,9 @@ gemm_bs_kernel(const GemmArgs a) {
         // blocks) 13.5 -> 12.7 us, while long-K weight-streaming tiles lost
         // 2-4% (their workgroup's exit waits on the staging while its
         // neighbour on the CU streams) and decode rows write few lines
-        if (kLdsEpi && vec && (kGrouped || kSorted || BM == 256 || BN == 256 || (KB <= 16 && min(a.M - m0, BM) >= 16))) {
+        static_assert(!kGlu || kLdsEpi, "the SiLU*Mul epilogue runs on the LDS-staged block");
+        if (kLdsEpi && (vec || kGlu) &&
+            (kGrouped || kSorted || BM == 256 || BN == 256 || (KB <= 16 && min(a.M - m0, BM) >= 16))) {
             constexpr int kCh = TN / 8;                            // 16-B chunks per wavefront row
             constexpr int kRowB2 = TN * 2;                         // bytes per wavefront row
             constexpr int kRowsPer = kCh == 12 ? 4 : 64 / kCh;     // rows per store instruction
@@ -1078,10 +1097,37 @@ gemm_bs_kernel(const GemmArgs a) {
             uint64_t row_mask = ~0ull;
             if constexpr (kGrouped) {
                 static_assert(!kGrouped || TM <= 64, "one mask bit per wavefront row");
-                const int r = m0 + wm * TM + lane;
-                row_mask = __ballot(lane < TM && r < a.M && a.expert_ids[r] == expert);
+                // kGlu: the rows of this wavefront's SiLU*Mul pass below
+                const int r = m0 + (kGlu ? wave * (BM / 4) : wm * TM) + lane;
+                row_mask = __ballot(lane < (kGlu ? BM / 4 : TM) && r < a.M && a.expert_ids[r] == expert);
             }
             wait_lds();
+            if constexpr (kGlu) {
+                // SiLU*Mul + 1x128 quant: wavefront w takes tile rows [32 w, 32 w + 32),
+                // 16 lanes (one 128-column group) per row, four rows per pass;
+                // row rt's gate block is wavefront (rt / 64, 0)'s, its up block
+                // wavefront (rt / 64, 1)'s, both laid out as stored above
+                __syncthreads();   // every wavefront's block is in LDS
+                const int sub = lane & 15, rq = lane >> 4;
+#pragma unroll
+                for (int it = 0; it < BM / 4 / 4; ++it) {
+                    const int rt = wave * (BM / 4) + it * 4 + rq;
+                    const int r = m0 + rt;
+                    if ((row_mask >> (it * 4 + rq)) & 1) {   // uniform over the row's 16 lanes
+                        const int bw = rt / TM, rl = rt % TM;
+                        const uint8_t* gate = smem + (bw * WN) * (TM * kRowB2) + rl * kRowB2 + ((sub + rl) % kCh) * 16;
+                        const u32x4 g = *reinterpret_cast<const u32x4*>(gate);
+                        const u32x4 u = *reinterpret_cast<const u32x4*>(gate + TM * kRowB2);
+                        const uint32_t w[4] = {silu_mul_pair(a.silu_lut, g.x, u.x), silu_mul_pair(a.silu_lut, g.y, u.y),
+                                               silu_mul_pair(a.silu_lut, g.z, u.z), silu_mul_pair(a.silu_lut, g.w, u.w)};
+                        uint8_t* q = a.q2 + (int64_t)r * a.ldq2 + n0;
+                        const float sc = a.glu_ue8m0 ? quant8_store<true, false>(w, a.glu_eps, sub, q)
+                                                     : quant8_store<false, false>(w, a.glu_eps, sub, q);
+                        if (sub == 0) a.s2[(int64_t)r * a.s2_sm + (int64_t)(n0 / 128) * a.s2_sg] = sc;
+                    }
+                }
+                return;
+            }
             const bool active = lane < kRowsPer * kCh;             // 96 columns: 48 lanes of 64 store
             const int cl = active ? lane % kCh : 0, rsub = active ? lane / kCh : 0;
             const int col = n0 + wn * TN + cl * 8;
@@ -1253,10 +1299,11 @@ unsigned* splitk_flags_for(hipStream_t st, int64_t tail_tiles);
 int launch_gemm_256(const GemmArgs& a, const Schedule& sc, int64_t K, hipStream_t st, const char* what);
 int launch_gemm_256_roww(const GemmArgs& a, const Schedule& sc, int64_t K, hipStream_t st, const char* what);
 
-template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, int kWaves = 4, int kFuseA = 0, bool kRowW = false>
+template <int BM, int BN, int kStages, bool kUe8m0, bool kGrouped, int kWaves = 4, int kFuseA = 0, bool kRowW = false,
+          bool kGlu = false>
 static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const char* what) {
     a.tiles_m = (a.M + BM - 1) / BM;
-    a.tiles_n = (a.N + BN - 1) / BN;
+    a.tiles_n = kGlu ? a.glu_half / (BN / 2) : (a.N + BN - 1) / BN;
     const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
     KBN_CHECK_ARG(tiles <= 0x7FFFFFFFLL, "%s: too many tiles", what);
     const int64_t dp = (!kGrouped && a.P && sc.splits > 1) ? sc.dp_tiles : tiles;
@@ -1267,7 +1314,7 @@ static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const cha
         a.kb_per_split = a.K / kRowB;
         const int64_t grid = kGrouped ? moe_dealt_grid(a.tiles_m, a.tiles_n) : dp;
         KBN_CHECK_ARG(grid <= 0x7FFFFFFFLL, "%s: too many tiles", what);
-        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped, false, kWaves, false, kFuseA, kRowW>
+        gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped, false, kWaves, false, kFuseA, kRowW, kGlu>
             <<<dim3((unsigned)grid), dim3(64 * kWaves), 0, st>>>(a);
         KBN_CHECK_LAUNCH(what);
     }

@@ -33,17 +33,18 @@
 #include "kbn_common.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace kbn {
 
+// External linkage: a namespace-scope const is otherwise internal, its
+// device symbol stays local in the code object, and the runtime cannot
+// resolve it for hipGetSymbolAddress (silu_lut_device below).
+extern __device__ const uint16_t kSiluLut[65536];
 __device__ const uint16_t kSiluLut[65536] __attribute__((aligned(16))) = {
 #include "silu_lut.inc"
 };
 
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 
 // Launch shape (tunable at build time; defaults are the measured best on MI355X).
@@ -98,90 +99,6 @@ struct GroupCursor {
         }
     }
 };
-
-// bf16(silu(g)) * up for the two bf16 values of each word: the exact fp32
-// products rounded to bf16 by one v_cvt_pk_bf16_f32, returned packed.
-__device__ __forceinline__ uint32_t silu_mul_pair(const uint16_t* __restrict__ lut, uint32_t gw, uint32_t uw) {
-    const float s0 = __uint_as_float((uint32_t)lut[gw & 0xFFFFu] << 16);
-    const float s1 = __uint_as_float((uint32_t)lut[gw >> 16] << 16);
-    const bf16x2 p = __builtin_convertvector((f32x2{s0 * bf16lo(uw), s1 * bf16hi(uw)}), bf16x2);
-    return __builtin_bit_cast(uint32_t, p);
-}
-
-// Largest magnitude of the eight bf16 values in four packed words, as the
-// fp32 bit pattern of that bf16 magnitude.  Magnitude bits of bf16 order
-// like the values they encode (NaN patterns above infinity), so this is a
-// packed 16-bit integer max (v_pk_max_u16) over the sign-cleared words.
-__device__ __forceinline__ uint32_t absmax8_bits(const uint32_t (&w)[4]) {
-    auto mag = [](uint32_t x) { return __builtin_bit_cast(u16x2, x & 0x7FFF7FFFu); };
-    const u16x2 m = __builtin_elementwise_max(__builtin_elementwise_max(mag(w[0]), mag(w[1])),
-                                              __builtin_elementwise_max(mag(w[2]), mag(w[3])));
-    const uint32_t lo = m.x, hi = m.y;
-    return (lo > hi ? lo : hi) << 16;
-}
-
-// Quantize the 8 bf16 values owned by this lane (four packed words; 16
-// lanes per group); returns the group scale (valid in every lane of the
-// group).
-// Codes leave through L2 (plain stores) for the quant kernel: its consumer,
-// the GEMM, reads them next, and at 4096x18432 the cached stores are 7%
-// faster than non-temporal ones (40 against 43 us).  The SiLU kernel's
-// non-temporal stores measure the same either way and are kept.
-//
-// UE8M0 scales: the group absmax comes from the packed magnitudes and the
-// codes from the scaled conversion of the packed values, so the values are
-// never widened to fp32.  A group holding an infinity or a NaN (absmax
-// pattern >= infinity's) takes the general path below, where the absmax
-// ignores NaN as the reference's max does.
-template <bool kUe8m0, bool kNtStore>
-__device__ __forceinline__ float quant8_store(const uint32_t (&w)[4], float eps, int sub,
-                                              uint8_t* __restrict__ qptr) {
-    if constexpr (kUe8m0) {
-        const uint32_t abits = row16_max_u32(absmax8_bits(w));
-        const float sc = ue8m0_ceil_div448(fmaxf(__uint_as_float(abits), eps));
-        // finite absmax and a normal scale (a subnormal one needs eps < 2^-118)
-        if (ue8m0_fast_path(abits, sc)) {
-            const u32x2 o{pack4_e4m3_bf16(w[0], w[1], sc), pack4_e4m3_bf16(w[2], w[3], sc)};
-            if constexpr (kNtStore) __builtin_nontemporal_store(o, reinterpret_cast<u32x2*>(qptr + sub * 8));
-            else *reinterpret_cast<u32x2*>(qptr + sub * 8) = o;
-            return sc;
-        }
-    }
-    // general path: the non-UE8M0 contract, and UE8M0 groups with an
-    // infinity, a NaN or a subnormal scale (uniform over the group's 16 lanes)
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        v[2 * i] = bf16lo(w[i]);
-        v[2 * i + 1] = bf16hi(w[i]);
-    }
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    amax = __uint_as_float(row16_max_u32(__float_as_uint(amax)));
-    amax = fmaxf(amax, eps);
-    float sc = kUe8m0 ? ue8m0_ceil_div448(amax) : amax / kFp8Max;
-    // The reference clamps v / sc to [-448, 448] before the cast.  Here that
-    // clamp can never act on a finite value: sc >= fl(amax / 448), so
-    // |v / sc| <= 448 (1 + 2^-23)^2 < 464, and the hardware conversion rounds
-    // to nearest even, which maps (448, 464] to 448 (it only goes to NaN above
-    // 464).  NaN stays NaN, as under the reference's torch.clamp.  Dropping the
-    // two compares and two selects per element is worth 4% (SiLU) to 14%
-    // (quant) of kernel time.
-    uint32_t lo, hi;
-    if (kUe8m0) {
-        // an infinite absmax gives an infinite scale: x / inf is +-0 for
-        // finite x (code 0x00 / 0x80) and NaN otherwise, as in the reference
-        lo = pack4_e4m3_ue8m0_general(v[0], v[1], v[2], v[3], sc);
-        hi = pack4_e4m3_ue8m0_general(v[4], v[5], v[6], v[7], sc);
-    } else {
-        lo = pack4_e4m3(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
-        hi = pack4_e4m3(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);
-    }
-    if constexpr (kNtStore) __builtin_nontemporal_store(u32x2{lo, hi}, reinterpret_cast<u32x2*>(qptr + sub * 8));
-    else *reinterpret_cast<u32x2*>(qptr + sub * 8) = u32x2{lo, hi};
-    return sc;
-}
 
 // Input element types of the plain quant (the reference's Triton kernel loads
 // any float input and widens it to fp32, tasks/baseline/L1/fp8_linear.py:197).
@@ -347,9 +264,37 @@ __global__ __launch_bounds__(kThreads) void group_quant_kernel(const QuantArgs a
     }
 }
 
-__global__ void silu_bf16_debug_kernel(const uint16_t* __restrict__ g, uint16_t* __restrict__ out, int64_t n) {
+const uint16_t* silu_lut_device(const char* what) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static const uint16_t* ptr[kMaxDevices] = {};
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        set_error("%s: no current HIP device (or device index >= %d)", what, kMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(kSiluLut));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            set_error("%s: hipGetSymbolAddress(kSiluLut) failed on device %d: %s", what, dev, hipGetErrorString(e));
+            return nullptr;
+        }
+        ptr[dev] = static_cast<const uint16_t*>(p);
+    }
+    return ptr[dev];
+}
+
+// path 0: the table read directly; path 1: the table at the device address
+// that hipGetSymbolAddress gives (the grouped GEMM's SiLU*Mul epilogue reads
+// it there)
+__global__ void silu_bf16_debug_kernel(const uint16_t* __restrict__ g, uint16_t* __restrict__ out, int64_t n,
+                                       const uint16_t* __restrict__ lut, int path) {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) out[i] = kSiluLut[g[i]];
+    if (i < n) out[i] = path ? lut[g[i]] : kSiluLut[g[i]];
 }
 
 
@@ -466,12 +411,15 @@ extern "C" int kbn_silu_mul_quant_fp8_rows(const void* in_bf16, int64_t M, int64
     return 0;
 }
 
-extern "C" int kbn_debug_silu_bf16(const uint16_t* g_bf16, uint16_t* out_bf16, int64_t n, void* stream) {
+extern "C" int kbn_debug_silu_bf16(const uint16_t* g_bf16, uint16_t* out_bf16, int64_t n, int path, void* stream) {
     KBN_CHECK_ARG(n >= 0 && n <= 0x7FFFFFFFLL, "debug_silu_bf16: bad n");
+    KBN_CHECK_ARG(path == 0 || path == 1, "debug_silu_bf16: path must be 0 (the table) or 1 (its symbol address)");
     if (n == 0) return 0;
     KBN_CHECK_ARG(g_bf16 && out_bf16, "debug_silu_bf16: null pointer");
+    const uint16_t* lut = silu_lut_device("debug_silu_bf16");
+    if (!lut) return 1;
     silu_bf16_debug_kernel<<<(unsigned)((n + 255) / 256), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
-        g_bf16, out_bf16, n);
+        g_bf16, out_bf16, n, lut, path);
     KBN_CHECK_LAUNCH("debug_silu_bf16");
     return 0;
 }

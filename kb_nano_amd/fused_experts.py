@@ -9,9 +9,12 @@ Mirrors ``FusedExperts`` of ``tasks/baseline/L2/fused_experts.py:139-283``
 
 Every step runs in this package's gfx950 kernels: ``PerTokenGroupQuantFp8``,
 the permute and unpermute-and-reduce of ``moe_layout``,
-``m_grouped_fp8_gemm_nt_contiguous`` and ``SiluMulQuantFp8``.  Scratch
-buffers are shared by all layers, as in the reference (layers run one after
-another).
+``m_grouped_fp8_gemm_nt_contiguous`` and ``SiluMulQuantFp8``.  When the
+SiLU*Mul+quant module is this package's own and unhooked, GEMM1 and that
+step are one launch (``_ops.grouped_gemm_silu_quant``: the GEMM's epilogue
+applies SiLU*Mul and the 1x128 quant to its bf16 tile, the same bits as the
+two launches, with no bf16 intermediate).  Scratch buffers are shared by all
+layers, as in the reference (layers run one after another).
 
 The reference falls back to its Triton ``fused_moe_kernel`` for BF16 weights,
 for shapes DeepGEMM does not take and while a CUDA graph is being captured
@@ -90,6 +93,9 @@ class FusedExperts(nn.Module):
         self.per_token_group_quant_fp8 = PerTokenGroupQuantFp8()
         self.silu_mul_quant_fp8 = SiluMulQuantFp8()
         self._sb = _SHARED_BUF
+        # GEMM1 applies SiLU*Mul + quant in its own epilogue (the same bits as
+        # the two launches) when the SiLU module is this package's and unhooked
+        self.fuse_gate_up_silu = True
 
     def _get_fp8_bufs(self, M: int, K: int, device):
         sb = self._sb
@@ -163,10 +169,23 @@ class FusedExperts(nn.Module):
                                                                         alignment, zero_padding=False,
                                                                         scale_colmajor=True)
 
+        quant_out = self._get_dg_workspace(2, (M_sum, N), dev, torch.float8_e4m3fn)
+        if self.fuse_gate_up_silu and N2 % 256 == 0 and _direct_call_ok(self.silu_mul_quant_fp8):
+            # GEMM1 with SiLU*Mul + quant in its epilogue: the codes and
+            # column-major scales GEMM1 into a bf16 buffer followed by the
+            # row-skipping SiLU*Mul+quant launch below would write, with no
+            # bf16 [M_sum, N2] intermediate written or read
+            a2_fp8 = quant_out
+            a2_scale = torch.empty_strided((M_sum, N // _FP8_GROUP_SIZE), (1, M_sum), dtype=torch.float32,
+                                           device=dev)
+            _ops.grouped_gemm_silu_quant(a1_perm, a1_scale_perm, w13, w13_scale, expert_ids, True, a2_fp8, a2_scale,
+                                         True, 1e-10)
+            return self._down_and_unpermute(a2_fp8, a2_scale, w2, w2_scale, expert_ids, topk_ids, topk_weights,
+                                            inv_perm, M, K, M_sum, dev, hidden_states.dtype)
+
         mm1_out = self._get_dg_workspace(1, (M_sum, N2), dev, hidden_states.dtype)
         m_grouped_fp8_gemm_nt_contiguous((a1_perm, a1_scale_perm), (w13, w13_scale), mm1_out, expert_ids)
 
-        quant_out = self._get_dg_workspace(2, (M_sum, N), dev, torch.float8_e4m3fn)
         if _direct_call_ok(self.silu_mul_quant_fp8):
             # this package's module: the same launch over the rows with an
             # expert id only (padding rows hold nothing GEMM1 wrote, and
@@ -180,10 +199,16 @@ class FusedExperts(nn.Module):
         else:   # a swapped-in or hooked module (or the compiler's trace) keeps the reference's call
             a2_fp8, a2_scale = self.silu_mul_quant_fp8(mm1_out, output=quant_out)
 
-        mm2_out = self._get_dg_workspace(1, (M_sum, K), dev, hidden_states.dtype)
+        return self._down_and_unpermute(a2_fp8, a2_scale, w2, w2_scale, expert_ids, topk_ids, topk_weights,
+                                        inv_perm, M, K, M_sum, dev, hidden_states.dtype)
+
+    def _down_and_unpermute(self, a2_fp8, a2_scale, w2, w2_scale, expert_ids, topk_ids, topk_weights, inv_perm, M, K,
+                            M_sum, dev, dtype) -> torch.Tensor:
+        """GEMM2 and the unpermute-and-reduce (reference :276-283)."""
+        mm2_out = self._get_dg_workspace(1, (M_sum, K), dev, dtype)
         m_grouped_fp8_gemm_nt_contiguous((a2_fp8, a2_scale), (w2, w2_scale), mm2_out, expert_ids)
 
-        output = torch.empty(M, K, dtype=hidden_states.dtype, device=dev)
+        output = torch.empty(M, K, dtype=dtype, device=dev)
         _deepgemm_unpermute_and_reduce(mm2_out, topk_ids, topk_weights, inv_perm, output)
         if torch.cuda.is_current_stream_capturing():
             self._sb.hold_for_graph()

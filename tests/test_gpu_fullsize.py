@@ -166,6 +166,13 @@ def test_fused_experts_cfg4_full_size(gpu_device, cfg4):
     ref = _oracle_expert_tokens(bf16_bits(cfg4["hidden"]), tokens, cfg4["topk_ids"].numpy(),
                                 cfg4["topk_w"].numpy(), cfg4["w13"], cfg4["s13"], cfg4["w2"], cfg4["s2"])
     assert_gemm_close(out[torch.from_numpy(tokens).to(dev)], ref, "FusedExperts cfg4")
+    print("cfg4 FusedExperts layer, GEMM1 to bf16 + separate SiLU*Mul+quant", flush=True)
+    layer = FusedExperts()
+    layer.fuse_gate_up_silu = False
+    out2 = layer(cfg4["hidden"].to(dev), cfg4["w13"], cfg4["w2"], cfg4["topk_w"].to(dev), cfg4["topk_ids"].to(dev),
+                 E, w13_scale=cfg4["s13"], w2_scale=cfg4["s2"], use_fp8_w8a8=True, block_shape=[128, 128])
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16)), "fused GLU epilogue differs at config 4"
 
 
 # ---------------------------------------------------------------- config 5

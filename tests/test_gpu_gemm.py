@@ -347,6 +347,54 @@ def test_grouped_gemm_padding_garbage_is_isolated(gpu_device, K, ue8m0):
     assert torch.all(outs[1][torch.from_numpy(pad).to(dev)] == 7.0)
 
 
+@pytest.mark.parametrize("E,N2,K,M_tok,topk", [(6, 512, 1024, 96, 2), (5, 768, 2560, 80, 2), (8, 4096, 7168, 64, 8)])
+@pytest.mark.parametrize("ue8m0", [True, False])
+def test_grouped_gemm_silu_quant_equals_two_launches(gpu_device, E, N2, K, M_tok, topk, ue8m0):
+    """GEMM1 with SiLU*Mul + 1x128 quant in its epilogue writes exactly the
+    codes and scales of the grouped GEMM into a bf16 buffer followed by the
+    row-skipping SiLU*Mul+quant kernel (both scale contracts of the GEMM,
+    UE8M0 and FP32 quant scales, column-major and row-major scale layouts),
+    leaves rows with id -1 untouched, and its output also matches the oracle's
+    SiLU*Mul+quant of the oracle's GEMM to the bf16 GEMM tolerance."""
+    from kb_nano_amd import _ops
+    print(f"gemm+silu {E}x{N2}x{K} tokens={M_tok} top{topk} ue8m0={ue8m0}", flush=True)
+    dev = gpu_device
+    ids, qa, sa, qb, sb, M_sum = _grouped_case(E, N2, K, M_tok=M_tok, topk=topk, seed=N2 + K, dev=dev)
+    if not ue8m0:
+        sb = (sb * np.float32(1.37)).astype(np.float32)
+    A, sA = to_fp8(qa, dev), torch.from_numpy(sa).to(dev)
+    B, sB, idt = to_fp8(qb, dev), torch.from_numpy(sb).to(dev), torch.from_numpy(ids).to(dev)
+    N = N2 // 2
+    valid = torch.from_numpy(ids >= 0).to(dev)
+    for q_ue8m0 in (False, True):      # the last run (UE8M0) is checked against the oracle below
+        for col_major in (False, True):
+            C = torch.empty((M_sum, N2), dtype=torch.bfloat16, device=dev)
+            _ops.m_grouped_gemm_nt_contiguous(A, sA, B, sB, C, idt, disable_ue8m0_cast=not ue8m0)
+            q1 = torch.full((M_sum, N), 0x5A, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+            shape, strides = (M_sum, N // 128), ((1, M_sum) if col_major else (N // 128, 1))
+            s1 = torch.empty_strided(shape, strides, device=dev).fill_(-3.0)
+            _ops.silu_mul_quant_fp8(C, q1, s1, q_ue8m0, 1e-10, row_ids=idt)
+            q2 = torch.full_like(q1.view(torch.uint8), 0x5A).view(torch.float8_e4m3fn)
+            s2 = torch.empty_strided(shape, strides, device=dev).fill_(-3.0)
+            _ops.grouped_gemm_silu_quant(A, sA, B, sB, idt, not ue8m0, q2, s2, q_ue8m0, 1e-10)
+            torch.cuda.synchronize()
+            assert torch.equal(q2.view(torch.uint8), q1.view(torch.uint8)), (q_ue8m0, col_major)
+            assert torch.equal(s2, s1), (q_ue8m0, col_major)
+            assert torch.all(q2.view(torch.uint8)[~valid] == 0x5A) and torch.all(s2[~valid] == -3.0)
+    # against the oracle: SiLU*Mul+quant of the oracle GEMM, dequantized
+    ref_h = oracle.grouped_gemm_nt_sample(qa, sa, qb, sb, ids, ue8m0=ue8m0)
+    v = ids >= 0
+    hb = oracle.f32_to_bf16_bits(ref_h[v].astype(np.float32))
+    qo, so = oracle.silu_mul_quant(hb, use_ue8m0=True)
+    deq = lambda c, sc: oracle.e4m3_decode(c).astype(np.float64) * np.repeat(sc, 128, axis=1)
+    got = deq(fp8_codes(q2[valid]), s2[valid].cpu().numpy())
+    ref = deq(qo, so)
+    # codes may differ by one e4m3 step where the bf16 GEMM rows differ in the last bit
+    err = np.abs(got - ref).mean() / np.abs(ref).mean()
+    cos = (got * ref).sum() / np.sqrt((got * got).sum() * (ref * ref).sum())
+    assert err < 0.02 and cos > 0.999, (err, cos)
+
+
 # ------------------------------------------------- FP32 scale contract
 # disable_ue8m0_cast: the scales' exponents go to the MFMA, their
 # significands are carried per row and the running sum is rescaled when they

@@ -66,6 +66,30 @@ def test_fused_experts_matches_oracle(gpu_device, M, K, I, E, k):
     assert_gemm_close(out, ref, f"FusedExperts M={M} K={K} I={I} E={E} k={k}")
 
 
+@pytest.mark.parametrize("M,K,I,E,k", [(160, 512, 640, 8, 2), (200, 1024, 768, 16, 6)])
+def test_fused_experts_glu_epilogue_equals_separate_launches(gpu_device, M, K, I, E, k):
+    """GEMM1 with SiLU*Mul + quant in its epilogue gives the same layer output, bit for bit, as
+    GEMM1 to bf16 followed by the separate SiLU*Mul + quant launch."""
+    from kb_nano_amd.fused_experts import FusedExperts
+    dev = gpu_device
+    hidden = from_bits(bf16_bits(seeded_bf16((M, K), seed=M + 7)), dev)
+    topk = torch.from_numpy(_routing(M, k, E, seed=M))
+    topk_w = torch.from_numpy(np.random.default_rng(M + 1).random((M, k)).astype(np.float32))
+    w13, s13 = _experts(E, 2 * I, K, seed=3)
+    w2, s2 = _experts(E, K, I, seed=4)
+    args = (hidden, to_fp8(w13, dev), to_fp8(w2, dev), topk_w.to(dev), topk.to(dev), E)
+    kw = dict(w13_scale=torch.from_numpy(s13).to(dev), w2_scale=torch.from_numpy(s2).to(dev),
+              use_fp8_w8a8=True, block_shape=[128, 128])
+    outs = []
+    for fuse in (False, True):
+        layer = FusedExperts()
+        layer.fuse_gate_up_silu = fuse
+        print(f"FusedExperts M={M} I={I} E={E} k={k} fuse={fuse}", flush=True)
+        outs.append(layer(*args, **kw))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
 def test_fused_experts_rejects_paths_it_does_not_take(gpu_device):
     from kb_nano_amd.fused_experts import FusedExperts
     dev = gpu_device

@@ -171,13 +171,17 @@ def test_quant_empty(gpu_device):
 
 # ------------------------------------------------------------ SiLU + quant
 
-def test_silu_exhaustive(gpu_device):
+@pytest.mark.parametrize("path", [0, 1])
+def test_silu_exhaustive(gpu_device, path):
     """All 65,536 bf16 gate values through the kernels' silu vs the oracle's
-    correctly rounded table (itself pinned against 50-digit decimal)."""
+    correctly rounded table (itself pinned against 50-digit decimal): path 0
+    the table as the SiLU*Mul + quant kernels read it, path 1 at the symbol
+    address the grouped GEMM's SiLU*Mul epilogue reads (every pattern,
+    infinities and NaNs included, the same bits)."""
     from kb_nano_amd import _ops
     g = torch.arange(65536, dtype=torch.int32).to(torch.int16).to(gpu_device)
     out = torch.empty_like(g)
-    _ops.debug_silu_bf16(g, out)
+    _ops.debug_silu_bf16(g, out, path=path)
     torch.cuda.synchronize()
     got = out.cpu().numpy().astype(np.uint16)
     want = oracle.silu_bf16_table()
@@ -185,6 +189,11 @@ def test_silu_exhaustive(gpu_device):
     finite = (allb & 0x7F80) != 0x7F80
     mism = np.nonzero((got != want) & finite)[0]
     assert mism.size == 0, [(hex(i), hex(got[i]), hex(want[i])) for i in mism[:10]]
+    if path == 1:
+        table = torch.empty_like(g)
+        _ops.debug_silu_bf16(g, table, path=0)
+        torch.cuda.synchronize()
+        assert torch.equal(out, table)
 
 
 def _silu_gpu(inp, col_major=True, use_ue8m0=True):
