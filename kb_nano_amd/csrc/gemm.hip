@@ -266,7 +266,8 @@ static int launch_sorted(GemmArgs a, hipStream_t st, const char* what) {
     a.tile_count = (int)tiles;
     a.splits = 1;
     a.kb_per_split = a.K / kRowB;
-    const int64_t grid = moe_dealt_grid(a.tiles_m, a.tiles_n);
+    a.group_m = moe_group_m(a.K);
+    const int64_t grid = moe_dealt_grid(a.tiles_m, a.tiles_n, a.group_m);
     KBN_CHECK_ARG(grid <= 0x7FFFFFFFLL, "%s: too many tiles", what);
     gemm_bs_kernel<BM, BN, kStages, false, false, false, 4, true><<<dim3((unsigned)grid), dim3(256), 0, st>>>(a);
     KBN_CHECK_LAUNCH(what);

@@ -69,6 +69,7 @@ struct GemmArgs {
     const int32_t* expert_ids;   // grouped only
     int M, N, K, E;
     int tiles_m, tiles_n;
+    int group_m;                 // MoE layouts: row tiles per column group (moe_group_m)
     int vec_store;               // D rows allow aligned 16-B stores
     // This launch covers tiles [tile_base, tile_base + tile_count) of the
     // grouped tile order.  Split-K: workgroup (tile, split) accumulates K
@@ -204,7 +205,7 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int tile_b
 // Tile order of the MoE layouts.  Their padded row grid ends in row tiles no
 // expert owns (those workgroups exit at once), so contiguous per-XCD ranges
 // would give the last XCDs nothing but empty tiles (cfg4: two of eight idle).
-// The tile sequence (column groups of kGroupM row tiles, as tile_coords) is
+// The tile sequence (column groups of group_m row tiles, as tile_coords) is
 // split in two parts:
 //   - as many whole column groups as make full rounds of eight are dealt to
 //     the XCDs round-robin: XCD x runs groups x, x + 8, x + 16, ... in order;
@@ -213,12 +214,11 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int tile_b
 // with the rest, and an expert's row tiles still meet its weight panel in one
 // L2.  The grid has moe_dealt_grid slots; a slot past an XCD's share returns
 // false.
-template <int kGroupM>
-__device__ __forceinline__ bool tile_coords_dealt(int tiles_m, int tiles_n, int& tm, int& tn) {
+__device__ __forceinline__ bool tile_coords_dealt(int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
     const int bid = blockIdx.x;
     const int xcd = bid & 7, i = bid >> 3;
     const int total = tiles_m * tiles_n;
-    const int group = kGroupM * tiles_n;
+    const int group = group_m * tiles_n;
     const int rounds = total / group / 8;          // dealt groups per XCD
     const int dealt = rounds * group;              // dealt tiles per XCD
     int t;
@@ -232,21 +232,26 @@ __device__ __forceinline__ bool tile_coords_dealt(int tiles_m, int tiles_n, int&
         t = 8 * dealt + xcd * per + min(xcd, rem) + r;
     }
     const int g = t / group;
-    const int first_m = g * kGroupM;
-    const int gm = min(tiles_m - first_m, kGroupM);
+    const int first_m = g * group_m;
+    const int gm = min(tiles_m - first_m, group_m);
     const int w = t - g * group;
     tm = first_m + w % gm;
     tn = w / gm;
     return true;
 }
-// 16 row tiles per column group measured best at cfg4 (gate_up 1760 us
-// against 1800 with 8, 1770 with 12, 1845 with 24).
-constexpr int kMoeGroupM = 16;
+// Row tiles per column group.  An XCD runs 32 tiles at once, i.e. 32 /
+// group_m columns of the group, and an activation panel is fetched again for
+// each such set of columns; smaller groups cut those fetches but cut more
+// experts' row tiles apart, so more weight panels are fetched twice.  At cfg4
+// (UE8M0, HIP events; HBM fetch per call) gate_up (K = 7168) took 1718 us
+// with 16 (10.65 GB), 1658 with 8 (9.44 GB), 1674 with 4 (9.05 GB) and 1772
+// with 2 (9.57 GB); down (K = 2048) 940 / 943 / 954 / 988 us.
+static inline int moe_group_m(int64_t K) { return K >= 4096 ? 8 : 16; }
 // Workgroups of a dealt launch over tiles_m x tiles_n tiles.
-static inline int64_t moe_dealt_grid(int64_t tiles_m, int64_t tiles_n) {
+static inline int64_t moe_dealt_grid(int64_t tiles_m, int64_t tiles_n, int64_t group_m) {
     const int64_t total = tiles_m * tiles_n;
     if (total <= 0) return 0;
-    const int64_t group = kMoeGroupM * tiles_n;
+    const int64_t group = group_m * tiles_n;
     const int64_t dealt = total / group / 8 * group;
     return 8 * (dealt + (total - 8 * dealt + 7) / 8);
 }
@@ -412,13 +417,13 @@ gemm_bs_kernel(const GemmArgs a) {
     static_assert(!kGrouped || BM == 128, "grouped tiles cover one 128-row block of the contiguous layout");
 
     int tm, tn, trel = 0, split = 0;
-    // MoE tiles walk column groups of kMoeGroupM row tiles dealt over the
+    // MoE tiles walk column groups of a.group_m row tiles dealt over the
     // XCDs (tile_coords_dealt), so an expert's row tiles meet its weight panel
     // in one L2; dense tiles walk groups of 4 row tiles, which the split
     // reduction's tile order also assumes
     if constexpr (kGrouped || kSorted) {
         static_assert(!kSplitK, "MoE layouts run data-parallel");
-        if (!tile_coords_dealt<kMoeGroupM>(a.tiles_m, a.tiles_n, tm, tn)) return;
+        if (!tile_coords_dealt(a.tiles_m, a.tiles_n, a.group_m, tm, tn)) return;
     } else {
         tile_coords<4>(a.tiles_m, a.tiles_n, a.tile_base, kSplitK ? a.splits : 1, tm, tn, trel, split);
     }
@@ -1312,7 +1317,8 @@ static int launch_gemm(GemmArgs a, const Schedule& sc, hipStream_t st, const cha
         a.tile_count = (int)dp;
         a.splits = 1;
         a.kb_per_split = a.K / kRowB;
-        const int64_t grid = kGrouped ? moe_dealt_grid(a.tiles_m, a.tiles_n) : dp;
+        if (kGrouped) a.group_m = moe_group_m(a.K);
+        const int64_t grid = kGrouped ? moe_dealt_grid(a.tiles_m, a.tiles_n, a.group_m) : dp;
         KBN_CHECK_ARG(grid <= 0x7FFFFFFFLL, "%s: too many tiles", what);
         gemm_bs_kernel<BM, BN, kStages, kUe8m0, kGrouped, false, kWaves, false, kFuseA, kRowW, kGlu>
             <<<dim3((unsigned)grid), dim3(64 * kWaves), 0, st>>>(a);
