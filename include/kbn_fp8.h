@@ -244,7 +244,7 @@ int kbn_fp8_grouped_gemm_nt_contiguous(const void* A, int64_t lda, const float* 
  * kbn_silu_mul_quant_fp8_rows(C, row ids = expert_ids) writes, without C.
  * Replaces, inside FusedExperts._forward_deep_gemm, the GEMM1 call and the
  * SiLU*Mul+quant call that reads its output (tasks/baseline/L2/
- * fused_experts.py:264-270; tasks/baseline/L1/silu_mul_quant_fp8.py:23-76).
+ * fused_experts.py:264-274; tasks/baseline/L1/silu_mul_quant_fp8.py:23-76).
  *   A, sA, B, sB, expert_ids, M_sum, K, E, scale_ue8m0   as the grouped GEMM, B [E, N2, K]
  *   N2 % 256 == 0: B's rows [0, N2/2) are the gate, [N2/2, N2) the up rows
  *   q        fp8 [M_sum, N2/2], row stride ldq (multiple of 8)
