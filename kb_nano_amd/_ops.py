@@ -422,6 +422,30 @@ _WS_CACHE: dict = {}
 _WS_BUFS: dict = {}
 
 
+def scales_are_pow2(s: torch.Tensor) -> bool:
+    """Whether every element of the fp32 block-scale tensor ``s`` is a
+    positive, finite power of two.  The block-scaled GEMMs then give the same
+    bits under the UE8M0 and the FP32 scale contracts: the FP32 contract's
+    per-block significands are all 1, so it never rescales its running sums.
+
+    Checked on the device (one reduction and a synchronize) once per tensor
+    object, storage and version; a view shares its base's version counter,
+    and this package's in-place scale writers (``fp8_block_requant``) bump it.
+    During graph capture an unchecked tensor counts as not all powers of two
+    (nothing synchronizes there)."""
+    tag = getattr(s, "_kbn_pow2", None)
+    key = (s._version, s.data_ptr(), s.shape, s.stride())
+    if tag is not None and tag[0] == key:
+        return tag[1]
+    if s.dtype is not torch.float32 or (s.is_cuda and _capturing()):
+        return False
+    b = s.view(torch.int32)
+    e = (b >> 23) & 0xFF
+    r = bool(((b & -0x7F800001) == 0).logical_and_(e != 0).logical_and_(e != 255).all())
+    s._kbn_pow2 = (key, r)
+    return r
+
+
 def _workspace(nbytes: int, idx: int, stream: int, like: torch.Tensor) -> torch.Tensor:
     """Scratch for one launch on ``stream``.  Eager launches on a stream reuse
     one buffer per (device, stream), grown as needed: launches on a stream
@@ -850,6 +874,10 @@ def fp8_block_requant(w_in: torch.Tensor, s_in: torch.Tensor | None, w_out: torc
     check(lib().kbn_fp8_block_requant(
         w_in.data_ptr(), int(in_f32), s_in.data_ptr() if not in_f32 else None, si_e, si_ld, E, N, K,
         w_out.data_ptr(), s_out.data_ptr(), so_e, so_ld, int(bool(use_ue8m0)), float(eps), _stream(w_out)), what)
+    # written through raw pointers: tell torch (and scales_are_pow2's cache)
+    # that both tensors changed
+    torch.autograd.graph.increment_version(w_out)
+    torch.autograd.graph.increment_version(s_out)
 
 
 def debug_silu_bf16(g_bits: torch.Tensor, out_bits: torch.Tensor, path: int = 0) -> None:

@@ -66,15 +66,22 @@ class _SharedBuf:
 _SHARED_BUF = _SharedBuf()
 
 
+def _own_module(mod: nn.Module, cls) -> bool:
+    """Whether ``mod`` is this package's ``cls`` with no forward hook or
+    pre-hook (its own or a global one) and no compiler trace running: its
+    outputs are then known (e.g. power-of-two scales)."""
+    return (type(mod) is cls and not torch.compiler.is_compiling()
+            and not mod._forward_hooks and not mod._forward_pre_hooks
+            and not _module._global_forward_hooks and not _module._global_forward_pre_hooks)
+
+
 def _direct_call_ok(mod: nn.Module) -> bool:
     """Whether the experts layer may launch the SiLU*Mul+quant kernel itself
     (over the rows with an expert id only) instead of calling the submodule:
     only for this package's own module, outside a compiler trace, and when
     no forward hook or pre-hook (the module's own or a global one) would see
     the call the reference makes (tasks/baseline/L2/fused_experts.py:272)."""
-    return (type(mod) is SiluMulQuantFp8 and not torch.compiler.is_compiling()
-            and not mod._forward_hooks and not mod._forward_pre_hooks
-            and not _module._global_forward_hooks and not _module._global_forward_pre_hooks)
+    return _own_module(mod, SiluMulQuantFp8)
 
 
 class FusedExperts(nn.Module):
@@ -96,6 +103,10 @@ class FusedExperts(nn.Module):
         # GEMM1 applies SiLU*Mul + quant in its own epilogue (the same bits as
         # the two launches) when the SiLU module is this package's and unhooked
         self.fuse_gate_up_silu = True
+        # the grouped GEMMs run the UE8M0 kernels where they give the FP32
+        # contract's bits: weight scales all powers of two, activation scales
+        # from this package's quant (which writes powers of two)
+        self.ue8m0_when_exact = True
 
     def _get_fp8_bufs(self, M: int, K: int, device):
         sb = self._sb
@@ -170,6 +181,13 @@ class FusedExperts(nn.Module):
                                                                         scale_colmajor=True)
 
         quant_out = self._get_dg_workspace(2, (M_sum, N), dev, torch.float8_e4m3fn)
+        # the reference runs both GEMMs under the FP32 contract (its scales as
+        # given, disable_ue8m0_cast=True); where every scale is a power of
+        # two the UE8M0 kernels give the same bits, and skip the contract's
+        # per-block significand bookkeeping
+        exact = self.ue8m0_when_exact and _own_module(self.per_token_group_quant_fp8, PerTokenGroupQuantFp8)
+        ue1 = exact and _ops.scales_are_pow2(w13_scale)
+        ue2 = self.ue8m0_when_exact and not torch.compiler.is_compiling() and _ops.scales_are_pow2(w2_scale)
         if self.fuse_gate_up_silu and N2 % 256 == 0 and _direct_call_ok(self.silu_mul_quant_fp8):
             # GEMM1 with SiLU*Mul + quant in its epilogue: the codes and
             # column-major scales GEMM1 into a bf16 buffer followed by the
@@ -178,13 +196,17 @@ class FusedExperts(nn.Module):
             a2_fp8 = quant_out
             a2_scale = torch.empty_strided((M_sum, N // _FP8_GROUP_SIZE), (1, M_sum), dtype=torch.float32,
                                            device=dev)
-            _ops.grouped_gemm_silu_quant(a1_perm, a1_scale_perm, w13, w13_scale, expert_ids, True, a2_fp8, a2_scale,
-                                         True, 1e-10)
+            _ops.grouped_gemm_silu_quant(a1_perm, a1_scale_perm, w13, w13_scale, expert_ids, not ue1, a2_fp8,
+                                         a2_scale, True, 1e-10)
             return self._down_and_unpermute(a2_fp8, a2_scale, w2, w2_scale, expert_ids, topk_ids, topk_weights,
-                                            inv_perm, M, K, M_sum, dev, hidden_states.dtype)
+                                            inv_perm, M, K, M_sum, dev, hidden_states.dtype, ue2)
 
         mm1_out = self._get_dg_workspace(1, (M_sum, N2), dev, hidden_states.dtype)
-        m_grouped_fp8_gemm_nt_contiguous((a1_perm, a1_scale_perm), (w13, w13_scale), mm1_out, expert_ids)
+        if ue1:
+            _ops.m_grouped_gemm_nt_contiguous(a1_perm, a1_scale_perm, w13, w13_scale, mm1_out, expert_ids,
+                                              disable_ue8m0_cast=False)
+        else:
+            m_grouped_fp8_gemm_nt_contiguous((a1_perm, a1_scale_perm), (w13, w13_scale), mm1_out, expert_ids)
 
         if _direct_call_ok(self.silu_mul_quant_fp8):
             # this package's module: the same launch over the rows with an
@@ -198,15 +220,22 @@ class FusedExperts(nn.Module):
             _ops.silu_mul_quant_fp8(mm1_out, a2_fp8, a2_scale, True, 1e-10, row_ids=expert_ids)
         else:   # a swapped-in or hooked module (or the compiler's trace) keeps the reference's call
             a2_fp8, a2_scale = self.silu_mul_quant_fp8(mm1_out, output=quant_out)
+            ue2 = False   # its scales are not known to be powers of two
 
         return self._down_and_unpermute(a2_fp8, a2_scale, w2, w2_scale, expert_ids, topk_ids, topk_weights,
-                                        inv_perm, M, K, M_sum, dev, hidden_states.dtype)
+                                        inv_perm, M, K, M_sum, dev, hidden_states.dtype, ue2)
 
     def _down_and_unpermute(self, a2_fp8, a2_scale, w2, w2_scale, expert_ids, topk_ids, topk_weights, inv_perm, M, K,
-                            M_sum, dev, dtype) -> torch.Tensor:
-        """GEMM2 and the unpermute-and-reduce (reference :276-283)."""
+                            M_sum, dev, dtype, ue8m0: bool = False) -> torch.Tensor:
+        """GEMM2 and the unpermute-and-reduce (reference :276-283); ``ue8m0``:
+        every scale is a power of two, so the UE8M0 kernel gives the FP32
+        contract's bits."""
         mm2_out = self._get_dg_workspace(1, (M_sum, K), dev, dtype)
-        m_grouped_fp8_gemm_nt_contiguous((a2_fp8, a2_scale), (w2, w2_scale), mm2_out, expert_ids)
+        if ue8m0:
+            _ops.m_grouped_gemm_nt_contiguous(a2_fp8, a2_scale, w2, w2_scale, mm2_out, expert_ids,
+                                              disable_ue8m0_cast=False)
+        else:
+            m_grouped_fp8_gemm_nt_contiguous((a2_fp8, a2_scale), (w2, w2_scale), mm2_out, expert_ids)
 
         output = torch.empty(M, K, dtype=dtype, device=dev)
         _deepgemm_unpermute_and_reduce(mm2_out, topk_ids, topk_weights, inv_perm, output)

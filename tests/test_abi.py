@@ -624,3 +624,32 @@ def test_weight_stream_plans_narrow_and_wide():
     assert tuple(_plan(L, 4096, 7168, 18432)[:2]) == (256, 256)
     assert L.kbn_debug_gemm_plan(65, 2048, 2048, 1, 1, np.zeros(9, np.int64).ctypes.data) == 1
     assert "bad arguments" in _err()
+
+
+def test_scales_are_pow2_predicate_and_cache():
+    """The check that lets the MoE layers run the UE8M0 kernels under the
+    FP32 contract: true only when every scale is a positive, finite, normal
+    power of two; its per-tensor answer is recomputed after an in-place change
+    (through the tensor or a view of it) and after this package's raw-pointer
+    scale writer bumps the version."""
+    import torch
+    from kb_nano_amd import _ops
+    s = torch.tensor([[1.0, 0.5, 2.0 ** -100], [2.0 ** 100, 4.0, 2.0 ** -126]])
+    assert _ops.scales_are_pow2(s)
+    for bad in (1.1, 0.0, -2.0, float("inf"), float("nan"), 1e-40, 3.0):
+        t = s.clone()
+        t[1, 1] = bad
+        assert not _ops.scales_are_pow2(t), bad
+    s[0, 0] = 1.5                      # in place: the version moves, the answer follows
+    assert not _ops.scales_are_pow2(s)
+    s[0, 0] = 8.0
+    assert _ops.scales_are_pow2(s)
+    s[1:].fill_(0.75)                  # through a view: the base's version moves too
+    assert not _ops.scales_are_pow2(s)
+    assert not _ops.scales_are_pow2(torch.ones(2, 2, dtype=torch.float64))
+    u = torch.ones(3, 3)
+    assert _ops.scales_are_pow2(u)
+    v0 = u._version
+    torch.autograd.graph.increment_version(u)   # what fp8_block_requant does after writing
+    assert u._version == v0 + 1 and u._kbn_pow2[0][0] == v0
+    assert _ops.scales_are_pow2(u) and u._kbn_pow2[0][0] == v0 + 1

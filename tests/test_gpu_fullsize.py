@@ -173,6 +173,17 @@ def test_fused_experts_cfg4_full_size(gpu_device, cfg4):
                  E, w13_scale=cfg4["s13"], w2_scale=cfg4["s2"], use_fp8_w8a8=True, block_shape=[128, 128])
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16)), "fused GLU epilogue differs at config 4"
+    # config 4's block scales are powers of two: the layer ran the UE8M0 kernels; the
+    # FP32-contract kernels give the same bits
+    from kb_nano_amd import _ops
+    assert _ops.scales_are_pow2(cfg4["s13"]) and _ops.scales_are_pow2(cfg4["s2"])
+    print("cfg4 FusedExperts layer, FP32-contract kernels", flush=True)
+    layer = FusedExperts()
+    layer.ue8m0_when_exact = False
+    out3 = layer(cfg4["hidden"].to(dev), cfg4["w13"], cfg4["w2"], cfg4["topk_w"].to(dev), cfg4["topk_ids"].to(dev),
+                 E, w13_scale=cfg4["s13"], w2_scale=cfg4["s2"], use_fp8_w8a8=True, block_shape=[128, 128])
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), out3.view(torch.int16)), "UE8M0 kernels differ at config 4"
 
 
 # ---------------------------------------------------------------- config 5

@@ -90,6 +90,46 @@ def test_fused_experts_glu_epilogue_equals_separate_launches(gpu_device, M, K, I
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
 
 
+@pytest.mark.parametrize("M,K,I,E,k", [(160, 512, 640, 8, 2), (200, 1024, 768, 16, 6)])
+def test_fused_experts_ue8m0_kernels_on_power_of_two_scales(gpu_device, M, K, I, E, k):
+    """With every weight block scale a power of two the layer runs the UE8M0
+    GEMM kernels under the reference's FP32 contract: the output is the same,
+    bit for bit, as with the FP32-contract kernels (with and without GEMM1's
+    SiLU*Mul+quant epilogue), and the oracle's within tolerance.  Scales that
+    are not all powers of two keep the FP32-contract kernels."""
+    from kb_nano_amd import _ops
+    from kb_nano_amd.fused_experts import FusedExperts
+    dev = gpu_device
+    hb = bf16_bits(seeded_bf16((M, K), seed=M + 11))
+    hidden = from_bits(hb, dev)
+    topk_np = _routing(M, k, E, seed=M + 3)
+    topk_w_np = np.random.default_rng(M + 5).random((M, k)).astype(np.float32)
+    g = torch.Generator().manual_seed(E + K)
+    def experts(N, Kd):
+        codes, scales = zip(*(oracle.quant_block128((torch.randn(N, Kd, generator=g) * 0.02).numpy(),
+                                                    use_ue8m0=True) for _ in range(E)))
+        return np.stack(codes), np.stack(scales)
+    w13, s13 = experts(2 * I, K)
+    w2, s2 = experts(K, I)
+    s13_d, s2_d = torch.from_numpy(s13).to(dev), torch.from_numpy(s2).to(dev)
+    assert _ops.scales_are_pow2(s13_d) and _ops.scales_are_pow2(s2_d)
+    assert not _ops.scales_are_pow2(s13_d * 1.1)
+    args = (hidden, to_fp8(w13, dev), to_fp8(w2, dev), torch.from_numpy(topk_w_np).to(dev),
+            torch.from_numpy(topk_np).to(dev), E)
+    kw = dict(w13_scale=s13_d, w2_scale=s2_d, use_fp8_w8a8=True, block_shape=[128, 128])
+    outs = []
+    for exact, fuse in ((True, True), (True, False), (False, True), (False, False)):
+        layer = FusedExperts()
+        layer.ue8m0_when_exact, layer.fuse_gate_up_silu = exact, fuse
+        print(f"FusedExperts M={M} E={E} ue8m0_when_exact={exact} fuse={fuse}", flush=True)
+        outs.append(layer(*args, **kw))
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(outs[0].view(torch.int16), o.view(torch.int16))
+    ref = _oracle_moe(hb, topk_np, topk_w_np, w13, s13, w2, s2, E)
+    assert_gemm_close(outs[0], ref, f"FusedExperts pow2 scales M={M} E={E}")
+
+
 def test_fused_experts_rejects_paths_it_does_not_take(gpu_device):
     from kb_nano_amd.fused_experts import FusedExperts
     dev = gpu_device
