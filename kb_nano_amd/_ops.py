@@ -422,6 +422,9 @@ _WS_CACHE: dict = {}
 _WS_BUFS: dict = {}
 
 
+_SCALE_WRITES = [0]   # bumped by this package's in-place scale writers
+
+
 def scales_are_pow2(s: torch.Tensor) -> bool:
     """Whether every element of the fp32 block-scale tensor ``s`` is a
     positive, finite power of two.  The block-scaled GEMMs then give the same
@@ -431,10 +434,14 @@ def scales_are_pow2(s: torch.Tensor) -> bool:
     Checked on the device (one reduction and a synchronize) once per tensor
     object, storage and version; a view shares its base's version counter,
     and this package's in-place scale writers (``fp8_block_requant``) bump it.
-    During graph capture an unchecked tensor counts as not all powers of two
-    (nothing synchronizes there)."""
+    Inference tensors (``torch.inference_mode``) have no version counter:
+    for them the check is redone after this package's in-place scale writes
+    only, so a caller that rewrites such a tensor in place by other means
+    sets the layer's ``ue8m0_when_exact`` to False.  During graph capture an
+    unchecked tensor counts as not all powers of two (nothing synchronizes
+    there)."""
     tag = getattr(s, "_kbn_pow2", None)
-    key = (s._version, s.data_ptr(), s.shape, s.stride())
+    key = (-1 if s.is_inference() else s._version, _SCALE_WRITES[0], s.data_ptr(), s.shape, s.stride())
     if tag is not None and tag[0] == key:
         return tag[1]
     if s.dtype is not torch.float32 or (s.is_cuda and _capturing()):
@@ -442,7 +449,10 @@ def scales_are_pow2(s: torch.Tensor) -> bool:
     b = s.view(torch.int32)
     e = (b >> 23) & 0xFF
     r = bool(((b & -0x7F800001) == 0).logical_and_(e != 0).logical_and_(e != 255).all())
-    s._kbn_pow2 = (key, r)
+    try:
+        s._kbn_pow2 = (key, r)
+    except AttributeError:   # a tensor type without attributes: checked again next time
+        pass
     return r
 
 
@@ -878,6 +888,7 @@ def fp8_block_requant(w_in: torch.Tensor, s_in: torch.Tensor | None, w_out: torc
     # that both tensors changed
     torch.autograd.graph.increment_version(w_out)
     torch.autograd.graph.increment_version(s_out)
+    _SCALE_WRITES[0] += 1
 
 
 def debug_silu_bf16(g_bits: torch.Tensor, out_bits: torch.Tensor, path: int = 0) -> None:

@@ -653,3 +653,13 @@ def test_scales_are_pow2_predicate_and_cache():
     torch.autograd.graph.increment_version(u)   # what fp8_block_requant does after writing
     assert u._version == v0 + 1 and u._kbn_pow2[0][0] == v0
     assert _ops.scales_are_pow2(u) and u._kbn_pow2[0][0] == v0 + 1
+    # inference tensors have no version counter: checked once, again after
+    # this package's in-place scale writes (the generation fp8_block_requant bumps)
+    with torch.inference_mode():
+        w = torch.ones(2, 3)
+    assert _ops.scales_are_pow2(w)
+    with torch.inference_mode():
+        w[0, 0] = 3.0
+        assert _ops.scales_are_pow2(w)          # not seen: documented
+        _ops._SCALE_WRITES[0] += 1
+        assert not _ops.scales_are_pow2(w)
