@@ -130,6 +130,34 @@ def test_fused_experts_ue8m0_kernels_on_power_of_two_scales(gpu_device, M, K, I,
     assert_gemm_close(outs[0], ref, f"FusedExperts pow2 scales M={M} E={E}")
 
 
+def test_fused_experts_under_inference_mode(gpu_device):
+    """Weights created and the layer called under torch.inference_mode (the
+    tensors have no version counter): the same bits as outside it."""
+    from kb_nano_amd.fused_experts import FusedExperts
+    dev = gpu_device
+    M, K, I, E, k = 160, 512, 640, 8, 2
+    hidden = from_bits(bf16_bits(seeded_bf16((M, K), seed=21)), dev)
+    topk = torch.from_numpy(_routing(M, k, E, seed=22)).to(dev)
+    topk_w = torch.from_numpy(np.random.default_rng(23).random((M, k)).astype(np.float32)).to(dev)
+    g = torch.Generator().manual_seed(24)
+    def experts(N, Kd):
+        codes, scales = zip(*(oracle.quant_block128((torch.randn(N, Kd, generator=g) * 0.02).numpy(),
+                                                    use_ue8m0=True) for _ in range(E)))
+        return to_fp8(np.stack(codes), dev), torch.from_numpy(np.stack(scales)).to(dev)
+    w13, s13 = experts(2 * I, K)
+    w2, s2 = experts(K, I)
+    kw = dict(use_fp8_w8a8=True, block_shape=[128, 128])
+    ref = FusedExperts()(hidden, w13, w2, topk_w, topk, E, w13_scale=s13, w2_scale=s2, **kw)
+    with torch.inference_mode():
+        iw13, is13, iw2, is2 = w13.clone(), s13.clone(), w2.clone(), s2.clone()
+        layer = FusedExperts()
+        outs = [layer(hidden, iw13, iw2, topk_w, topk, E, w13_scale=is13, w2_scale=is2, **kw) for _ in range(2)]
+    torch.cuda.synchronize()
+    assert is13.is_inference()
+    for o in outs:
+        assert torch.equal(ref.view(torch.int16), o.view(torch.int16))
+
+
 def test_fused_experts_rejects_paths_it_does_not_take(gpu_device):
     from kb_nano_amd.fused_experts import FusedExperts
     dev = gpu_device
