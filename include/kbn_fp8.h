@@ -302,6 +302,27 @@ int kbn_moe_permute_contiguous(const void* topk_ids, int ids_bytes, int64_t M, i
                                void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * kbn_moe_permute_contiguous with the 1x128 FP8 quant of the rows folded in
+ * (no counterpart in one reference call: it replaces FusedExperts'
+ * per_token_group_quant_fp8 of the hidden states followed by
+ * _deepgemm_permute, tasks/baseline/L2/fused_experts.py:257-262).
+ *   x_bf16   bf16 [M, K] (row stride ld_x elements, 16-byte aligned rows),
+ *            K % 128 == 0; top_k <= 64
+ *   x_perm / scale_perm / expert_ids / inv_perm / workspace as in
+ *            kbn_moe_permute_contiguous (row_bytes = K, scale_cols = K/128)
+ *   Each token's row is quantized once, as kbn_per_token_group_quant_fp8
+ *   does (absmax floor eps, UE8M0 scales when use_ue8m0), and its codes and
+ *   scales go to every routed pair's row: the bytes that quant followed by
+ *   kbn_moe_permute_contiguous writes.
+ */
+int kbn_moe_permute_quant_contiguous(const void* topk_ids, int ids_bytes, int64_t M, int64_t top_k,
+                                     int64_t num_experts, int64_t alignment, const void* x_bf16, int64_t ld_x,
+                                     int64_t K, float eps, int use_ue8m0, int64_t M_sum, void* x_perm,
+                                     float* scale_perm, int64_t sp_stride_m, int64_t sp_stride_c,
+                                     int32_t* expert_ids, int32_t* inv_perm, int zero_padding, void* workspace,
+                                     int64_t workspace_bytes, void* stream);
+
+/*
  * Unpermute and top-k weighted reduction.
  * Replaces _deepgemm_unpermute_and_reduce (tasks/baseline/L2/fused_experts.py:119-136).
  *   y         bf16 [M_sum, H] (the second grouped GEMM's output), row stride ld_y

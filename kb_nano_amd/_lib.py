@@ -47,6 +47,8 @@ SIGNATURES = {
     "kbn_moe_permute_contiguous": (
         [_P, _I, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _P, _I,
          _P, _I64, _P], _I),
+    "kbn_moe_permute_quant_contiguous": (
+        [_P, _I, _I64, _I64, _I64, _I64, _P, _I64, _I64, _F, _I, _I64, _P, _P, _I64, _I64, _P, _P, _I, _P, _I64, _P], _I),
     "kbn_moe_unpermute_reduce": ([_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I, _P, _I64, _P], _I),
     "kbn_rmsnorm_fp8_quant": ([_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _F, _P], _I),
     "kbn_rmsnorm_fp8_quant_typed": ([_P, _I, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _F, _P], _I),

@@ -642,6 +642,55 @@ def moe_permute_contiguous(x: torch.Tensor, x_scale: torch.Tensor, topk_ids: tor
         _stream(x_perm)), what)
 
 
+def moe_permute_quant_contiguous(x: torch.Tensor, topk_ids: torch.Tensor, num_experts: int, alignment: int,
+                                 M_sum: int, x_perm: torch.Tensor, scale_perm: torch.Tensor,
+                                 expert_ids: torch.Tensor, inv_perm: torch.Tensor, zero_padding: bool = True,
+                                 use_ue8m0: bool = True, eps: float = QUANT_EPS) -> None:
+    """``per_token_group_quant_fp8(x)`` followed by ``moe_permute_contiguous``
+    in one launch: each bf16 row of ``x [M, K]`` is quantized 1x128 once and
+    its codes and scales are written to the expert-contiguous rows of all the
+    token's routed pairs (``x_perm`` fp8 [M_sum, K], ``scale_perm`` fp32
+    [M_sum, K/128], row- or column-major), with ``expert_ids`` and
+    ``inv_perm`` as the permute writes them; the same bytes as the two
+    launches."""
+    what = "moe_permute_quant_contiguous"
+    _dev_check(what, x, topk_ids, x_perm, scale_perm, expert_ids, inv_perm)
+    _dtype_check(what, x, _BF16, "x")
+    _dtype_check(what, x_perm, FP8, "x_perm")
+    _dtype_check(what, scale_perm, torch.float32, "scale_perm")
+    _dtype_check(what, expert_ids, torch.int32, "expert_ids")
+    _dtype_check(what, inv_perm, torch.int32, "inv_perm")
+    if topk_ids.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"{what}: topk_ids must be int32 or int64, got {topk_ids.dtype}")
+    if x.dim() != 2 or topk_ids.dim() != 2 or topk_ids.shape[0] != x.shape[0]:
+        raise ValueError(f"{what}: x [M, K] and topk_ids [M, top_k] expected, got {tuple(x.shape)} and "
+                         f"{tuple(topk_ids.shape)}")
+    M, K = x.shape
+    top_k = topk_ids.shape[1]
+    cols = K // GROUP
+    if K % GROUP:
+        raise ValueError(f"{what}: K={K} must be a multiple of {GROUP}")
+    if tuple(x_perm.shape) != (M_sum, K) or tuple(scale_perm.shape) != (M_sum, cols):
+        raise ValueError(f"{what}: outputs must be {(M_sum, K)} and {(M_sum, cols)}")
+    if tuple(expert_ids.shape) != (M_sum,) or tuple(inv_perm.shape) != (M, top_k):
+        raise ValueError(f"{what}: expert_ids must be {(M_sum,)} and inv_perm {(M, top_k)}")
+    for t, name in ((topk_ids, "topk_ids"), (x_perm, "x_perm"), (expert_ids, "expert_ids"), (inv_perm, "inv_perm")):
+        if not t.is_contiguous():
+            raise ValueError(f"{what}: {name} must be contiguous")
+    if x.stride(1) != 1 and M > 1:
+        raise ValueError(f"{what}: rows of x must be contiguous")
+    L = lib()
+    ws_bytes = int(L.kbn_moe_permute_workspace_bytes(M * top_k, num_experts))
+    if ws_bytes < 0:
+        raise ValueError(f"{what}: num_experts={num_experts} outside [1, 1024] or too many pairs")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    check(L.kbn_moe_permute_quant_contiguous(
+        topk_ids.data_ptr(), topk_ids.element_size(), M, top_k, num_experts, alignment,
+        x.data_ptr() if M else None, x.stride(0) if M else K, K, float(eps), int(bool(use_ue8m0)), M_sum,
+        x_perm.data_ptr(), scale_perm.data_ptr(), scale_perm.stride(0), scale_perm.stride(1), expert_ids.data_ptr(),
+        inv_perm.data_ptr(), int(zero_padding), ws.data_ptr(), ws_bytes, _stream(x_perm)), what)
+
+
 def moe_unpermute_reduce(y: torch.Tensor, inv_perm: torch.Tensor, topk_weights: torch.Tensor,
                          out: torch.Tensor) -> None:
     """``out[m] = sum_j topk_weights[m, j] * y[inv_perm[m, j]]`` (bf16 rows,

@@ -80,6 +80,7 @@ struct PermuteArgs {
     int M_sum;
     int zero_padding;
     int place_blocks;       // blocks [0, place_blocks) copy pairs, the rest fill rows
+    float eps;              // quantizing permute: the 1x128 quant's absmax floor
     // moe_align_block_size
     int32_t* sorted_ids;    // [sorted_len]: pair index per slot, numel elsewhere
     int sorted_len;
@@ -203,13 +204,68 @@ __device__ __forceinline__ void wave_row(const uint8_t* src, uint8_t* dst, int b
     }
 }
 
+// Quantizing permute (kQuant 1: UE8M0 scales, 2: fp32 scales): a.x holds
+// bf16 rows [M, K] (stride ld_x bytes), and kQuantWaves wavefronts per token
+// (taking turns over steps of kQuantPasses x 4 groups) quantize its row 1x128 once
+// (quant8_codes: the codes and scales of per-token-group quant) and write the
+// codes and the scale of each group to the destination rows of all the
+// token's routed pairs.  At cfg4 (4096 tokens x 7168, top-8) one wavefront
+// per token took 73 us against 78 / 82 us with two / four.
+constexpr int kQuantWaves = 1;
+constexpr int kQuantPasses = 2;
+template <int kQuant>
+__device__ __forceinline__ void place_quant_token(const PermuteArgs& a, int t, int part, int lane) {
+    int dest = -1;
+    if (lane < a.top_k) {   // top_k <= 64, checked on the host
+        const int i = t * a.top_k + lane;
+        const int e = load_id(a, i);
+        if (e >= 0) dest = a.offsets[e] + a.hist[(int64_t)(i / a.chunk) * a.E + e] + a.rank[i];
+        if (part == 0) a.inv_perm[i] = dest;
+    }
+    const uint8_t* xrow = a.x + (int64_t)t * a.ld_x;
+    const int G = a.scale_cols, sub = lane & 15, gq = lane >> 4;
+    for (int g0 = 4 * kQuantPasses * part; g0 < G; g0 += 4 * kQuantPasses * kQuantWaves) {
+        // kQuantPasses x 4 groups per step, 16 lanes per group
+        u32x4 v[kQuantPasses];
+#pragma unroll
+        for (int u = 0; u < kQuantPasses; ++u) {
+            const int g = g0 + 4 * u + gq;
+            v[u] = g < G ? *reinterpret_cast<const u32x4*>(xrow + (int64_t)g * 256 + sub * 16) : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < kQuantPasses; ++u) {
+            const int g = g0 + 4 * u + gq;
+            const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+            float sc;
+            const u32x2 o = quant8_codes<kQuant == 1>(w, a.eps, sc);   // every lane of the 16-lane group
+            if (g < G) {
+                for (int j = 0; j < a.top_k; ++j) {
+                    const int d = __builtin_amdgcn_readlane(dest, j);
+                    if (d < 0) continue;
+                    __builtin_nontemporal_store(
+                        o, reinterpret_cast<u32x2*>(a.xp + (int64_t)d * a.row_bytes + (int64_t)g * 128 + sub * 8));
+                    if (sub == 0) a.sp[(int64_t)d * a.sp_m + (int64_t)g * a.sp_c] = sc;
+                }
+            }
+        }
+    }
+}
+
+template <int kQuant>
 __global__ __launch_bounds__(64 * kPlaceWaves) void moe_place_kernel(const PermuteArgs a) {
     __shared__ int s_off[kMaxExperts + 1];
     __shared__ int s_cnt[kMaxExperts];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
-    if ((int)blockIdx.x < a.place_blocks) {
+    if (kQuant && (int)blockIdx.x < a.place_blocks) {
+        // kQuantWaves wavefronts per token
+        const int tw = (int)blockIdx.x * kPlaceWaves + wave;
+        const int t = tw / kQuantWaves;
+        if (t < a.n / a.top_k) place_quant_token<kQuant>(a, t, tw % kQuantWaves, lane);
+        return;
+    }
+    if (!kQuant && (int)blockIdx.x < a.place_blocks) {
         // one routed pair per wavefront
         const int i = (int)blockIdx.x * kPlaceWaves + wave;
         if (i >= a.n) return;
@@ -497,14 +553,15 @@ extern "C" int64_t kbn_moe_permute_workspace_bytes(int64_t num_pairs, int64_t nu
     return permute_plan(num_pairs, num_experts).bytes;
 }
 
-extern "C" int kbn_moe_permute_contiguous(const void* topk_ids, int ids_bytes, int64_t M, int64_t top_k,
-                                          int64_t num_experts, int64_t alignment, const void* x, int64_t ld_x_bytes,
-                                          int64_t row_bytes, const float* x_scale, int64_t s_stride_m,
-                                          int64_t s_stride_c, int64_t scale_cols, int64_t M_sum, void* x_perm,
-                                          float* scale_perm, int64_t sp_stride_m, int64_t sp_stride_c,
-                                          int32_t* expert_ids, int32_t* inv_perm,
-                                          int zero_padding, void* workspace, int64_t workspace_bytes, void* stream) {
-    const char* what = "moe_permute_contiguous";
+// The contiguous permute; quant 0: copy rows of x (row_bytes each) and their
+// scales; quant 1 / 2: x holds bf16 rows of row_bytes elements, quantized
+// 1x128 on the way (UE8M0 / fp32 scales, absmax floor eps).
+static int permute_impl(const char* what, const void* topk_ids, int ids_bytes, int64_t M, int64_t top_k,
+                        int64_t num_experts, int64_t alignment, const void* x, int64_t ld_x_bytes, int64_t row_bytes,
+                        const float* x_scale, int64_t s_stride_m, int64_t s_stride_c, int64_t scale_cols,
+                        int64_t M_sum, void* x_perm, float* scale_perm, int64_t sp_stride_m, int64_t sp_stride_c,
+                        int32_t* expert_ids, int32_t* inv_perm, int zero_padding, void* workspace,
+                        int64_t workspace_bytes, void* stream, int quant, float eps) {
     KBN_CHECK_ARG(ids_bytes == 4 || ids_bytes == 8, "%s: ids_bytes must be 4 or 8, got %d", what, ids_bytes);
     KBN_CHECK_ARG(M >= 0 && top_k >= 1 && M * top_k <= 0x7FFFFFFFLL, "%s: bad M=%lld top_k=%lld", what,
                   (long long)M, (long long)top_k);
@@ -526,7 +583,7 @@ extern "C" int kbn_moe_permute_contiguous(const void* topk_ids, int ids_bytes, i
             KBN_CHECK_ARG(x && aligned16(x) && ld_x_bytes >= row_bytes && ld_x_bytes % 16 == 0,
                           "%s: x must be 16-byte aligned with a row stride (%lld B) >= row_bytes and a multiple of 16",
                           what, (long long)ld_x_bytes);
-        if (scale_cols > 0) KBN_CHECK_ARG(x_scale, "%s: null x_scale", what);
+        if (scale_cols > 0 && !quant) KBN_CHECK_ARG(x_scale, "%s: null x_scale", what);
     }
     if (row_bytes > 0) KBN_CHECK_ARG(x_perm && aligned16(x_perm), "%s: x_perm must be 16-byte aligned", what);
     if (scale_cols > 0) {
@@ -576,7 +633,9 @@ extern "C" int kbn_moe_permute_contiguous(const void* topk_ids, int ids_bytes, i
     a.inv_perm = inv_perm;
     a.M_sum = (int)M_sum;
     a.zero_padding = zero_padding != 0;
-    a.place_blocks = (int)((n + kPlaceWaves - 1) / kPlaceWaves);
+    a.eps = eps;
+    // a wavefront per routed pair (copy), kQuantWaves per token (quantizing)
+    a.place_blocks = (int)(((quant ? M * kQuantWaves : n) + kPlaceWaves - 1) / kPlaceWaves);
     const int64_t pad_blocks = (M_sum + kPlaceWaves * kPadRowsPerWave - 1) / (kPlaceWaves * kPadRowsPerWave);
 
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -588,10 +647,44 @@ extern "C" int kbn_moe_permute_contiguous(const void* topk_ids, int ids_bytes, i
     KBN_CHECK_LAUNCH(what);
     const int64_t blocks = a.place_blocks + pad_blocks;
     if (blocks > 0) {
-        moe_place_kernel<<<dim3((unsigned)blocks), dim3(64 * kPlaceWaves), 0, st>>>(a);
+        if (quant == 1) moe_place_kernel<1><<<dim3((unsigned)blocks), dim3(64 * kPlaceWaves), 0, st>>>(a);
+        else if (quant == 2) moe_place_kernel<2><<<dim3((unsigned)blocks), dim3(64 * kPlaceWaves), 0, st>>>(a);
+        else moe_place_kernel<0><<<dim3((unsigned)blocks), dim3(64 * kPlaceWaves), 0, st>>>(a);
         KBN_CHECK_LAUNCH(what);
     }
     return 0;
+}
+
+extern "C" int kbn_moe_permute_contiguous(const void* topk_ids, int ids_bytes, int64_t M, int64_t top_k,
+                                          int64_t num_experts, int64_t alignment, const void* x, int64_t ld_x_bytes,
+                                          int64_t row_bytes, const float* x_scale, int64_t s_stride_m,
+                                          int64_t s_stride_c, int64_t scale_cols, int64_t M_sum, void* x_perm,
+                                          float* scale_perm, int64_t sp_stride_m, int64_t sp_stride_c,
+                                          int32_t* expert_ids, int32_t* inv_perm,
+                                          int zero_padding, void* workspace, int64_t workspace_bytes, void* stream) {
+    return permute_impl("moe_permute_contiguous", topk_ids, ids_bytes, M, top_k, num_experts, alignment, x,
+                        ld_x_bytes, row_bytes, x_scale, s_stride_m, s_stride_c, scale_cols, M_sum, x_perm,
+                        scale_perm, sp_stride_m, sp_stride_c, expert_ids, inv_perm, zero_padding, workspace,
+                        workspace_bytes, stream, 0, 0.0f);
+}
+
+extern "C" int kbn_moe_permute_quant_contiguous(const void* topk_ids, int ids_bytes, int64_t M, int64_t top_k,
+                                                int64_t num_experts, int64_t alignment, const void* x_bf16,
+                                                int64_t ld_x, int64_t K, float eps, int use_ue8m0, int64_t M_sum,
+                                                void* x_perm, float* scale_perm, int64_t sp_stride_m,
+                                                int64_t sp_stride_c, int32_t* expert_ids, int32_t* inv_perm,
+                                                int zero_padding, void* workspace, int64_t workspace_bytes,
+                                                void* stream) {
+    const char* what = "moe_permute_quant_contiguous";
+    KBN_CHECK_ARG(K >= 0 && K % kGroup == 0 && K <= 0x3FFFFFFFLL, "%s: K=%lld must be a multiple of 128", what,
+                  (long long)K);
+    KBN_CHECK_ARG(top_k >= 1 && top_k <= 64, "%s: top_k=%lld outside [1, 64]", what, (long long)top_k);
+    KBN_CHECK_ARG(ld_x >= K && ld_x <= 0x3FFFFFFFLL, "%s: ld_x=%lld < K", what, (long long)ld_x);
+    KBN_CHECK_ARG(M == 0 || (x_bf16 && aligned16(x_bf16) && ld_x % 8 == 0),
+                  "%s: x rows must be 16-byte aligned", what);
+    return permute_impl(what, topk_ids, ids_bytes, M, top_k, num_experts, alignment, x_bf16, ld_x * 2, K, nullptr, 0,
+                        0, K / kGroup, M_sum, x_perm, scale_perm, sp_stride_m, sp_stride_c, expert_ids, inv_perm,
+                        zero_padding, workspace, workspace_bytes, stream, use_ue8m0 ? 1 : 2, eps);
 }
 
 extern "C" int kbn_moe_align_block_size(const void* topk_ids, int ids_bytes, int64_t numel, int64_t num_experts,

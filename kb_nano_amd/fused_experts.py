@@ -34,7 +34,7 @@ from torch.nn.modules import module as _module
 from . import _ops
 from .fp8_linear import PerTokenGroupQuantFp8
 from .moe_grouped_gemm import _valid_deep_gemm, m_grouped_fp8_gemm_nt_contiguous
-from .moe_layout import _compute_aligned_M, _deepgemm_permute, _deepgemm_unpermute_and_reduce
+from .moe_layout import _compute_aligned_M, _deepgemm_permute, _deepgemm_permute_quant, _deepgemm_unpermute_and_reduce
 from .silu_mul_quant_fp8 import SiluMulQuantFp8
 
 __all__ = ["FusedExperts", "_compute_aligned_M", "_deepgemm_permute", "_deepgemm_unpermute_and_reduce"]
@@ -107,6 +107,10 @@ class FusedExperts(nn.Module):
         # contract's bits: weight scales all powers of two, activation scales
         # from this package's quant (which writes powers of two)
         self.ue8m0_when_exact = True
+        # the 1x128 quant of the hidden states runs inside the permute (the
+        # same codes and scales, no token-order fp8 copy) when the quant
+        # module is this package's and unhooked
+        self.fuse_quant_permute = True
 
     def _get_fp8_bufs(self, M: int, K: int, device):
         sb = self._sb
@@ -169,24 +173,27 @@ class FusedExperts(nn.Module):
         alignment = _FP8_GROUP_SIZE
         M_sum = _compute_aligned_M(M, top_k, num_experts, alignment)
 
-        a_fp8, a_scale = self._get_fp8_bufs(M, K, dev)
-        self.per_token_group_quant_fp8(hidden_states, a_fp8, a_scale)
-
         # padding rows stay unwritten: the grouped GEMM skips them and never
         # writes their output rows, so nothing downstream reads them.  The
         # scales come out column-major, so GEMM1 reads each K block's row
         # scales contiguously (GEMM2's come column-major from SiLU*Mul+quant).
-        a1_perm, a1_scale_perm, expert_ids, inv_perm = _deepgemm_permute(a_fp8, a_scale, topk_ids, num_experts,
-                                                                        alignment, zero_padding=False,
-                                                                        scale_colmajor=True)
+        own_quant = _own_module(self.per_token_group_quant_fp8, PerTokenGroupQuantFp8)
+        if self.fuse_quant_permute and own_quant and hidden_states.dtype is torch.bfloat16:
+            a1_perm, a1_scale_perm, expert_ids, inv_perm = _deepgemm_permute_quant(
+                hidden_states, topk_ids, num_experts, alignment, zero_padding=False, scale_colmajor=True)
+        else:
+            a_fp8, a_scale = self._get_fp8_bufs(M, K, dev)
+            self.per_token_group_quant_fp8(hidden_states, a_fp8, a_scale)
+            a1_perm, a1_scale_perm, expert_ids, inv_perm = _deepgemm_permute(a_fp8, a_scale, topk_ids, num_experts,
+                                                                            alignment, zero_padding=False,
+                                                                            scale_colmajor=True)
 
         quant_out = self._get_dg_workspace(2, (M_sum, N), dev, torch.float8_e4m3fn)
         # the reference runs both GEMMs under the FP32 contract (its scales as
         # given, disable_ue8m0_cast=True); where every scale is a power of
         # two the UE8M0 kernels give the same bits, and skip the contract's
         # per-block significand bookkeeping
-        exact = self.ue8m0_when_exact and _own_module(self.per_token_group_quant_fp8, PerTokenGroupQuantFp8)
-        ue1 = exact and _ops.scales_are_pow2(w13_scale)
+        ue1 = self.ue8m0_when_exact and own_quant and _ops.scales_are_pow2(w13_scale)
         ue2 = self.ue8m0_when_exact and not torch.compiler.is_compiling() and _ops.scales_are_pow2(w2_scale)
         if self.fuse_gate_up_silu and N2 % 256 == 0 and _direct_call_ok(self.silu_mul_quant_fp8):
             # GEMM1 with SiLU*Mul + quant in its epilogue: the codes and

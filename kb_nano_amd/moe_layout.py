@@ -57,6 +57,28 @@ def _deepgemm_permute(hidden_states: torch.Tensor, a_scale: torch.Tensor, topk_i
     return a_perm, a_scale_perm, expert_ids, inv_perm
 
 
+def _deepgemm_permute_quant(hidden_states: torch.Tensor, topk_ids: torch.Tensor, local_num_experts: int,
+                            alignment: int, zero_padding: bool = True, scale_colmajor: bool = False,
+                            use_ue8m0: bool = True):
+    """The 1x128 quant of bf16 ``hidden_states`` and ``_deepgemm_permute`` of
+    its codes and scales in one launch: the same (a_perm, a_scale_perm,
+    expert_ids, inv_perm) as the two steps, with no token-order fp8 copy."""
+    M, K = hidden_states.shape
+    k = topk_ids.size(1)
+    dev = hidden_states.device
+    M_sum = _compute_aligned_M(M, k, local_num_experts, alignment)
+    a_perm = torch.empty(M_sum, K, dtype=torch.float8_e4m3fn, device=dev)
+    if scale_colmajor:
+        a_scale_perm = torch.empty(K // _GROUP, M_sum, dtype=torch.float32, device=dev).t()
+    else:
+        a_scale_perm = torch.empty(M_sum, K // _GROUP, dtype=torch.float32, device=dev)
+    expert_ids = torch.empty(M_sum, dtype=torch.int32, device=dev)
+    inv_perm = torch.empty(M, k, dtype=torch.int32, device=dev)
+    _ops.moe_permute_quant_contiguous(hidden_states, topk_ids.contiguous(), local_num_experts, alignment, M_sum,
+                                      a_perm, a_scale_perm, expert_ids, inv_perm, zero_padding, use_ue8m0)
+    return a_perm, a_scale_perm, expert_ids, inv_perm
+
+
 def _deepgemm_unpermute_and_reduce(mm2_out: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
                                    inv_perm: torch.Tensor, output: torch.Tensor) -> None:
     """output[m] = sum_j topk_weights[m,j] * mm2_out[inv_perm[m,j]] in the

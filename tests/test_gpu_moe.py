@@ -69,7 +69,8 @@ def test_fused_experts_matches_oracle(gpu_device, M, K, I, E, k):
 @pytest.mark.parametrize("M,K,I,E,k", [(160, 512, 640, 8, 2), (200, 1024, 768, 16, 6)])
 def test_fused_experts_glu_epilogue_equals_separate_launches(gpu_device, M, K, I, E, k):
     """GEMM1 with SiLU*Mul + quant in its epilogue gives the same layer output, bit for bit, as
-    GEMM1 to bf16 followed by the separate SiLU*Mul + quant launch."""
+    GEMM1 to bf16 followed by the separate SiLU*Mul + quant launch; so does the quant of the
+    hidden states folded into the permute, against the quant launch followed by the permute."""
     from kb_nano_amd.fused_experts import FusedExperts
     dev = gpu_device
     hidden = from_bits(bf16_bits(seeded_bf16((M, K), seed=M + 7)), dev)
@@ -81,13 +82,14 @@ def test_fused_experts_glu_epilogue_equals_separate_launches(gpu_device, M, K, I
     kw = dict(w13_scale=torch.from_numpy(s13).to(dev), w2_scale=torch.from_numpy(s2).to(dev),
               use_fp8_w8a8=True, block_shape=[128, 128])
     outs = []
-    for fuse in (False, True):
+    for fuse, fuse_q in ((False, False), (True, False), (False, True), (True, True)):
         layer = FusedExperts()
-        layer.fuse_gate_up_silu = fuse
-        print(f"FusedExperts M={M} I={I} E={E} k={k} fuse={fuse}", flush=True)
+        layer.fuse_gate_up_silu, layer.fuse_quant_permute = fuse, fuse_q
+        print(f"FusedExperts M={M} I={I} E={E} k={k} fuse={fuse} fuse_quant_permute={fuse_q}", flush=True)
         outs.append(layer(*args, **kw))
     torch.cuda.synchronize()
-    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    for o in outs[1:]:
+        assert torch.equal(outs[0].view(torch.int16), o.view(torch.int16))
 
 
 @pytest.mark.parametrize("M,K,I,E,k", [(160, 512, 640, 8, 2), (200, 1024, 768, 16, 6)])
@@ -190,6 +192,55 @@ def _routing(M, k, E, seed):
 def _rand_bytes(shape, seed):
     g = torch.Generator().manual_seed(seed)
     return torch.randint(0, 256, shape, dtype=torch.uint8, generator=g)
+
+
+@pytest.mark.parametrize("M,k,E,align,K,ids_dtype,colmajor,ue8m0,zero_padding", [
+    (200, 8, 32, 128, 7168, torch.int64, True, True, False),     # the experts layer's call
+    (300, 6, 256, 128, 640, torch.int32, False, True, True),     # 5 groups: a partly idle pass
+    (64, 1, 4, 128, 128, torch.int64, True, False, True),        # one group, fp32 scales
+    (1, 8, 8, 128, 1024, torch.int32, False, False, False),
+    (0, 4, 8, 128, 256, torch.int64, False, True, True),
+    (5000, 8, 1024, 1, 384, torch.int32, True, True, False),     # most experts, no padding
+])
+def test_permute_quant_equals_quant_then_permute(gpu_device, M, k, E, align, K, ids_dtype, colmajor, ue8m0,
+                                                  zero_padding):
+    """The permute with the 1x128 quant folded in writes the same bytes as
+    per_token_group_quant_fp8 followed by the permute: codes and scales of
+    every routed pair's row (special values included: NaN, infinities, zero
+    rows, values that round to 448), expert ids, inv_perm (dropped ids -1),
+    and zeroed or untouched padding rows."""
+    from kb_nano_amd import _ops
+    from kb_nano_amd.moe_layout import _compute_aligned_M, _deepgemm_permute, _deepgemm_permute_quant
+    dev = gpu_device
+    print(f"permute+quant M={M} k={k} E={E} K={K} ue8m0={ue8m0} zero_padding={zero_padding}", flush=True)
+    x = seeded_bf16((M, K), seed=M + K + k)
+    if M >= 4:
+        x[0, :128] = float("nan")
+        x[1, 5] = float("inf")
+        x[2, :] = 0.0
+        x[3, 7] = 448.0 * 1.03
+    topk = torch.from_numpy(_routing(M, k, E, seed=M + 1)).to(ids_dtype)
+    if M >= 2:
+        topk[1, 0] = -1
+        topk[M - 1, k - 1] = E + 3
+    xd, td = x.to(dev), topk.to(dev)
+    M_sum = _compute_aligned_M(M, k, E, align)
+    q = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=dev)
+    sq = torch.empty(M, K // 128, device=dev)
+    _ops.per_token_group_quant_fp8(xd, q, sq, use_ue8m0=ue8m0)
+    ref = _deepgemm_permute(q, sq, td, E, align, zero_padding=zero_padding, scale_colmajor=colmajor)
+    got = _deepgemm_permute_quant(xd, td, E, align, zero_padding=zero_padding, scale_colmajor=colmajor,
+                                  use_ue8m0=ue8m0)
+    torch.cuda.synchronize()
+    assert got[1].stride() == ref[1].stride()
+    ids = ref[2].cpu().numpy()
+    assert np.array_equal(ids, got[2].cpu().numpy()) and torch.equal(ref[3], got[3])
+    rows = torch.from_numpy(np.flatnonzero(ids >= 0)).to(dev)
+    assert torch.equal(ref[0].view(torch.uint8)[rows], got[0].view(torch.uint8)[rows])
+    assert torch.equal(ref[1][rows].view(torch.int32), got[1][rows].view(torch.int32))
+    if zero_padding and M_sum > rows.numel():
+        pad = torch.from_numpy(np.flatnonzero(ids < 0)).to(dev)
+        assert not got[0].view(torch.uint8)[pad].any() and not got[1][pad].any()
 
 
 @pytest.mark.parametrize("M,k,E,align,K,ids_dtype,colmajor", [
