@@ -13,8 +13,12 @@ the permute and unpermute-and-reduce of ``moe_layout``,
 SiLU*Mul+quant module is this package's own and unhooked, GEMM1 and that
 step are one launch (``_ops.grouped_gemm_silu_quant``: the GEMM's epilogue
 applies SiLU*Mul and the 1x128 quant to its bf16 tile, the same bits as the
-two launches, with no bf16 intermediate).  Scratch buffers are shared by all
-layers, as in the reference (layers run one after another).
+two launches, with no bf16 intermediate); likewise the quant of the hidden
+states runs inside the permute (``_deepgemm_permute_quant``) when the quant
+module is this package's own.  Where every block scale is a power of two the
+grouped GEMMs run their UE8M0 kernels, which give the bits of the reference's
+scales-as-given contract there.  Scratch buffers are shared by all layers, as
+in the reference (layers run one after another).
 
 The reference falls back to its Triton ``fused_moe_kernel`` for BF16 weights,
 for shapes DeepGEMM does not take and while a CUDA graph is being captured
