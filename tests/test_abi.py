@@ -320,6 +320,49 @@ def test_moe_permute_rejects_bad_arguments():
     assert call(sp=(1, 1)) == 1 and "strides" in _err()
 
 
+def test_moe_permute_quant_rejects_bad_arguments():
+    """The quantizing permute refuses what the copy permute refuses, plus its
+    own limits (bf16 rows: K a multiple of 128, ld_x >= K with 16-byte rows,
+    top_k <= 64), before any launch."""
+    from kb_nano_amd._lib import lib
+    L = lib()
+    p = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+
+    def call(M=4, k=2, E=8, ld=256, K=256, M_sum=None, x=p, ws=1 << 20, sp=(2, 1)):
+        M_sum = (M * k + E * 127 + 127) // 128 * 128 if M_sum is None else M_sum
+        return L.kbn_moe_permute_quant_contiguous(p, 8, M, k, E, 128, x, ld, K, 1e-10, 1, M_sum, p, p, sp[0], sp[1],
+                                                  p, p, 0, p, ws, None)
+    assert call(K=200, ld=200) == 1 and "multiple of 128" in _err()
+    assert call(k=65, E=128) == 1 and "top_k" in _err()
+    assert call(ld=128) == 1 and "ld_x" in _err()
+    assert call(ld=260) == 1 and "16-byte aligned" in _err()
+    assert call(x=ctypes.c_void_p(4098)) == 1 and "16-byte aligned" in _err()
+    assert call(M_sum=1152) == 1 and "M_sum" in _err()
+    assert call(ws=16) == 1 and "workspace" in _err()
+    assert call(sp=(1, 1)) == 1 and "strides" in _err()
+
+
+def test_grouped_gemm_silu_quant_rejects_bad_arguments():
+    """The grouped GEMM with the SiLU*Mul + quant epilogue refuses shapes it
+    cannot tile (N2 not a multiple of 256, M_sum not a multiple of 128),
+    unaligned outputs and negative scale strides, before any launch."""
+    from kb_nano_amd._lib import lib
+    L = lib()
+    p = ctypes.c_void_p(4096)
+
+    def call(M_sum=256, N2=512, K=256, q=p, ldq=256, qs=p, qs_sm=1, qs_sg=256):
+        return L.kbn_fp8_grouped_gemm_silu_quant(p, K, p, 1, M_sum, p, p, p, M_sum, N2, K, 4, 1, q, ldq, qs,
+                                                 qs_sm, qs_sg, 1e-10, 1, None)
+    assert call(N2=384, ldq=192) == 1 and "multiple of 256" in _err()
+    assert call(M_sum=200) == 1 and "128-row alignment" in _err()
+    assert call(q=ctypes.c_void_p(4100)) == 1 and "8-byte aligned" in _err()
+    assert call(ldq=260) == 1 and "8-byte aligned" in _err()
+    assert call(qs_sm=-1) == 1 and "scale strides" in _err()
+    assert call(qs=ctypes.c_void_p(4098)) == 1 and "scale strides" in _err()
+    assert call(K=200) == 1 and "multiple of 128" in _err()
+    assert call(M_sum=0) == 0                                   # nothing to do
+
+
 def test_moe_unpermute_rejects_bad_arguments():
     from kb_nano_amd._lib import lib
     L = lib()
