@@ -479,6 +479,15 @@ def bench_moe(steps, warmup, dev):
     ms_layer = _events_time_ms(lambda i: layer(hidden, w13, w2, topk_w, topk_ids, E, w13_scale=s13, w2_scale=s2,
                                                use_fp8_w8a8=True, block_shape=[128, 128]), steps, warmup, min_warm_ms=WARM_MS)
     res["layer_us"] = ms_layer * 1e3
+    # the same layer with its folded steps switched off: the reference's
+    # step order in separate launches (quant, permute, GEMM1 to bf16,
+    # SiLU*Mul+quant, GEMM2) and the scales-as-given kernels
+    plain = FusedExperts()
+    plain.fuse_quant_permute = plain.fuse_gate_up_silu = plain.ue8m0_when_exact = False
+    ms_plain = _events_time_ms(lambda i: plain(hidden, w13, w2, topk_w, topk_ids, E, w13_scale=s13, w2_scale=s2,
+                                               use_fp8_w8a8=True, block_shape=[128, 128]), steps, warmup,
+                               min_warm_ms=WARM_MS)
+    res["layer_separate_steps_us"] = ms_plain * 1e3
     del w13, s13, w2, s2
     for tag, ms, N, K in (("gate_up", ms1, I2, H), ("down", ms2, H, I)):
         t = ms * 1e-3
