@@ -395,6 +395,57 @@ def test_grouped_gemm_silu_quant_equals_two_launches(gpu_device, E, N2, K, M_tok
     assert err < 0.02 and cos > 0.999, (err, cos)
 
 
+@pytest.mark.parametrize("K", [1024, 2560])
+@pytest.mark.parametrize("ue8m0", [True, False])
+def test_grouped_gemm_segment_end_fragments(gpu_device, K, ue8m0):
+    """Blocks holding 1, 32, 33, 64, 65, 96, 97, 128 and 20 rows of their
+    expert, and one with a hole (rows 64-95 id -1 between live rows): each
+    wavefront of a 128-row tile skips the 32-row fragments past its last live
+    row, so every case of 0, 1 or 2 live fragments per wavefront and both
+    sides of each 32-row boundary occur.  Padding rows hold random codes and
+    scales.  The plain kernel matches the oracle on every live row, the
+    kernel with the SiLU*Mul+quant epilogue equals the two launches bit for
+    bit, and no padding row is written."""
+    from kb_nano_amd import _ops
+    dev = gpu_device
+    print(f"grouped segment ends K={K} ue8m0={ue8m0}", flush=True)
+    E, N2 = 3, 512
+    counts = [1, 32, 33, 64, 65, 96, 97, 128, 20, 128]
+    ids = np.full(128 * len(counts), -1, dtype=np.int32)
+    for b, c in enumerate(counts):
+        ids[128 * b: 128 * b + c] = b % E
+    ids[128 * 9 + 64: 128 * 9 + 96] = -1                     # the hole
+    M_sum = ids.size
+    a = seeded_bf16((M_sum, K), seed=K + 3)
+    qa, sa = oracle.quant_group128(bf16_bits(a))
+    g = torch.Generator().manual_seed(K)
+    qb = np.empty((E, N2, K), dtype=np.uint8)
+    sb = np.empty((E, N2 // 128, K // 128), dtype=np.float32)
+    for e in range(E):
+        qb[e], sb[e] = oracle.quant_block128((torch.randn(N2, K, generator=g) * 0.02).numpy())
+    if not ue8m0:
+        sb = (sb * np.float32(1.37)).astype(np.float32)
+    A, sA = to_fp8(qa, dev), torch.from_numpy(sa).to(dev)
+    B, sB, idt = to_fp8(qb, dev), torch.from_numpy(sb).to(dev), torch.from_numpy(ids).to(dev)
+    valid = ids >= 0
+    vt = torch.from_numpy(valid).to(dev)
+    C = torch.full((M_sum, N2), 7.0, dtype=torch.bfloat16, device=dev)
+    _ops.m_grouped_gemm_nt_contiguous(A, sA, B, sB, C, idt, disable_ue8m0_cast=not ue8m0)
+    N = N2 // 2
+    q1 = torch.full((M_sum, N), 0x5A, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    s1 = torch.empty_strided((M_sum, N // 128), (1, M_sum), device=dev).fill_(-3.0)
+    _ops.silu_mul_quant_fp8(C, q1, s1, True, 1e-10, row_ids=idt)
+    q2 = torch.full_like(q1.view(torch.uint8), 0x5A).view(torch.float8_e4m3fn)
+    s2 = torch.empty_strided((M_sum, N // 128), (1, M_sum), device=dev).fill_(-3.0)
+    _ops.grouped_gemm_silu_quant(A, sA, B, sB, idt, not ue8m0, q2, s2, True, 1e-10)
+    torch.cuda.synchronize()
+    ref = oracle.grouped_gemm_nt_sample(qa, sa, qb, sb, ids, ue8m0=ue8m0)
+    assert_gemm_close(C[vt], ref[valid], f"segment ends K={K} ue8m0={ue8m0}")
+    assert torch.all(C[~vt] == 7.0), "padding rows must stay unwritten"
+    assert torch.equal(q2.view(torch.uint8), q1.view(torch.uint8)) and torch.equal(s2, s1)
+    assert torch.all(q2.view(torch.uint8)[~vt] == 0x5A) and torch.all(s2[~vt] == -3.0)
+
+
 # ------------------------------------------------- FP32 scale contract
 # disable_ue8m0_cast: the scales' exponents go to the MFMA, their
 # significands are carried per row and the running sum is rescaled when they
